@@ -1,0 +1,279 @@
+"""ctypes binding of libcvs_hip (the C ABI declared in include/cvs_hip.h).
+
+Python host code for tests and benchmarks.  It loads the in-tree shared
+library built by ``make -C cuvs-silicon_amd`` and raises if it is missing:
+there is no CPU fallback.
+
+Errors map like the C++ front-end does (reference src/cagra.cpp:26-32,
+:100-111): CVS_ERR_INVALID_ARGUMENT / CVS_ERR_UNSUPPORTED -> ValueError,
+everything else -> RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libcvs_hip.so")
+CXX_LIB_PATH = os.path.join(LIB_DIR, "libcuvs_silicon.so")
+SYNTH_LIB_PATH = os.path.join(LIB_DIR, "libcvs_synth.so")
+
+CVS_OK = 0
+CVS_ERR_INVALID_ARGUMENT = 1
+CVS_ERR_RUNTIME = 2
+CVS_ERR_NO_DEVICE = 3
+CVS_ERR_OUT_OF_MEMORY = 4
+CVS_ERR_UNSUPPORTED = 5
+
+BF_MAX_DIM = 1024
+BF_MAX_K = 48
+
+# Every extern "C" symbol declared in include/cvs_hip.h: name -> (restype, argtypes).
+_SIGNATURES = {
+    "cvs_last_error": (c_char_p, []),
+    "cvs_dispatch_count": (c_uint64, []),
+    "cvs_reset_dispatch_count": (None, []),
+    "cvs_device_count": (c_int, [POINTER(c_int)]),
+    "cvs_context_create": (c_int, [c_int, POINTER(c_void_p)]),
+    "cvs_context_destroy": (c_int, [c_void_p]),
+    "cvs_context_synchronize": (c_int, [c_void_p]),
+    "cvs_context_device_info": (c_int, [c_void_p, c_char_p, c_size_t, POINTER(c_int), POINTER(c_int64)]),
+    "cvs_context_set_timing": (c_int, [c_void_p, c_int]),
+    "cvs_context_kernel_time": (c_int, [c_void_p, c_char_p, POINTER(c_double), POINTER(c_uint64)]),
+    "cvs_device_alloc": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),
+    "cvs_device_free": (c_int, [c_void_p, c_void_p]),
+    "cvs_copy_to_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
+    "cvs_copy_to_host": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
+    "cvs_dataset_create": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, POINTER(c_void_p)]),
+    "cvs_dataset_destroy": (c_int, [c_void_p]),
+    "cvs_dataset_shape": (c_int, [c_void_p, POINTER(c_int64), POINTER(c_int64)]),
+    "cvs_dataset_rows": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "cvs_bf_search": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "cvs_bf_search_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+}
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Loads libcvs_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {PKG_DIR}`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+class CvsError(RuntimeError):
+    pass
+
+
+def _check(status: int) -> None:
+    if status == CVS_OK:
+        return
+    msg = load().cvs_last_error().decode()
+    if status in (CVS_ERR_INVALID_ARGUMENT, CVS_ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise RuntimeError(f"cvs error {status}: {msg}")
+
+
+def device_count() -> int:
+    n = c_int(0)
+    _check(load().cvs_device_count(byref(n)))
+    return n.value
+
+
+def dispatch_count() -> int:
+    return int(load().cvs_dispatch_count())
+
+
+def reset_dispatch_count() -> None:
+    load().cvs_reset_dispatch_count()
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class DeviceArray:
+    """A device allocation with numpy shape/dtype bookkeeping."""
+
+    def __init__(self, ctx: "Context", shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = c_void_p()
+        _check(load().cvs_device_alloc(ctx.handle, max(self.nbytes, 1), byref(p)))
+        self.ptr = p
+
+    @classmethod
+    def from_host(cls, ctx: "Context", host: np.ndarray) -> "DeviceArray":
+        host = np.ascontiguousarray(host)
+        arr = cls(ctx, host.shape, host.dtype)
+        if arr.nbytes:
+            _check(load().cvs_copy_to_device(ctx.handle, arr.ptr, host.ctypes.data_as(c_void_p), arr.nbytes))
+        return arr
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        if self.nbytes:
+            _check(load().cvs_copy_to_host(self.ctx.handle, out.ctypes.data_as(c_void_p), self.ptr, self.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr is not None and self.ctx.handle is not None:
+            _check(load().cvs_device_free(self.ctx.handle, self.ptr))
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """One device + one HIP stream (C: cvs_context)."""
+
+    def __init__(self, device: int = 0):
+        h = c_void_p()
+        _check(load().cvs_context_create(int(device), byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle is not None:
+            _check(load().cvs_context_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self) -> None:
+        _check(load().cvs_context_synchronize(self.handle))
+
+    def device_info(self):
+        name = ctypes.create_string_buffer(256)
+        cu = c_int(0)
+        mem = c_int64(0)
+        _check(load().cvs_context_device_info(self.handle, name, 256, byref(cu), byref(mem)))
+        return {"name": name.value.decode(), "compute_units": cu.value, "total_mem_bytes": mem.value}
+
+    def set_timing(self, enable: bool) -> None:
+        _check(load().cvs_context_set_timing(self.handle, 1 if enable else 0))
+
+    def kernel_time(self, kernel: str):
+        """(total_ms, launches) of `kernel` since the last query."""
+        ms = c_double(0)
+        n = c_uint64(0)
+        _check(load().cvs_context_kernel_time(self.handle, kernel.encode(), byref(ms), byref(n)))
+        return ms.value, int(n.value)
+
+    def dataset(self, rows) -> "Dataset":
+        return Dataset(self, rows)
+
+
+class Dataset:
+    """Device-resident dataset (C: cvs_dataset)."""
+
+    def __init__(self, ctx: Context, rows):
+        self.ctx = ctx
+        h = c_void_p()
+        if isinstance(rows, DeviceArray):
+            n, d = rows.shape
+            _check(load().cvs_dataset_create(ctx.handle, rows.ptr, n, d, 1, byref(h)))
+        else:
+            rows = _f32(rows)
+            if rows.ndim != 2:
+                raise ValueError("dataset must be a 2-D array")
+            n, d = rows.shape
+            _check(load().cvs_dataset_create(ctx.handle, rows.ctypes.data_as(c_void_p), n, d, 0, byref(h)))
+        self.handle = h
+        self.n, self.d = int(n), int(d)
+
+    def close(self) -> None:
+        if self.handle is not None:
+            _check(load().cvs_dataset_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def bf_search(self, queries, k: int):
+        """Exact k-NN of host queries; returns (neighbors u32 [q,k], distances f32 [q,k])."""
+        queries = _f32(queries)
+        if queries.ndim != 2 or queries.shape[1] != self.d:
+            raise ValueError("queries must be (q, d)")
+        q = queries.shape[0]
+        nbr = np.empty((q, k), dtype=np.uint32)
+        dist = np.empty((q, k), dtype=np.float32)
+        _check(load().cvs_bf_search(self.ctx.handle, self.handle, queries.ctypes.data_as(c_void_p), q, int(k),
+                                    nbr.ctypes.data_as(c_void_p), dist.ctypes.data_as(c_void_p)))
+        return nbr, dist
+
+    def bf_search_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray) -> None:
+        _check(load().cvs_bf_search_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0], int(k),
+                                          nbr.ptr, dist.ptr))
+
+
+# ---- synthetic data (lib/libcvs_synth.so) ---------------------------------
+STREAM_BASE = 1
+STREAM_QUERIES = 2
+_synth = None
+
+
+def _synth_lib():
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_LIB_PATH):
+            raise RuntimeError(f"{SYNTH_LIB_PATH} is missing: build it with `make -C {PKG_DIR}`")
+        lib = ctypes.CDLL(SYNTH_LIB_PATH)
+        lib.cvs_synth_clustered.restype = None
+        lib.cvs_synth_clustered.argtypes = [c_uint64, c_uint32, c_int64, c_int64, c_int64, c_int, c_double, c_void_p]
+        lib.cvs_synth_normal.restype = c_double
+        lib.cvs_synth_normal.argtypes = [c_uint64, c_uint32, c_uint64, c_uint64]
+        _synth = lib
+    return _synth
+
+
+def synth_clustered(seed: int, stream: int, n: int, d: int, n_centers: int = 64, sigma: float = 0.3,
+                    row0: int = 0) -> np.ndarray:
+    """Rows [row0, row0+n) of the clustered L2-normalised distribution."""
+    out = np.empty((int(n), int(d)), dtype=np.float32)
+    _synth_lib().cvs_synth_clustered(int(seed), int(stream), int(row0), int(n), int(d), int(n_centers),
+                                     float(sigma), out.ctypes.data_as(c_void_p))
+    return out
+
+
+def synth_normal(seed: int, stream: int, row: int, col: int) -> float:
+    return float(_synth_lib().cvs_synth_normal(int(seed), int(stream), int(row), int(col)))

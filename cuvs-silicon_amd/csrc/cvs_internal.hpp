@@ -1,0 +1,137 @@
+// Internal definitions shared by the HIP translation units of libcvs_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "cvs_hip.h"
+
+namespace cvs {
+
+// Exception carrying a C-ABI status code; converted at the extern "C" edge.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] inline void fail(int code, const std::string& msg) { throw Error(code, msg); }
+
+inline void check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+                       ? CVS_ERR_OUT_OF_MEMORY
+                       : CVS_ERR_RUNTIME;
+  fail(code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define CVS_HIP(call) ::cvs::check_hip((call), #call)
+
+void set_last_error(const std::string& msg);
+void count_dispatch(uint64_t n = 1);
+
+// Runs `fn`, mapping exceptions to status codes + thread-local message.
+template <typename Fn>
+int guarded(Fn&& fn) {
+  try {
+    fn();
+    set_last_error("");
+    return CVS_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return CVS_ERR_OUT_OF_MEMORY;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return CVS_ERR_RUNTIME;
+  }
+}
+
+// A growable device allocation owned by a context (workspaces).
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  void reserve(size_t need);
+  void release();
+  template <typename T>
+  T* as() const { return static_cast<T*>(ptr); }
+};
+
+// Event pairs bracketing the launches of one kernel family.
+struct KernelTimer {
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+  std::vector<hipEvent_t> pool;
+};
+
+}  // namespace cvs
+
+struct cvs_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int compute_units = 0;
+  int64_t total_mem = 0;
+  std::string name;
+  bool timing = false;
+  std::map<std::string, cvs::KernelTimer> timers;
+  // Workspaces reused across calls (never shrink).
+  cvs::DeviceBuffer ws_queries;   // fp16 query tiles + query norms
+  cvs::DeviceBuffer ws_partial;   // per-workgroup candidate lists
+  cvs::DeviceBuffer ws_io;        // staging of host queries / results
+};
+
+struct cvs_dataset {
+  cvs_context* ctx = nullptr;
+  int64_t n = 0;          // rows
+  int64_t d = 0;          // dimensions
+  int64_t dp = 0;         // padded dimensions (32 * power of two)
+  int64_t n_tiles = 0;    // 16-row tiles, padded to a multiple of 32
+  float* rows = nullptr;          // n x d fp32, row-major
+  uint16_t* tiles = nullptr;      // n_tiles x (dp/32) x 64 lanes x 8 fp16
+  float* norms = nullptr;         // n_tiles*16 squared norms of fp16 rows (+inf pad)
+};
+
+namespace cvs {
+
+// Makes the context's device current for the calling thread.
+void bind(cvs_context* ctx);
+
+// Event bracketing for the timing facility.
+hipEvent_t timer_begin(cvs_context* ctx, const char* kernel);
+void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin);
+
+// Launch-site helper: checks the launch, counts the dispatch.
+inline void after_launch(const char* what) {
+  check_hip(hipGetLastError(), what);
+  count_dispatch(1);
+}
+
+// fp16 tile layout (shared by dataset and query tiles): tile t holds rows
+// [16t, 16t+16); k-step s holds columns [32s, 32s+32); lane l of a 64-lane
+// wave holds row 16t + (l % 16), columns 32s + 8*(l/16) + [0, 8).  One k-step
+// of one tile is therefore 1 KiB contiguous, loaded by one wave with one
+// 16-byte access per lane, and is exactly the per-lane operand of
+// v_mfma_f32_16x16x32_f16.
+constexpr int kTileRows = 16;
+constexpr int kStepCols = 32;
+constexpr int kStepBytes = 1024;
+
+inline int64_t padded_dim(int64_t d) {
+  int64_t p = kStepCols;
+  while (p < d) p *= 2;
+  return p;
+}
+
+// Launches the fp32 -> fp16-tile conversion (rows may be n x d with row
+// stride d); writes n_tiles tiles and n_tiles*16 norms.
+void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
+                     int64_t dp, int64_t n_tiles, uint16_t* tiles, float* norms);
+
+}  // namespace cvs

@@ -1,0 +1,342 @@
+// Context, error, memory, timing and dataset-layout parts of the C ABI.
+//
+// Replaces the reference's MetalContext singleton and its buffer caches
+// (src/metal_context.mm:22-117, :155-175): one explicit context per device
+// with a single HIP stream, explicit dataset handles instead of a cache keyed
+// by host pointer, and a device-side fp32 -> fp16 conversion in place of the
+// host loop at src/metal_context.mm:161-167.
+#include <atomic>
+#include <cmath>
+#include <cstring>
+
+#include "cvs_internal.hpp"
+
+namespace cvs {
+
+namespace {
+thread_local std::string g_last_error;
+std::atomic<uint64_t> g_dispatches{0};
+}  // namespace
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+void count_dispatch(uint64_t n) { g_dispatches.fetch_add(n, std::memory_order_relaxed); }
+
+void DeviceBuffer::reserve(size_t need) {
+  if (need <= bytes) return;
+  release();
+  size_t want = need + need / 4;  // headroom for slightly larger calls
+  check_hip(hipMalloc(&ptr, want), "hipMalloc(workspace)");
+  bytes = want;
+}
+
+void DeviceBuffer::release() {
+  if (ptr) (void)hipFree(ptr);
+  ptr = nullptr;
+  bytes = 0;
+}
+
+void bind(cvs_context* ctx) {
+  if (!ctx) fail(CVS_ERR_INVALID_ARGUMENT, "null context");
+  CVS_HIP(hipSetDevice(ctx->device));
+}
+
+hipEvent_t timer_begin(cvs_context* ctx, const char* kernel) {
+  if (!ctx->timing) return nullptr;
+  KernelTimer& t = ctx->timers[kernel];
+  hipEvent_t e;
+  if (!t.pool.empty()) {
+    e = t.pool.back();
+    t.pool.pop_back();
+  } else {
+    CVS_HIP(hipEventCreate(&e));
+  }
+  CVS_HIP(hipEventRecord(e, ctx->stream));
+  return e;
+}
+
+void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin) {
+  if (!ctx->timing || !begin) return;
+  KernelTimer& t = ctx->timers[kernel];
+  hipEvent_t e;
+  if (!t.pool.empty()) {
+    e = t.pool.back();
+    t.pool.pop_back();
+  } else {
+    CVS_HIP(hipEventCreate(&e));
+  }
+  CVS_HIP(hipEventRecord(e, ctx->stream));
+  t.pending.emplace_back(begin, e);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 rows -> fp16 16-row tiles + squared norms of the fp16-rounded rows.
+// One 64-lane wave per tile.  Lane l owns row 16t + l%16 and, for every
+// k-step s, the 8 columns 32s + 8*(l/16) + [0,8); the four lanes sharing a
+// row combine their partial norms with two xor-shuffles.  Rows >= n and
+// columns >= d are written as zeros; padding rows get norm +inf so that no
+// distance involving them can pass a candidate filter.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void to_tiles_kernel(const float* __restrict__ rows,
+                                                      int64_t n, int64_t d, int ksteps,
+                                                      uint4* __restrict__ tiles,
+                                                      float* __restrict__ norms) {
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t r = t * kTileRows + (lane & 15);
+  const int cgrp = lane >> 4;
+  const bool row_ok = r < n;
+  const float* src = rows + (row_ok ? r : 0) * d;
+  float acc = 0.f;
+  for (int s = 0; s < ksteps; ++s) {
+    const int64_t c0 = int64_t(s) * kStepCols + cgrp * 8;
+    _Float16 h[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t c = c0 + i;
+      const float v = (row_ok && c < d) ? src[c] : 0.f;
+      h[i] = static_cast<_Float16>(v);
+      const float hv = static_cast<float>(h[i]);
+      acc += hv * hv;
+    }
+    uint4 packed;
+    __builtin_memcpy(&packed, h, sizeof(packed));
+    tiles[(t * ksteps + s) * 64 + lane] = packed;
+  }
+  acc += __shfl_xor(acc, 16);
+  acc += __shfl_xor(acc, 32);
+  if (cgrp == 0) norms[t * kTileRows + (lane & 15)] = row_ok ? acc : INFINITY;
+}
+
+void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp,
+                     int64_t n_tiles, uint16_t* tiles, float* norms) {
+  if (n_tiles <= 0) return;
+  hipLaunchKernelGGL(to_tiles_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(64), 0,
+                     ctx->stream, rows, n, d, static_cast<int>(dp / kStepCols),
+                     reinterpret_cast<uint4*>(tiles), norms);
+  after_launch("to_tiles_kernel");
+}
+
+}  // namespace cvs
+
+using namespace cvs;
+
+extern "C" {
+
+const char* cvs_last_error(void) { return g_last_error.c_str(); }
+uint64_t cvs_dispatch_count(void) { return g_dispatches.load(); }
+void cvs_reset_dispatch_count(void) { g_dispatches.store(0); }
+
+int cvs_device_count(int* out_count) {
+  return guarded([&] {
+    if (!out_count) fail(CVS_ERR_INVALID_ARGUMENT, "null out_count");
+    int c = 0;
+    if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+    *out_count = c;
+  });
+}
+
+int cvs_context_create(int device, cvs_context** out_ctx) {
+  return guarded([&] {
+    if (!out_ctx) fail(CVS_ERR_INVALID_ARGUMENT, "null out_ctx");
+    *out_ctx = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+      fail(CVS_ERR_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= count)
+      fail(CVS_ERR_INVALID_ARGUMENT, "device index out of range");
+    hipDeviceProp_t prop;
+    CVS_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      fail(CVS_ERR_NO_DEVICE, std::string("kernels are built for gfx950, device is ") +
+                                  prop.gcnArchName);
+    auto* ctx = new cvs_context();
+    ctx->device = device;
+    ctx->compute_units = prop.multiProcessorCount;
+    ctx->total_mem = static_cast<int64_t>(prop.totalGlobalMem);
+    ctx->name = prop.name;
+    try {
+      CVS_HIP(hipSetDevice(device));
+      CVS_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    } catch (...) {
+      delete ctx;
+      throw;
+    }
+    *out_ctx = ctx;
+  });
+}
+
+int cvs_context_destroy(cvs_context* ctx) {
+  return guarded([&] {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->timers) {
+      for (auto& p : kv.second.pending) {
+        (void)hipEventDestroy(p.first);
+        (void)hipEventDestroy(p.second);
+      }
+      for (auto e : kv.second.pool) (void)hipEventDestroy(e);
+    }
+    ctx->ws_queries.release();
+    ctx->ws_partial.release();
+    ctx->ws_io.release();
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+  });
+}
+
+int cvs_context_synchronize(cvs_context* ctx) {
+  return guarded([&] {
+    bind(ctx);
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int cvs_context_device_info(cvs_context* ctx, char* name, size_t name_len, int* compute_units,
+                            int64_t* total_mem_bytes) {
+  return guarded([&] {
+    if (!ctx) fail(CVS_ERR_INVALID_ARGUMENT, "null context");
+    if (name && name_len) {
+      std::strncpy(name, ctx->name.c_str(), name_len - 1);
+      name[name_len - 1] = '\0';
+    }
+    if (compute_units) *compute_units = ctx->compute_units;
+    if (total_mem_bytes) *total_mem_bytes = ctx->total_mem;
+  });
+}
+
+int cvs_context_set_timing(cvs_context* ctx, int enable) {
+  return guarded([&] {
+    if (!ctx) fail(CVS_ERR_INVALID_ARGUMENT, "null context");
+    ctx->timing = enable != 0;
+  });
+}
+
+int cvs_context_kernel_time(cvs_context* ctx, const char* kernel, double* total_ms,
+                            uint64_t* launches) {
+  return guarded([&] {
+    bind(ctx);
+    if (!kernel || !total_ms || !launches) fail(CVS_ERR_INVALID_ARGUMENT, "null argument");
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+    double sum = 0.0;
+    uint64_t cnt = 0;
+    auto it = ctx->timers.find(kernel);
+    if (it != ctx->timers.end()) {
+      for (auto& p : it->second.pending) {
+        float ms = 0.f;
+        CVS_HIP(hipEventElapsedTime(&ms, p.first, p.second));
+        sum += ms;
+        ++cnt;
+        it->second.pool.push_back(p.first);
+        it->second.pool.push_back(p.second);
+      }
+      it->second.pending.clear();
+    }
+    *total_ms = sum;
+    *launches = cnt;
+  });
+}
+
+int cvs_device_alloc(cvs_context* ctx, size_t bytes, void** out_ptr) {
+  return guarded([&] {
+    bind(ctx);
+    if (!out_ptr) fail(CVS_ERR_INVALID_ARGUMENT, "null out_ptr");
+    *out_ptr = nullptr;
+    if (bytes == 0) fail(CVS_ERR_INVALID_ARGUMENT, "zero-byte allocation");
+    CVS_HIP(hipMalloc(out_ptr, bytes));
+  });
+}
+
+int cvs_device_free(cvs_context* ctx, void* ptr) {
+  return guarded([&] {
+    bind(ctx);
+    if (ptr) CVS_HIP(hipFree(ptr));
+  });
+}
+
+int cvs_copy_to_device(cvs_context* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    bind(ctx);
+    if (bytes == 0) return;
+    if (!dst || !src) fail(CVS_ERR_INVALID_ARGUMENT, "null pointer");
+    CVS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int cvs_copy_to_host(cvs_context* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    bind(ctx);
+    if (bytes == 0) return;
+    if (!dst || !src) fail(CVS_ERR_INVALID_ARGUMENT, "null pointer");
+    CVS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int cvs_dataset_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
+                       int rows_on_device, cvs_dataset** out_ds) {
+  return guarded([&] {
+    bind(ctx);
+    if (!out_ds) fail(CVS_ERR_INVALID_ARGUMENT, "null out_ds");
+    *out_ds = nullptr;
+    if (!rows || n <= 0 || d <= 0)
+      fail(CVS_ERR_INVALID_ARGUMENT, "dataset must be non-null and non-empty");
+    if (n > int64_t(UINT32_MAX) - 1)
+      fail(CVS_ERR_UNSUPPORTED, "dataset rows must fit uint32 ids");
+    auto* ds = new cvs_dataset();
+    ds->ctx = ctx;
+    ds->n = n;
+    ds->d = d;
+    ds->dp = padded_dim(d);
+    const int64_t tiles = (n + kTileRows - 1) / kTileRows;
+    ds->n_tiles = (tiles + 31) / 32 * 32;  // whole 32-tile groups: no ragged loads
+    try {
+      const size_t row_bytes = size_t(n) * size_t(d) * sizeof(float);
+      CVS_HIP(hipMalloc(&ds->rows, row_bytes));
+      CVS_HIP(hipMalloc(&ds->tiles, size_t(ds->n_tiles) * size_t(ds->dp / kStepCols) * kStepBytes));
+      CVS_HIP(hipMalloc(&ds->norms, size_t(ds->n_tiles) * kTileRows * sizeof(float)));
+      CVS_HIP(hipMemcpyAsync(ds->rows, rows, row_bytes,
+                             rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                             ctx->stream));
+      launch_to_tiles(ctx, ds->rows, n, d, ds->dp, ds->n_tiles, ds->tiles, ds->norms);
+      CVS_HIP(hipStreamSynchronize(ctx->stream));
+    } catch (...) {
+      if (ds->rows) (void)hipFree(ds->rows);
+      if (ds->tiles) (void)hipFree(ds->tiles);
+      if (ds->norms) (void)hipFree(ds->norms);
+      delete ds;
+      throw;
+    }
+    *out_ds = ds;
+  });
+}
+
+int cvs_dataset_destroy(cvs_dataset* ds) {
+  return guarded([&] {
+    if (!ds) return;
+    bind(ds->ctx);
+    (void)hipStreamSynchronize(ds->ctx->stream);
+    (void)hipFree(ds->rows);
+    (void)hipFree(ds->tiles);
+    (void)hipFree(ds->norms);
+    delete ds;
+  });
+}
+
+int cvs_dataset_shape(const cvs_dataset* ds, int64_t* n, int64_t* d) {
+  return guarded([&] {
+    if (!ds) fail(CVS_ERR_INVALID_ARGUMENT, "null dataset");
+    if (n) *n = ds->n;
+    if (d) *d = ds->d;
+  });
+}
+
+int cvs_dataset_rows(const cvs_dataset* ds, const float** out_rows) {
+  return guarded([&] {
+    if (!ds || !out_rows) fail(CVS_ERR_INVALID_ARGUMENT, "null argument");
+    *out_rows = ds->rows;
+  });
+}
+
+}  // extern "C"

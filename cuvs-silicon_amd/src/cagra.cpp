@@ -1,0 +1,145 @@
+// Front-end of the cuVS-style CAGRA API (reference: src/cagra.cpp:20-266).
+//
+// Validation, exception types, output layout and the graph_degree == 0
+// routing follow the reference; all compute is delegated to libcvs_hip.
+// There is no CPU search path: without a gfx950 device, build()/search()
+// throw std::runtime_error.
+#include <cuvs/neighbors/cagra.hpp>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <limits>
+#include <stdexcept>
+
+#include "backend.hpp"
+
+namespace cuvs_silicon_amd {
+
+namespace {
+std::atomic<std::uint64_t> g_api_dispatches{0};
+}
+
+void add_dispatches(std::uint64_t n) { g_api_dispatches.fetch_add(n); }
+
+Backend::Backend() { check(cvs_context_create(0, &ctx_)); }
+Backend::~Backend() {
+  if (ctx_) cvs_context_destroy(ctx_);
+}
+Backend& Backend::instance() {
+  static Backend b;
+  return b;
+}
+
+std::shared_ptr<DatasetHandle> upload_dataset(const float* rows, std::int64_t n, std::int64_t d) {
+  cvs_dataset* ds = nullptr;
+  counted([&] { return cvs_dataset_create(Backend::instance().ctx(), rows, n, d, 0, &ds); });
+  return std::make_shared<DatasetHandle>(ds);
+}
+
+}  // namespace cuvs_silicon_amd
+
+namespace cuvs::neighbors::cagra {
+
+namespace detail {
+struct device_state {
+  std::shared_ptr<cuvs_silicon_amd::DatasetHandle> dataset;
+};
+std::shared_ptr<device_state> make_device_state() { return std::make_shared<device_state>(); }
+}  // namespace detail
+
+using cuvs_silicon_amd::Backend;
+using cuvs_silicon_amd::check;
+using cuvs_silicon_amd::counted;
+
+template <>
+index<float, std::uint32_t> build<float, std::int64_t>(
+    const raft::resources& resources, const index_params& params,
+    raft::device_matrix_view<const float, std::int64_t> dataset) {
+  (void)resources;
+  if (params.metric != cuvs::distance::DistanceType::L2Expanded)
+    throw std::invalid_argument("CAGRA build supports the L2Expanded metric only");
+  if (dataset.data_handle() == nullptr || dataset.extent(0) <= 0 || dataset.extent(1) <= 0)
+    throw std::invalid_argument("CAGRA build requires a non-empty dataset");
+
+  const std::int64_t n = dataset.extent(0);
+  const std::int64_t d = dataset.extent(1);
+  const float* data = dataset.data_handle();
+
+  std::vector<float> storage;
+  if (params.attach_dataset_on_build) storage.assign(data, data + n * d);
+  index<float, std::uint32_t> idx{std::move(storage), n, d};
+
+  const std::uint32_t degree =
+      std::min<std::uint32_t>(params.graph_degree, static_cast<std::uint32_t>(n - 1));
+  if (n > 1 && degree > 0) {
+    throw std::runtime_error("CAGRA graph build is not available in this build");
+  }
+  return idx;
+}
+
+namespace {
+
+void validate_search(const index<float, std::uint32_t>& index,
+                     raft::device_matrix_view<const float, std::int64_t> queries,
+                     raft::device_matrix_view<std::uint32_t, std::int64_t> neighbors,
+                     raft::device_matrix_view<float, std::int64_t> distances) {
+  if (queries.data_handle() == nullptr || neighbors.data_handle() == nullptr ||
+      distances.data_handle() == nullptr)
+    throw std::invalid_argument("CAGRA search requires valid buffers");
+  if (queries.extent(1) != index.cols())
+    throw std::invalid_argument("CAGRA search query dimension mismatch");
+  if (neighbors.extent(0) != queries.extent(0) || distances.extent(0) != queries.extent(0) ||
+      neighbors.extent(1) != distances.extent(1))
+    throw std::invalid_argument("CAGRA search output shape mismatch");
+}
+
+// Device copy of the index's dataset, uploaded on first use.
+detail::device_state& device_state_of(const index<float, std::uint32_t>& index) {
+  auto& cache = index.device_cache();
+  if (!cache) cache = detail::make_device_state();
+  if (!cache->dataset) {
+    if (index.dataset().empty())
+      throw std::invalid_argument("CAGRA search requires an index with an attached dataset");
+    cache->dataset =
+        cuvs_silicon_amd::upload_dataset(index.dataset().data(), index.rows(), index.cols());
+  }
+  return *cache;
+}
+
+}  // namespace
+
+template <>
+void search<float, std::uint32_t, std::int64_t>(
+    const raft::resources& resources, const search_params& params,
+    const index<float, std::uint32_t>& index,
+    raft::device_matrix_view<const float, std::int64_t> queries,
+    raft::device_matrix_view<std::uint32_t, std::int64_t> neighbors,
+    raft::device_matrix_view<float, std::int64_t> distances) {
+  (void)resources;
+  (void)params;
+  validate_search(index, queries, neighbors, distances);
+  const std::int64_t q = queries.extent(0);
+  const std::int64_t k = neighbors.extent(1);
+  if (q == 0) return;
+  if (k <= 0) throw std::invalid_argument("CAGRA search requires k > 0");
+
+  detail::device_state& dev = device_state_of(index);
+  cvs_context* ctx = Backend::instance().ctx();
+  const bool has_graph = index.graph_degree() > 0 && !index.knn_graph().empty();
+  if (has_graph) throw std::runtime_error("CAGRA graph search is not available in this build");
+  counted([&] {
+    return cvs_bf_search(ctx, dev.dataset->ds, queries.data_handle(), q, k,
+                         neighbors.data_handle(), distances.data_handle());
+  });
+}
+
+std::uint64_t metal_dispatch_count() noexcept {
+  return cuvs_silicon_amd::g_api_dispatches.load();
+}
+void reset_metal_dispatch_count() noexcept { cuvs_silicon_amd::g_api_dispatches.store(0); }
+void increment_metal_dispatch_count() noexcept { cuvs_silicon_amd::add_dispatches(1); }
+std::uint64_t gpu_dispatch_count() noexcept { return metal_dispatch_count(); }
+void reset_gpu_dispatch_count() noexcept { reset_metal_dispatch_count(); }
+
+}  // namespace cuvs::neighbors::cagra

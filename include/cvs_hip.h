@@ -1,0 +1,131 @@
+/*
+ * cvs_hip.h - C ABI of the MI355X (gfx950) search backend.
+ *
+ * This is the device boundary of the library.  It replaces the reference's
+ * Objective-C++ backend class `cuvs_silicon::MetalContext`
+ * (include/cuvs_silicon/metal_context.hpp:12-81, src/metal_context.mm) with
+ * plain `extern "C"` functions over pointers and sizes, so that any host
+ * language (C++, Python ctypes, cgo, JNI) can bind it.
+ *
+ * Conventions
+ *  - Every function returns CVS_OK (0) or a CVS_ERR_* code; the message of the
+ *    last failure on the calling thread is returned by cvs_last_error().
+ *  - Matrices are row-major.  Dataset/query rows are fp32.  Neighbour ids are
+ *    uint32 row indices into the dataset; distances are *squared* L2.
+ *  - Result rows are sorted by (distance, id) ascending; slots beyond the
+ *    number of available results hold UINT32_MAX / +inf
+ *    (src/cagra.cpp:240-251 in the reference).
+ *  - Functions without the `_async` suffix take HOST pointers and block until
+ *    results are in the caller's host buffers (reference semantics:
+ *    src/metal_context.mm:224-225, :242-243, :1099-1100).  `_async` variants
+ *    take DEVICE pointers, are enqueued on the context's stream and return
+ *    immediately; call cvs_context_synchronize() before reading results.
+ *  - A context is not thread-safe: use one context per host thread.
+ *  - There is no CPU fallback: without a usable gfx950 device every compute
+ *    entry point fails with CVS_ERR_NO_DEVICE.
+ */
+#ifndef CVS_HIP_H
+#define CVS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum cvs_status {
+  CVS_OK = 0,
+  CVS_ERR_INVALID_ARGUMENT = 1, /* bad shape / null pointer -> std::invalid_argument */
+  CVS_ERR_RUNTIME = 2,          /* HIP runtime failure       -> std::runtime_error */
+  CVS_ERR_NO_DEVICE = 3,        /* no usable GPU             -> std::runtime_error */
+  CVS_ERR_OUT_OF_MEMORY = 4,    /* device allocation failed  -> std::runtime_error */
+  CVS_ERR_UNSUPPORTED = 5       /* shape outside kernel limits -> std::invalid_argument */
+};
+
+typedef struct cvs_context cvs_context; /* one device + one HIP stream */
+typedef struct cvs_dataset cvs_dataset; /* device-resident dataset (fp32 rows, fp16 tiles, norms) */
+
+/* Limits of the fused brute-force kernel (checked by cvs_bf_search*). */
+#define CVS_BF_MAX_DIM 1024
+#define CVS_BF_MAX_K 48
+
+/* ---- errors, counters ---------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* cvs_last_error(void);
+
+/* Number of kernel launches made by this process since the last reset.
+ * Backs the reference's dispatch instrumentation
+ * (include/cuvs/neighbors/cagra.hpp:119-122, src/cagra.cpp:255-266). */
+uint64_t cvs_dispatch_count(void);
+void cvs_reset_dispatch_count(void);
+
+/* ---- context ------------------------------------------------------------- */
+
+/* Number of visible HIP devices (0 when none; never fails). */
+int cvs_device_count(int* out_count);
+
+/* Create a context on `device` (replaces MetalContext::instance(),
+ * metal_context.hpp:15, and is_available(), metal_context.hpp:19). */
+int cvs_context_create(int device, cvs_context** out_ctx);
+int cvs_context_destroy(cvs_context* ctx);
+int cvs_context_synchronize(cvs_context* ctx);
+
+/* Device name and compute-unit count, for run metadata
+ * (replaces MetalContext::chip_model(), metal_context.hpp:23). */
+int cvs_context_device_info(cvs_context* ctx, char* name, size_t name_len,
+                            int* compute_units, int64_t* total_mem_bytes);
+
+/* Kernel timing: while enabled, the launches of each kernel family are
+ * bracketed by HIP events on the context stream.  cvs_context_kernel_time()
+ * synchronizes and returns the summed elapsed milliseconds and launch count
+ * for `kernel` ("bf_scan", "bf_merge", "bf_prep", ...), then clears them. */
+int cvs_context_set_timing(cvs_context* ctx, int enable);
+int cvs_context_kernel_time(cvs_context* ctx, const char* kernel,
+                            double* total_ms, uint64_t* launches);
+
+/* ---- device memory helpers (device-resident benchmarking and tests) ----- */
+
+int cvs_device_alloc(cvs_context* ctx, size_t bytes, void** out_ptr);
+int cvs_device_free(cvs_context* ctx, void* ptr);
+int cvs_copy_to_device(cvs_context* ctx, void* dst, const void* src, size_t bytes);
+int cvs_copy_to_host(cvs_context* ctx, void* dst, const void* src, size_t bytes);
+
+/* ---- dataset ------------------------------------------------------------- */
+
+/* Upload an n x d fp32 row-major dataset and build its search layouts: the
+ * fp32 rows (exact re-rank, graph search), fp16 16-row MFMA tiles and fp32
+ * squared norms of the fp16-rounded rows.  Replaces the reference's
+ * per-pointer dataset cache and host fp16 conversion
+ * (src/metal_context.mm:155-175, compute_row_norms :127-137).
+ * `rows_on_device` = 0: `rows` is a host pointer; 1: a device pointer. */
+int cvs_dataset_create(cvs_context* ctx, const float* rows, int64_t n,
+                       int64_t d, int rows_on_device, cvs_dataset** out_ds);
+int cvs_dataset_destroy(cvs_dataset* ds);
+int cvs_dataset_shape(const cvs_dataset* ds, int64_t* n, int64_t* d);
+/* Device pointer of the fp32 rows (n x d, row-major). */
+int cvs_dataset_rows(const cvs_dataset* ds, const float** out_rows);
+
+/* ---- exact brute-force k-NN --------------------------------------------- */
+
+/* Exact squared-L2 k-NN of q queries against the dataset.  Replaces
+ * MetalContext::search_brute_force (metal_context.hpp:35-40;
+ * src/metal_context.mm:139-255: MPS fp16 GEMM + l2_topk_from_cross).
+ * Fused: fp16 MFMA cross terms over LDS-staged tiles with a per-query
+ * candidate filter, then an exact fp32 re-rank.  Requires 1 <= k,
+ * k <= CVS_BF_MAX_K, d <= CVS_BF_MAX_DIM.  Host pointers, blocking. */
+int cvs_bf_search(cvs_context* ctx, const cvs_dataset* ds,
+                  const float* queries, int64_t q, int64_t k,
+                  uint32_t* out_neighbors, float* out_distances);
+
+/* Same, with device pointers; enqueued on the context stream. */
+int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds,
+                        const float* queries_dev, int64_t q, int64_t k,
+                        uint32_t* out_neighbors_dev, float* out_distances_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CVS_HIP_H */
