@@ -6,30 +6,37 @@
 // `l2_topk_from_cross` (shaders/cagra_kernels.metal:604-653), which re-reads
 // it and keeps a per-thread K-slot list merged serially by thread 0.
 //
-// Here the cross matrix never leaves registers:
+// Here the cross matrix never leaves registers.  Five launches per batch:
 //
-//  bf_scan   one persistent workgroup per compute unit streams a contiguous
-//            range of 16-row fp16 tiles HBM -> VGPRs -> LDS (double-buffered
-//            LDS, two stages of loads in flight).  Each of the 4 waves keeps
-//            the fp16 MFMA operands of its 32 queries for the full dimension
-//            resident in VGPRs and computes query.row cross terms with
-//            v_mfma_f32_16x16x32_f16 (fp32 accumulate).  The epilogue forms
-//            d = |q|^2 + |x|^2 - 2 q.x and appends (d, row) to the query's LDS
-//            candidate list only if d is below the query's running threshold.
-//            When a list nears capacity the owning wave compacts it to the
-//            kp smallest keys with a radix select and lowers the threshold.
-//            Each workgroup finally writes its kp best keys per query.
-//  bf_merge  one workgroup per query selects the kp smallest of all partial
-//            lists, re-ranks them with exact fp32 distances from the fp32
-//            rows, sorts by (distance, id) and writes k results, padding with
-//            UINT32_MAX / +inf (src/cagra.cpp:240-251).
+//  prep     queries fp32 -> fp16 32-row tiles + norms (the dataset layout).
+//  sample   the scan kernel over a strided sample of ~256*kp rows, writing
+//           every approximate query/row distance of the sample.
+//  select   per query, the kp-th smallest sampled distance T0.  At least kp
+//           dataset rows lie at or below T0, so T0 bounds the global kp-th
+//           distance and every row above it can be dropped by the scan.
+//  scan     one persistent workgroup per compute unit streams a contiguous
+//           range of fp16 tiles HBM -> VGPRs -> LDS (double-buffered LDS, two
+//           stages of loads in flight).  Each wave keeps the fp16 operands of
+//           its 32 queries for the full dimension resident in AGPRs; the
+//           dataset tile is the A operand of v_mfma_f32_32x32x16_f16 (fp32
+//           accumulate, two accumulation chains), so each lane owns one query
+//           and 16 rows of the 32x32 result.  The epilogue forms
+//           d = |q|^2 + |x|^2 - 2 q.x and appends (d, row) to the query's LDS
+//           list only if d is below the query's threshold (T0 at start).  A
+//           list that nears capacity is compacted by its wave to the kp
+//           smallest keys (ballot radix select), lowering the threshold.
+//  merge    one workgroup per query selects the kp smallest keys of all
+//           per-workgroup lists, re-ranks them with exact fp32 distances from
+//           the fp32 rows, sorts by (distance, id) and writes k results,
+//           padding with UINT32_MAX / +inf (src/cagra.cpp:240-251).
 //
 // The fp16 pass only *selects*; reported distances come from the fp32
 // re-rank, so distances agree with the reference's fp32 loop
 // (src/cagra.cpp:218-226) up to summation order.  kp > k candidates are kept
 // because fp16 inputs perturb |q-x|^2 by up to ~1e-4 absolute at unit norm,
-// which is far below the gap between rank k and rank kp.
+// far below the gap between rank k and rank kp on the target data.
 #include <cmath>
+#include <type_traits>
 
 #include "cvs_internal.hpp"
 
@@ -38,16 +45,21 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define CVS_INLINE __attribute__((always_inline))
 
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kWaves = 4;
-constexpr int kStageBytes = 32768;
-constexpr int kStageVecs = kStageBytes / 16;           // 16-byte vectors per stage
+constexpr int kQB = 128;                                // queries per workgroup (32 per wave)
+constexpr int kStageBlocks = 32;                        // 1 KiB blocks per stage
+constexpr int kStageVecs = kStageBlocks * 64;           // 16-byte vectors per stage
 constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 8
+constexpr int kCap = 80;                                // LDS list slots per query
 constexpr uint64_t kSentinel = ~0ull;
 
-#define CVS_INLINE __attribute__((always_inline))
+enum { kModeScan = 0, kModeSample = 1 };
 
 // Order-preserving map float -> uint32 (total order for non-NaN values).
 __device__ __forceinline__ uint32_t ord_f32(float f) {
@@ -58,182 +70,154 @@ __device__ __forceinline__ float unord_f32(uint32_t o) {
   return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
-template <int KS, int QS>
-struct Scan {
-  static constexpr int TPS = KS >= 32 ? 1 : 32 / KS;  // 16-row tiles per stage
-  static constexpr int QPW = 16 * QS;                  // queries per wave
-  static constexpr int QB = kWaves * QPW;              // queries per workgroup
-  static constexpr int CAP = QS == 2 ? 88 : 176;       // LDS candidate slots per query
-  static constexpr int EPL = CAP / 4;                  // slots per lane in compaction
-  static_assert(KS * TPS * 1024 == kStageBytes || KS > 32, "stage must be 32 KiB");
+__device__ __forceinline__ int popc(uint64_t m) { return __builtin_popcountll(m); }
+
+// Index of this lane among the set lanes of `mask` below it.
+__device__ __forceinline__ int mbcnt(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0));
+}
+
+template <int KS>
+struct Cfg {
+  static constexpr int TPS = KS >= 32 ? 1 : 32 / KS;      // tiles per stage
+  static constexpr int SPT = KS >= 32 ? KS / 32 : 1;      // stages per tile
+  static constexpr int RPU = 2 * kStageBlocks * 32 / KS;  // rows per 2-stage unit
+  static_assert(KS >= 2 && KS <= 64, "k-steps per tile");
 };
 
 struct ScanArgs {
-  const u32x4* tiles;   // dataset tiles (stage-padded)
-  const f32x4* norms;   // dataset norms, 16 per tile
-  int64_t n_stages;
+  const u32x4* tiles;   // dataset tiles (unit-padded)
+  const f32x4* norms;   // dataset norms, 32 per tile
+  int64_t n_units;      // 2-stage units in the dataset
   const u32x4* qtiles;  // query tiles
-  const float* qnorms;  // query norms, 16 per query tile
+  const float* qnorms;  // query norms, 32 per query tile
   int nq;
-  int n_qslices;        // number of 16-query tiles
+  int n_qtiles;         // number of 32-query tiles
   int kp;               // candidates kept per (workgroup, query)
-  uint64_t* part;       // [nq][gridDim.x][kp]
+  const float* thr0;    // per-query initial threshold (scan mode)
+  uint64_t* part;       // scan: [nq][gridDim.x][kp] keys
+  float* sdist;         // sample: [nq][s_rows] approximate distances
+  int64_t s_units;      // sample: number of sampled units
+  int64_t s_stride;     // sample: unit stride
+  int64_t s_rows;       // sample: rows per query = s_units * RPU
 };
 
-// Selects the kp-th smallest 64-bit key of one query's list, held by 4
-// consecutive lanes (entries g, g+4, g+8, ... of `cnt`), and compacts the
-// list in place to exactly min(cnt, kp) keys.  Returns the new threshold
-// (distance of the kp-th key) through *thr_out on lane g == 0.
-template <int EPL>
-__device__ __forceinline__ void compact_list(uint64_t* list, uint32_t* cnt_slot, float* thr_slot,
-                                             int g, int kp, bool active) {
-  const uint32_t cnt = active ? *cnt_slot : 0u;
-  const bool work = active && cnt > uint32_t(kp);
-  const int nv = (work && cnt > uint32_t(g)) ? int((cnt - g + 3) / 4) : 0;
-  uint32_t hi[EPL], lo[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    if (i < nv) {
-      const uint64_t key = list[g + 4 * i];
-      hi[i] = uint32_t(key >> 32);
-      lo[i] = uint32_t(key);
-    } else {
-      hi[i] = 0xffffffffu;
-      lo[i] = 0xffffffffu;
-    }
-  }
-  // Radix select on the distance word.
+// Compacts the LDS list of one query to its kp smallest keys and lowers the
+// query's threshold to the kp-th distance.  All 64 lanes take part (the list
+// pointer is wave-uniform); entry e lives in lane e % 64 (CAP <= 128).
+__device__ __forceinline__ void compact_query(uint64_t* list, uint32_t* cnt_slot, float* thr_slot,
+                                              int kp) {
+  const int lane = __lane_id();
+  const uint32_t cnt = *cnt_slot;
+  if (cnt <= uint32_t(kp)) return;
+  const bool v0 = uint32_t(lane) < cnt, v1 = uint32_t(lane + 64) < cnt;
+  const uint64_t k0 = v0 ? list[lane] : kSentinel;
+  const uint64_t k1 = v1 ? list[lane + 64] : kSentinel;
+  const uint32_t h0 = uint32_t(k0 >> 32), h1 = uint32_t(k1 >> 32);
+  const uint32_t l0 = uint32_t(k0), l1 = uint32_t(k1);
   int need = kp;
   uint32_t pre = 0;
   for (int b = 31; b >= 0; --b) {
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) c += (i < nv && ((hi[i] ^ pre) >> b) == 0) ? 1 : 0;
-    c += __shfl_xor(c, 1);
-    c += __shfl_xor(c, 2);
+    const int c = popc(__ballot(v0 && ((h0 ^ pre) >> b) == 0)) +
+                  popc(__ballot(v1 && ((h1 ^ pre) >> b) == 0));
     if (c < need) {
       need -= c;
       pre |= 1u << b;
     }
   }
   const uint32_t kth_hi = pre;
-  int lt = 0, eq = 0;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    lt += (i < nv && hi[i] < kth_hi) ? 1 : 0;
-    eq += (i < nv && hi[i] == kth_hi) ? 1 : 0;
-  }
-  lt += __shfl_xor(lt, 1);
-  lt += __shfl_xor(lt, 2);
-  eq += __shfl_xor(eq, 1);
-  eq += __shfl_xor(eq, 2);
-  const int need_eq = kp - lt;
+  const int lt = popc(__ballot(v0 && h0 < kth_hi)) + popc(__ballot(v1 && h1 < kth_hi));
+  const int eq = popc(__ballot(v0 && h0 == kth_hi)) + popc(__ballot(v1 && h1 == kth_hi));
   uint32_t kth_lo = 0xffffffffu;
-  if (__ballot(work && eq > need_eq) != 0) {
-    // Ties on the distance word: select on the row id among them.
-    int need2 = need_eq;
+  if (eq > kp - lt) {  // ties on the distance word: select on the row id
+    int need2 = kp - lt;
     uint32_t pre2 = 0;
     for (int b = 31; b >= 0; --b) {
-      int c = 0;
-#pragma unroll
-      for (int i = 0; i < EPL; ++i)
-        c += (i < nv && hi[i] == kth_hi && ((lo[i] ^ pre2) >> b) == 0) ? 1 : 0;
-      c += __shfl_xor(c, 1);
-      c += __shfl_xor(c, 2);
+      const int c = popc(__ballot(v0 && h0 == kth_hi && ((l0 ^ pre2) >> b) == 0)) +
+                    popc(__ballot(v1 && h1 == kth_hi && ((l1 ^ pre2) >> b) == 0));
       if (c < need2) {
         need2 -= c;
         pre2 |= 1u << b;
       }
     }
-    if (eq > need_eq) kth_lo = pre2;
+    kth_lo = pre2;
   }
-  // In-place compaction (all entries are already in registers).
-  int kc = 0;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i)
-    kc += (i < nv && (hi[i] < kth_hi || (hi[i] == kth_hi && lo[i] <= kth_lo))) ? 1 : 0;
-  const int lane = __lane_id();
-  const int base = lane & ~3;
-  const int k0 = __shfl(kc, base + 0), k1 = __shfl(kc, base + 1), k2 = __shfl(kc, base + 2);
-  int pos = (g > 0 ? k0 : 0) + (g > 1 ? k1 : 0) + (g > 2 ? k2 : 0);
-  if (work) {
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      if (i < nv && (hi[i] < kth_hi || (hi[i] == kth_hi && lo[i] <= kth_lo))) {
-        list[pos++] = (uint64_t(hi[i]) << 32) | lo[i];
-      }
-    }
-    if (g == 0) {
-      *cnt_slot = uint32_t(kp);
-      *thr_slot = unord_f32(kth_hi);
-    }
+  const bool keep0 = v0 && (h0 < kth_hi || (h0 == kth_hi && l0 <= kth_lo));
+  const bool keep1 = v1 && (h1 < kth_hi || (h1 == kth_hi && l1 <= kth_lo));
+  const uint64_t m0 = __ballot(keep0), m1 = __ballot(keep1);
+  if (keep0) list[mbcnt(m0)] = k0;
+  if (keep1) list[popc(m0) + mbcnt(m1)] = k1;
+  if (lane == 0) {
+    *cnt_slot = uint32_t(kp);
+    *thr_slot = unord_f32(kth_hi);
   }
 }
 
-template <int KS, int QS>
+template <int KS, int MODE>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void bf_scan_kernel(ScanArgs a) {
-  using C = Scan<KS, QS>;
-  constexpr int TPS = C::TPS, QPW = C::QPW, QB = C::QB, CAP = C::CAP;
+  using C = Cfg<KS>;
+  constexpr int TPS = C::TPS, SPT = C::SPT, RPU = C::RPU;
 
   __shared__ u32x4 s_stage[2][kStageVecs];
-  __shared__ float s_dn[2][TPS * 16];
-  __shared__ uint32_t s_cnt[QB];
-  __shared__ float s_thr[QB];
-  __shared__ uint64_t s_buf[QB * CAP];
+  __shared__ float s_dn[2][TPS * 32];
+  __shared__ uint32_t s_cnt[kQB];
+  __shared__ float s_thr[kQB];
+  __shared__ uint64_t s_buf[MODE == kModeScan ? kQB * kCap : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int G = gridDim.x;
   const int x = blockIdx.x;
-  const int qbase = blockIdx.y * QB;  // first query of this workgroup
+  const int qbase = blockIdx.y * kQB;
   const int kp = a.kp;
 
-  // Stage range of this workgroup.
-  const int64_t st0 = (a.n_stages * x) / G;
-  const int64_t st1 = (a.n_stages * (x + 1)) / G;
+  // Units of this workgroup: contiguous (scan) or a strided sample (sample).
+  const int64_t total = MODE == kModeScan ? a.n_units : a.s_units;
+  const int64_t i0 = (total * x) / G;
+  const int64_t i1 = (total * (x + 1)) / G;
+  const int n_stages = int(2 * (i1 - i0));
+  auto unit_of = [&](int64_t i) CVS_INLINE -> int64_t {
+    return MODE == kModeScan ? i : i * a.s_stride;
+  };
+  auto stage_of = [&](int j) CVS_INLINE -> int64_t { return 2 * unit_of(i0 + (j >> 1)) + (j & 1); };
 
-  // ---- per-query LDS state ----
-  for (int i = tid; i < QB; i += kThreads) {
-    s_cnt[i] = 0;
-    s_thr[i] = (qbase + i < a.nq) ? INFINITY : -INFINITY;
+  // ---- resident query operands: wave owns queries [qbase + 32*wave, +32) ----
+  const int qt = (qbase >> 5) + wave;
+  const int my_q = qbase + wave * 32 + (lane & 31);
+  const bool q_ok = my_q < a.nq;
+  half8 qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    u32x4 v = qt < a.n_qtiles ? a.qtiles[(int64_t(qt) * KS + s) * 64 + lane] : u32x4{0, 0, 0, 0};
+    half8 h = __builtin_bit_cast(half8, v);
+    // Pin the resident operand to an AGPR (MFMA reads B from AGPRs), leaving
+    // the arch VGPRs for stage loads, the A-fragment ring and accumulators.
+    asm volatile("" : "+a"(h));
+    qb[s] = h;
   }
-
-  // ---- resident query operands: wave owns queries [qbase + wave*QPW, +QPW) ----
-  half8 qa[QS][KS];
-  float qn[QS][4];
-  float thr[QS][4];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    const int sl = (qbase >> 4) + wave * QS + qs;
-    const bool ok = sl < a.n_qslices;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 v = ok ? a.qtiles[(int64_t(sl) * KS + s) * 64 + lane] : u32x4{0, 0, 0, 0};
-      half8 h = __builtin_bit_cast(half8, v);
-      // Pin the resident operand to an AGPR: MFMA reads A from AGPRs, and the
-      // 256 arch VGPRs stay free for stage loads and B-fragment prefetch.
-      asm volatile("" : "+a"(h));
-      qa[qs][s] = h;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = qbase + wave * QPW + qs * 16 + 4 * (lane >> 4) + j;
-      qn[qs][j] = (ok && q < a.nq) ? a.qnorms[int64_t(sl) * 16 + 4 * (lane >> 4) + j] : INFINITY;
-      thr[qs][j] = q < a.nq ? INFINITY : -INFINITY;
+  const float qn = q_ok ? a.qnorms[my_q] : INFINITY;
+  const int qw = wave * 32 + (lane & 31);  // this lane's query slot in the workgroup
+  float thr = -INFINITY;
+  if (MODE == kModeScan) {
+    if (q_ok) thr = nextafterf(a.thr0[my_q], INFINITY);
+    for (int i = tid; i < kQB; i += kThreads) {
+      s_cnt[i] = 0;
+      s_thr[i] = INFINITY;
     }
   }
 
   // ---- stage loads: HBM -> registers -> LDS ----
   u32x4 ra[kLoadsPerThread], rb[kLoadsPerThread];
   f32x4 na = {0, 0, 0, 0}, nb = {0, 0, 0, 0};
-  const bool norm_loader = tid < TPS * 4;
+  const bool norm_loader = tid < TPS * 8;
   auto gload = [&](u32x4 (&r)[kLoadsPerThread], f32x4& nr, int64_t st) CVS_INLINE {
     const u32x4* src = a.tiles + st * kStageVecs + tid;
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) r[i] = __builtin_nontemporal_load(src + i * kThreads);
-    if (norm_loader) nr = a.norms[st * TPS * 4 + tid];
+    const int64_t tile0 = KS >= 32 ? st / SPT : st * TPS;
+    if (norm_loader) nr = a.norms[tile0 * 8 + tid];
   };
   auto lstore = [&](int buf, const u32x4 (&r)[kLoadsPerThread], const f32x4& nr) CVS_INLINE {
 #pragma unroll
@@ -241,130 +225,189 @@ void bf_scan_kernel(ScanArgs a) {
     if (norm_loader) *reinterpret_cast<f32x4*>(&s_dn[buf][tid * 4]) = nr;
   };
 
-  auto refresh_thr = [&]() CVS_INLINE {
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        thr[qs][j] = s_thr[wave * QPW + qs * 16 + 4 * (lane >> 4) + j];
-  };
-
-  // Compacts the lists of this wave's queries whose count exceeds `limit`.
+  // Compacts every list of this wave whose count exceeds `limit`, then
+  // tightens this lane's threshold.
   auto compact_wave = [&](uint32_t limit) CVS_INLINE {
-#pragma unroll
-    for (int r = 0; r < QS; ++r) {
-      const int qw = r * 16 + (lane >> 2);
-      const int m = wave * QPW + qw;
-      const bool active = qbase + m < a.nq && s_cnt[m] > limit;
-      compact_list<C::EPL>(s_buf + m * CAP, &s_cnt[m], &s_thr[m], lane & 3, kp, active);
+    uint64_t over = __ballot(lane < 32 && s_cnt[wave * 32 + lane] > limit);
+    if (over == 0) return;
+    while (over) {
+      const int i = __builtin_ctzll(over);
+      over &= over - 1;
+      const int m = wave * 32 + i;
+      compact_query(s_buf + m * kCap, &s_cnt[m], &s_thr[m], kp);
     }
-    refresh_thr();
+    thr = fminf(thr, s_thr[qw]);
   };
 
-  auto compute = [&](int buf, int64_t st) CVS_INLINE {
-    const u32x4* sb = s_stage[buf];
-#pragma unroll 1
-    for (int rt = 0; rt < TPS; ++rt) {
-      f32x4 acc[QS];
+  f32x16 acc0, acc1;
 #pragma unroll
-      for (int qs = 0; qs < QS; ++qs) acc[qs] = f32x4{0, 0, 0, 0};
-      const u32x4* tb = sb + rt * KS * 64 + lane;
-      // B fragments (16 rows x 32 columns per k-step) through a PF-deep
-      // register ring so LDS latency overlaps the MFMAs.
-      constexpr int PF = KS < 4 ? KS : 4;
-      half8 bring[PF];
+  for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.f;
+
+  // Epilogue for one finished 32-row tile: this lane holds query `my_q`
+  // against rows row0 + 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
+  auto epilogue = [&](int buf, int tis, int64_t row0, int j) CVS_INLINE {
+    f32x4 dn4[4];
 #pragma unroll
-      for (int j = 0; j < PF; ++j) bring[j] = __builtin_bit_cast(half8, tb[j * 64]);
+    for (int g = 0; g < 4; ++g)
+      dn4[g] = *reinterpret_cast<const f32x4*>(&s_dn[buf][tis * 32 + 8 * g + 4 * (lane >> 5)]);
+    if (MODE == kModeSample) {
+      if (q_ok) {
+        const int64_t i = i0 + (j >> 1);
+        const int64_t srow0 = i * RPU + (row0 - unit_of(i) * RPU);
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const half8 b = bring[s % PF];
-        if (s + PF < KS) bring[s % PF] = __builtin_bit_cast(half8, tb[(s + PF) * 64]);
+        for (int g = 0; g < 4; ++g) {
+          f32x4 d;
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs)
-          acc[qs] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[qs][s], b, acc[qs], 0, 0, 0);
-      }
-      // Schedule: PF reads up front, then (QS MFMAs, 1 read) pairs, then drain.
-#pragma unroll
-      for (int j = 0; j < PF; ++j) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-      for (int j = 0; j < KS - PF; ++j) {
-        __builtin_amdgcn_sched_group_barrier(0x008, QS, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, QS * PF, 0);
-      // Epilogue: lane holds rows 4*(lane/16)+j of each query slice, row lane%16.
-      const float dn = s_dn[buf][rt * 16 + (lane & 15)];
-      const uint32_t row = uint32_t((st * TPS + rt) * 16 + (lane & 15));
-#pragma unroll
-      for (int qs = 0; qs < QS; ++qs) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float d = qn[qs][j] + dn - 2.0f * acc[qs][j];
-          if (d < thr[qs][j]) {
-            const int m = wave * QPW + qs * 16 + 4 * (lane >> 4) + j;
-            const uint32_t slot = atomicAdd(&s_cnt[m], 1u);
-            s_buf[m * CAP + slot] = (uint64_t(ord_f32(d)) << 32) | row;
-          }
+          for (int e = 0; e < 4; ++e)
+            d[e] = qn + dn4[g][e] - 2.0f * (acc0[4 * g + e] + acc1[4 * g + e]);
+          *reinterpret_cast<f32x4*>(a.sdist + int64_t(my_q) * a.s_rows + srow0 + 8 * g +
+                                    4 * (lane >> 5)) = d;
         }
       }
-      // Keep room for the next tile (at most 16 new keys per query).
-      const bool over = lane < QPW && s_cnt[wave * QPW + lane] > uint32_t(CAP - 16);
-      if (__ballot(over) != 0) compact_wave(uint32_t(CAP - 16));
+    } else {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int r = half * 8; r < half * 8 + 8; ++r) {
+          const float d = qn + dn4[r >> 2][r & 3] - 2.0f * (acc0[r] + acc1[r]);
+          if (d < thr) {
+            const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
+            const uint32_t slot = atomicAdd(&s_cnt[qw], 1u);
+            s_buf[qw * kCap + slot] = (uint64_t(ord_f32(d)) << 32) | row;
+          }
+        }
+        // At most 16 keys per query per half tile: keep that much room.
+        compact_wave(uint32_t(kCap - 16));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.f;
+  };
+
+  // MFMA over NB consecutive 1 KiB blocks at `sb` (k-steps KOFF .. KOFF+NB-1),
+  // A fragments through a PF-deep register ring, alternating two chains.
+  auto mfma_run = [&](const u32x4* sb, auto nb_c, auto koff_c) CVS_INLINE {
+    constexpr int NB = decltype(nb_c)::value, KOFF = decltype(koff_c)::value;
+    constexpr int PF = NB < 4 ? NB : 4;
+    half8 ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) ring[p] = __builtin_bit_cast(half8, sb[p * 64]);
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      const half8 av = ring[blk % PF];
+      if (blk + PF < NB) ring[blk % PF] = __builtin_bit_cast(half8, sb[(blk + PF) * 64]);
+      if (blk & 1)
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + blk], acc1, 0, 0, 0);
+      else
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + blk], acc0, 0, 0, 0);
     }
   };
 
-  // ---- software pipeline: LDS double buffer, two stages of loads in flight ----
-  if (st0 < st1) gload(ra, na, st0);
-  if (st0 + 1 < st1) gload(rb, nb, st0 + 1);
-  if (st0 < st1) lstore(0, ra, na);
-  if (st0 + 2 < st1) gload(ra, na, st0 + 2);
+  auto compute = [&](auto buf_c, int j) CVS_INLINE {
+    constexpr int BUF = decltype(buf_c)::value;
+    const int64_t st = stage_of(j);
+    if constexpr (KS >= 32) {
+      // One stage is 32 k-steps of a single tile.
+      constexpr int KOFF = (BUF * kStageBlocks) % KS;
+      mfma_run(s_stage[BUF] + lane, std::integral_constant<int, kStageBlocks>{},
+               std::integral_constant<int, KOFF>{});
+      if constexpr (KOFF + kStageBlocks == KS) epilogue(BUF, 0, (st / SPT) * 32, j);
+    } else {
+      // One stage holds TPS whole tiles.
+#pragma unroll 1
+      for (int t = 0; t < TPS; ++t) {
+        mfma_run(s_stage[BUF] + t * KS * 64 + lane, std::integral_constant<int, KS>{},
+                 std::integral_constant<int, 0>{});
+        epilogue(BUF, t, (st * TPS + t) * 32, j);
+      }
+    }
+  };
+
+  // ---- software pipeline over this workgroup's stages ----
+  if (n_stages > 0) {
+    gload(ra, na, stage_of(0));
+    gload(rb, nb, stage_of(1));
+    lstore(0, ra, na);
+    if (2 < n_stages) gload(ra, na, stage_of(2));
+  }
   __syncthreads();
-  for (int64_t st = st0; st < st1; st += 2) {
-    // stage st in LDS buffer 0; rb holds st+1, ra holds st+2
-    compute(0, st);
-    if (st + 1 < st1) lstore(1, rb, nb);
-    if (st + 3 < st1) gload(rb, nb, st + 3);
+  for (int j = 0; j < n_stages; j += 2) {
+    compute(std::integral_constant<int, 0>{}, j);
+    lstore(1, rb, nb);
+    if (j + 3 < n_stages) gload(rb, nb, stage_of(j + 3));
     __syncthreads();
-    if (st + 1 >= st1) break;
-    compute(1, st + 1);
-    if (st + 2 < st1) lstore(0, ra, na);
-    if (st + 4 < st1) gload(ra, na, st + 4);
+    compute(std::integral_constant<int, 1>{}, j + 1);
+    if (j + 2 < n_stages) lstore(0, ra, na);
+    if (j + 4 < n_stages) gload(ra, na, stage_of(j + 4));
     __syncthreads();
   }
 
-  // ---- final compaction to kp and write-out ----
-  compact_wave(uint32_t(kp));
-  const int64_t G64 = G;
-  for (int i = lane; i < QPW * kp; i += 64) {
-    const int qw = i / kp, e = i - qw * kp;
-    const int m = wave * QPW + qw;
-    const int q = qbase + m;
-    if (q >= a.nq) continue;
-    const uint32_t c = s_cnt[m];
-    a.part[(int64_t(q) * G64 + x) * kp + e] = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
+  if (MODE == kModeScan) {
+    compact_wave(uint32_t(kp));
+    const int64_t G64 = G;
+    for (int i = 0; i < 32; ++i) {
+      const int m = wave * 32 + i;
+      const int q = qbase + m;
+      if (q >= a.nq) break;
+      const uint32_t c = s_cnt[m];
+      for (int e = lane; e < kp; e += 64)
+        a.part[(int64_t(q) * G64 + x) * kp + e] = uint32_t(e) < c ? s_buf[m * kCap + e] : kSentinel;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Merge + exact re-rank: one workgroup per query.
+// Block-wide helpers (256 threads).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int block_sum(int v, int* s_red) {
+// Sum over the block; `phase` alternates the reduction buffer so that one
+// barrier per call suffices.
+__device__ __forceinline__ int block_sum(int v, int* s_red, int phase) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) s_red[phase * kWaves + (threadIdx.x >> 6)] = v;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) s_red[wave] = v;
-  __syncthreads();
-  return s_red[0] + s_red[1] + s_red[2] + s_red[3];
+  return s_red[phase * kWaves + 0] + s_red[phase * kWaves + 1] + s_red[phase * kWaves + 2] +
+         s_red[phase * kWaves + 3];
 }
 
+// kp-th smallest sampled distance per query -> initial scan threshold.
 template <int EPT>
-__global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restrict__ part, int m_keys,
-                                                       int kp, const float* __restrict__ rows,
-                                                       int64_t d, const float* __restrict__ queries,
-                                                       int64_t k, uint32_t* __restrict__ out_nbr,
+__global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict__ sdist,
+                                                        int64_t s_rows, int kp,
+                                                        float* __restrict__ thr0) {
+  __shared__ int s_red[2 * kWaves];
+  const int tid = threadIdx.x;
+  const float* src = sdist + int64_t(blockIdx.x) * s_rows;
+  uint32_t v[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int64_t e = tid + int64_t(i) * kThreads;
+    v[i] = e < s_rows ? ord_f32(src[e]) : 0xffffffffu;
+  }
+  int need = kp;
+  uint32_t pre = 0;
+  for (int b = 31; b >= 0; --b) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) c += ((v[i] ^ pre) >> b) == 0 ? 1 : 0;
+    c = block_sum(c, s_red, b & 1);
+    if (c < need) {
+      need -= c;
+      pre |= 1u << b;
+    }
+  }
+  if (tid == 0) thr0[blockIdx.x] = pre == 0xffffffffu ? INFINITY : unord_f32(pre);
+}
+
+// Merge + exact re-rank: one workgroup per query.
+template <int EPT>
+__global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restrict__ part,
+                                                       int m_keys, int kp,
+                                                       const float* __restrict__ rows, int64_t d,
+                                                       const float* __restrict__ queries, int64_t k,
+                                                       uint32_t* __restrict__ out_nbr,
                                                        float* __restrict__ out_dist) {
-  __shared__ int s_red[kWaves];
+  __shared__ int s_red[2 * kWaves];
   __shared__ int s_n;
   __shared__ uint64_t s_sel[64];
   __shared__ float s_ex[64];
@@ -389,7 +432,7 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
     int c = 0;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) c += ((hi[i] ^ pre) >> b) == 0 ? 1 : 0;
-    c = block_sum(c, s_red);
+    c = block_sum(c, s_red, b & 1);
     if (c < need) {
       need -= c;
       pre |= 1u << b;
@@ -401,14 +444,13 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
     int c = 0;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) c += (hi[i] == kth_hi && ((lo[i] ^ pre2) >> b) == 0) ? 1 : 0;
-    c = block_sum(c, s_red);
+    c = block_sum(c, s_red, b & 1);
     if (c < need) {
       need -= c;
       pre2 |= 1u << b;
     }
   }
   const uint64_t kth = (uint64_t(kth_hi) << 32) | pre2;
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const uint64_t key = (uint64_t(hi[i]) << 32) | lo[i];
@@ -468,17 +510,47 @@ int choose_kp(int64_t k) {
 }
 
 template <int KS>
-void launch_scan(cvs_context* ctx, dim3 grid, const ScanArgs& args) {
-  hipLaunchKernelGGL((bf_scan_kernel<KS, 2>), grid, dim3(kThreads), 0, ctx->stream, args);
+void launch_scan_ks(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode) {
+  if (mode == kModeScan)
+    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeScan>), grid, dim3(kThreads), 0, ctx->stream, args);
+  else
+    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeSample>), grid, dim3(kThreads), 0, ctx->stream,
+                       args);
+}
+
+void launch_scan(cvs_context* ctx, int ks, dim3 grid, const ScanArgs& args, int mode) {
+  switch (ks) {
+    case 2: launch_scan_ks<2>(ctx, grid, args, mode); break;
+    case 4: launch_scan_ks<4>(ctx, grid, args, mode); break;
+    case 8: launch_scan_ks<8>(ctx, grid, args, mode); break;
+    case 16: launch_scan_ks<16>(ctx, grid, args, mode); break;
+    case 32: launch_scan_ks<32>(ctx, grid, args, mode); break;
+    case 64: launch_scan_ks<64>(ctx, grid, args, mode); break;
+    default: fail(CVS_ERR_UNSUPPORTED, "unsupported padded dimension");
+  }
+  after_launch(mode == kModeScan ? "bf_scan_kernel" : "bf_sample_kernel");
+}
+
+template <template <int> class K, typename... Args>
+void launch_by_ept(int64_t ept, dim3 grid, hipStream_t s, Args... args) {
+  if (ept <= 16)
+    hipLaunchKernelGGL(K<16>::fn, grid, dim3(kThreads), 0, s, args...);
+  else if (ept <= 32)
+    hipLaunchKernelGGL(K<32>::fn, grid, dim3(kThreads), 0, s, args...);
+  else if (ept <= 64)
+    hipLaunchKernelGGL(K<64>::fn, grid, dim3(kThreads), 0, s, args...);
+  else
+    fail(CVS_ERR_RUNTIME, "list larger than the selection kernels support");
 }
 
 template <int EPT>
-void launch_merge(cvs_context* ctx, int64_t q, const uint64_t* part, int m_keys, int kp,
-                  const cvs_dataset* ds, const float* queries, int64_t k, uint32_t* nbr,
-                  float* dist) {
-  hipLaunchKernelGGL((bf_merge_kernel<EPT>), dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
-                     part, m_keys, kp, ds->rows, ds->d, queries, k, nbr, dist);
-}
+struct SelectK {
+  static constexpr auto fn = bf_select_kernel<EPT>;
+};
+template <int EPT>
+struct MergeK {
+  static constexpr auto fn = bf_merge_kernel<EPT>;
+};
 
 void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q,
                       int64_t k, uint32_t* nbr, float* dist) {
@@ -492,21 +564,35 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   if (q > (int64_t(1) << 24)) fail(CVS_ERR_UNSUPPORTED, "too many queries in one call");
 
   const int ks = int(ds->dp / kStepCols);
-  const int tps = ks >= 32 ? 1 : 32 / ks;
-  const int64_t n_stages = ds->n_tiles / tps;
+  const int rpu = 2 * kStageBlocks * 32 / ks;  // rows per unit
+  const int64_t n_units = ds->n_tiles * ks / (2 * kStageBlocks);
   int G = ctx->compute_units;
   if (G > 256) G = 256;
-  if (int64_t(G) > n_stages) G = int(n_stages);
+  if (int64_t(G) > n_units) G = int(n_units);
   const int kp = choose_kp(k);
-  const int qb = 128;
-  const int64_t q_tiles = (q + 15) / 16;
+  const int64_t q_tiles = (q + 31) / 32;
+  const unsigned qblocks = unsigned((q + kQB - 1) / kQB);
 
-  // Workspaces: query tiles + norms, partial lists.
+  // Sample: ~256*kp rows in whole units, evenly strided.
+  int64_t s_units = (256 * int64_t(kp)) / rpu;
+  if (s_units < 1) s_units = 1;
+  if (s_units > n_units) s_units = n_units;
+  const int64_t s_stride = n_units / s_units;
+  const int64_t s_rows = s_units * rpu;
+  int Gs = ctx->compute_units;
+  if (int64_t(Gs) > s_units) Gs = int(s_units);
+
+  // Workspaces: query tiles + norms | thresholds | sample distances; lists.
   const size_t qtile_bytes = size_t(q_tiles) * size_t(ks) * kStepBytes;
-  const size_t qnorm_bytes = size_t(q_tiles) * 16 * sizeof(float);
-  ctx->ws_queries.reserve(qtile_bytes + qnorm_bytes);
-  uint16_t* qtiles = ctx->ws_queries.as<uint16_t>();
-  float* qnorms = reinterpret_cast<float*>(ctx->ws_queries.as<char>() + qtile_bytes);
+  const size_t qnorm_bytes = size_t(q_tiles) * 32 * sizeof(float);
+  const size_t thr_bytes = (size_t(q) * sizeof(float) + 255) / 256 * 256;
+  const size_t sdist_bytes = size_t(q) * size_t(s_rows) * sizeof(float);
+  ctx->ws_queries.reserve(qtile_bytes + qnorm_bytes + thr_bytes + sdist_bytes);
+  char* wsq = ctx->ws_queries.as<char>();
+  uint16_t* qtiles = reinterpret_cast<uint16_t*>(wsq);
+  float* qnorms = reinterpret_cast<float*>(wsq + qtile_bytes);
+  float* thr0 = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes);
+  float* sdist = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes);
   const int m_keys = G * kp;
   ctx->ws_partial.reserve(size_t(q) * size_t(m_keys) * sizeof(uint64_t));
   uint64_t* part = ctx->ws_partial.as<uint64_t>();
@@ -515,40 +601,39 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   launch_to_tiles(ctx, queries, q, ds->d, ds->dp, q_tiles, qtiles, qnorms);
   timer_end(ctx, "bf_prep", t0);
 
-  ScanArgs args;
+  ScanArgs args{};
   args.tiles = reinterpret_cast<const u32x4*>(ds->tiles);
   args.norms = reinterpret_cast<const f32x4*>(ds->norms);
-  args.n_stages = n_stages;
+  args.n_units = n_units;
   args.qtiles = reinterpret_cast<const u32x4*>(qtiles);
   args.qnorms = qnorms;
   args.nq = int(q);
-  args.n_qslices = int(q_tiles);
+  args.n_qtiles = int(q_tiles);
   args.kp = kp;
+  args.thr0 = thr0;
   args.part = part;
-  const dim3 grid(unsigned(G), unsigned((q + qb - 1) / qb));
-  hipEvent_t t1 = timer_begin(ctx, "bf_scan");
-  switch (ks) {
-    case 1: launch_scan<1>(ctx, grid, args); break;
-    case 2: launch_scan<2>(ctx, grid, args); break;
-    case 4: launch_scan<4>(ctx, grid, args); break;
-    case 8: launch_scan<8>(ctx, grid, args); break;
-    case 16: launch_scan<16>(ctx, grid, args); break;
-    case 32: launch_scan<32>(ctx, grid, args); break;
-    default: fail(CVS_ERR_UNSUPPORTED, "unsupported padded dimension");
-  }
-  after_launch("bf_scan_kernel");
-  timer_end(ctx, "bf_scan", t1);
+  args.sdist = sdist;
+  args.s_units = s_units;
+  args.s_stride = s_stride;
+  args.s_rows = s_rows;
 
-  hipEvent_t t2 = timer_begin(ctx, "bf_merge");
-  const int ept = (m_keys + kThreads - 1) / kThreads;
-  if (ept <= 16)
-    launch_merge<16>(ctx, q, part, m_keys, kp, ds, queries, k, nbr, dist);
-  else if (ept <= 32)
-    launch_merge<32>(ctx, q, part, m_keys, kp, ds, queries, k, nbr, dist);
-  else
-    launch_merge<64>(ctx, q, part, m_keys, kp, ds, queries, k, nbr, dist);
+  hipEvent_t t1 = timer_begin(ctx, "bf_sample");
+  launch_scan(ctx, ks, dim3(unsigned(Gs), qblocks), args, kModeSample);
+  launch_by_ept<SelectK>((s_rows + kThreads - 1) / kThreads, dim3(unsigned(q)), ctx->stream,
+                         static_cast<const float*>(sdist), s_rows, kp, thr0);
+  after_launch("bf_select_kernel");
+  timer_end(ctx, "bf_sample", t1);
+
+  hipEvent_t t2 = timer_begin(ctx, "bf_scan");
+  launch_scan(ctx, ks, dim3(unsigned(G), qblocks), args, kModeScan);
+  timer_end(ctx, "bf_scan", t2);
+
+  hipEvent_t t3 = timer_begin(ctx, "bf_merge");
+  launch_by_ept<MergeK>((m_keys + kThreads - 1) / kThreads, dim3(unsigned(q)), ctx->stream,
+                        static_cast<const uint64_t*>(part), m_keys, kp,
+                        static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   after_launch("bf_merge_kernel");
-  timer_end(ctx, "bf_merge", t2);
+  timer_end(ctx, "bf_merge", t3);
 }
 
 }  // namespace

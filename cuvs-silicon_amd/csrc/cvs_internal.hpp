@@ -92,10 +92,10 @@ struct cvs_dataset {
   int64_t n = 0;          // rows
   int64_t d = 0;          // dimensions
   int64_t dp = 0;         // padded dimensions (32 * power of two)
-  int64_t n_tiles = 0;    // 16-row tiles, padded to a multiple of 32
+  int64_t n_tiles = 0;    // 32-row tiles, padded to a multiple of kTilePad
   float* rows = nullptr;          // n x d fp32, row-major
-  uint16_t* tiles = nullptr;      // n_tiles x (dp/32) x 64 lanes x 8 fp16
-  float* norms = nullptr;         // n_tiles*16 squared norms of fp16 rows (+inf pad)
+  uint16_t* tiles = nullptr;      // n_tiles x (dp/16) x 64 lanes x 8 fp16
+  float* norms = nullptr;         // n_tiles*32 squared norms of fp16 rows (+inf pad)
 };
 
 namespace cvs {
@@ -114,23 +114,25 @@ inline void after_launch(const char* what) {
 }
 
 // fp16 tile layout (shared by dataset and query tiles): tile t holds rows
-// [16t, 16t+16); k-step s holds columns [32s, 32s+32); lane l of a 64-lane
-// wave holds row 16t + (l % 16), columns 32s + 8*(l/16) + [0, 8).  One k-step
+// [32t, 32t+32); k-step s holds columns [16s, 16s+16); lane l of a 64-lane
+// wave holds row 32t + (l % 32), columns 16s + 8*(l/32) + [0, 8).  One k-step
 // of one tile is therefore 1 KiB contiguous, loaded by one wave with one
-// 16-byte access per lane, and is exactly the per-lane operand of
-// v_mfma_f32_16x16x32_f16.
-constexpr int kTileRows = 16;
-constexpr int kStepCols = 32;
+// 16-byte access per lane, and is exactly the per-lane A (or B) operand of
+// v_mfma_f32_32x32x16_f16.  The tile count is padded to a multiple of
+// kTilePad so that the scan can always stream whole 64 KiB units.
+constexpr int kTileRows = 32;
+constexpr int kStepCols = 16;
 constexpr int kStepBytes = 1024;
+constexpr int kTilePad = 64;
 
 inline int64_t padded_dim(int64_t d) {
-  int64_t p = kStepCols;
+  int64_t p = 32;
   while (p < d) p *= 2;
   return p;
 }
 
 // Launches the fp32 -> fp16-tile conversion (rows may be n x d with row
-// stride d); writes n_tiles tiles and n_tiles*16 norms.
+// stride d); writes n_tiles tiles and n_tiles*32 norms.
 void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
                      int64_t dp, int64_t n_tiles, uint16_t* tiles, float* norms);
 

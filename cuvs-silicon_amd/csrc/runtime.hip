@@ -69,10 +69,10 @@ void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin) {
 }
 
 // ---------------------------------------------------------------------------
-// fp32 rows -> fp16 16-row tiles + squared norms of the fp16-rounded rows.
-// One 64-lane wave per tile.  Lane l owns row 16t + l%16 and, for every
-// k-step s, the 8 columns 32s + 8*(l/16) + [0,8); the four lanes sharing a
-// row combine their partial norms with two xor-shuffles.  Rows >= n and
+// fp32 rows -> fp16 32-row tiles + squared norms of the fp16-rounded rows.
+// One 64-lane wave per tile.  Lane l owns row 32t + l%32 and, for every
+// k-step s, the 8 columns 16s + 8*(l/32) + [0,8); the two lanes sharing a
+// row combine their partial norms with one xor-shuffle.  Rows >= n and
 // columns >= d are written as zeros; padding rows get norm +inf so that no
 // distance involving them can pass a candidate filter.
 // ---------------------------------------------------------------------------
@@ -82,8 +82,8 @@ __global__ __launch_bounds__(64) void to_tiles_kernel(const float* __restrict__ 
                                                       float* __restrict__ norms) {
   const int64_t t = blockIdx.x;
   const int lane = threadIdx.x;
-  const int64_t r = t * kTileRows + (lane & 15);
-  const int cgrp = lane >> 4;
+  const int64_t r = t * kTileRows + (lane & 31);
+  const int cgrp = lane >> 5;
   const bool row_ok = r < n;
   const float* src = rows + (row_ok ? r : 0) * d;
   float acc = 0.f;
@@ -102,9 +102,8 @@ __global__ __launch_bounds__(64) void to_tiles_kernel(const float* __restrict__ 
     __builtin_memcpy(&packed, h, sizeof(packed));
     tiles[(t * ksteps + s) * 64 + lane] = packed;
   }
-  acc += __shfl_xor(acc, 16);
   acc += __shfl_xor(acc, 32);
-  if (cgrp == 0) norms[t * kTileRows + (lane & 15)] = row_ok ? acc : INFINITY;
+  if (cgrp == 0) norms[t * kTileRows + (lane & 31)] = row_ok ? acc : INFINITY;
 }
 
 void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp,
@@ -290,7 +289,7 @@ int cvs_dataset_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d
     ds->d = d;
     ds->dp = padded_dim(d);
     const int64_t tiles = (n + kTileRows - 1) / kTileRows;
-    ds->n_tiles = (tiles + 31) / 32 * 32;  // whole 32-tile groups: no ragged loads
+    ds->n_tiles = (tiles + kTilePad - 1) / kTilePad * kTilePad;  // no ragged stage loads
     try {
       const size_t row_bytes = size_t(n) * size_t(d) * sizeof(float);
       CVS_HIP(hipMalloc(&ds->rows, row_bytes));
