@@ -166,7 +166,7 @@ def main() -> int:
     for _ in range(args.steps):
         ds.bf_search_async(dq, k, dn, dd)
     ctx.synchronize()
-    kt = {name: ctx.kernel_time(name) for name in ("bf_prep", "bf_scan", "bf_merge")}
+    kt = {name: ctx.kernel_time(name) for name in ("bf_prep", "bf_sample", "bf_scan", "bf_merge")}
     ctx.set_timing(False)
     scan_ms = kt["bf_scan"][0] / max(kt["bf_scan"][1], 1)
     alg_bytes = n * d * 2 + n * 4 + q * d * 2 + q * k * 8

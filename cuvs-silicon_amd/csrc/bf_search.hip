@@ -55,8 +55,7 @@ constexpr int kWaves = 4;
 constexpr int kQB = 128;                                // queries per workgroup (32 per wave)
 constexpr int kStageBlocks = 32;                        // 1 KiB blocks per stage
 constexpr int kStageVecs = kStageBlocks * 64;           // 16-byte vectors per stage
-constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 8
-constexpr int kCap = 80;                                // LDS list slots per query
+constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 8 16-byte loads per thread and stage
 constexpr uint64_t kSentinel = ~0ull;
 
 enum { kModeScan = 0, kModeSample = 1 };
@@ -82,7 +81,19 @@ struct Cfg {
   static constexpr int TPS = KS >= 32 ? 1 : 32 / KS;      // tiles per stage
   static constexpr int SPT = KS >= 32 ? KS / 32 : 1;      // stages per tile
   static constexpr int RPU = 2 * kStageBlocks * 32 / KS;  // rows per 2-stage unit
+  static constexpr int NF = TPS * 32;                     // norms per stage
   static_assert(KS >= 2 && KS <= 64, "k-steps per tile");
+};
+
+// LDS list geometry per kp.  A query can receive 2 lanes x H keys between
+// two overflow checks (H rows per lane); lists keep that much room.
+template <int KP, int MODE>
+struct Lists {
+  static constexpr int H = KP <= 32 ? 16 : 8;  // rows per lane between checks
+  // Beyond kp + 2H, the slack (32, 24, 8 keys) sets how many pushes one
+  // compaction is amortized over; bounded by the 160 KiB LDS budget.
+  static constexpr int CAP = MODE != 0 ? 1 : (KP == 16 ? 80 : 88);
+  static_assert(MODE != 0 || CAP >= KP + 2 * H + 8, "list slack");
 };
 
 struct ScanArgs {
@@ -153,17 +164,19 @@ __device__ __forceinline__ void compact_query(uint64_t* list, uint32_t* cnt_slot
   }
 }
 
-template <int KS, int MODE>
+template <int KS, int MODE, int KP>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void bf_scan_kernel(ScanArgs a) {
   using C = Cfg<KS>;
-  constexpr int TPS = C::TPS, SPT = C::SPT, RPU = C::RPU;
+  using L = Lists<KP, MODE>;
+  constexpr int TPS = C::TPS, SPT = C::SPT, RPU = C::RPU, NF = C::NF;
+  constexpr int CAP = L::CAP;
 
   __shared__ u32x4 s_stage[2][kStageVecs];
-  __shared__ float s_dn[2][TPS * 32];
+  __shared__ float s_dn[2][NF];
   __shared__ uint32_t s_cnt[kQB];
   __shared__ float s_thr[kQB];
-  __shared__ uint64_t s_buf[MODE == kModeScan ? kQB * kCap : 1];
+  __shared__ uint64_t s_buf[kQB * CAP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -171,7 +184,6 @@ void bf_scan_kernel(ScanArgs a) {
   const int G = gridDim.x;
   const int x = blockIdx.x;
   const int qbase = blockIdx.y * kQB;
-  const int kp = a.kp;
 
   // Units of this workgroup: contiguous (scan) or a strided sample (sample).
   const int64_t total = MODE == kModeScan ? a.n_units : a.s_units;
@@ -183,19 +195,54 @@ void bf_scan_kernel(ScanArgs a) {
   };
   auto stage_of = [&](int j) CVS_INLINE -> int64_t { return 2 * unit_of(i0 + (j >> 1)) + (j & 1); };
 
+  // ---- stage loads: HBM -> registers (two stages in flight) -> LDS ----
+  constexpr int NPT = (NF + kThreads - 1) / kThreads;  // norms per thread and stage
+  u32x4 ra[kLoadsPerThread], rb[kLoadsPerThread];
+  float na[NPT], nb[NPT];
+  auto gload = [&](u32x4 (&r)[kLoadsPerThread], float (&nr)[NPT], int j) CVS_INLINE {
+    if (j >= n_stages) return;
+    const int64_t st = stage_of(j);
+    const u32x4* src = a.tiles + st * kStageVecs + tid;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) r[i] = __builtin_nontemporal_load(src + i * kThreads);
+    const int64_t tile0 = KS >= 32 ? st / SPT : st * TPS;
+    const float* ns = reinterpret_cast<const float*>(a.norms) + tile0 * 32;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+      if (tid + i * kThreads < NF) nr[i] = ns[tid + i * kThreads];
+  };
+  auto lstore = [&](int buf, const u32x4 (&r)[kLoadsPerThread], const float (&nr)[NPT]) CVS_INLINE {
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) s_stage[buf][tid + i * kThreads] = r[i];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+      if (tid + i * kThreads < NF) s_dn[buf][tid + i * kThreads] = nr[i];
+  };
+  gload(ra, na, 0);
+  gload(rb, nb, 1);
+
   // ---- resident query operands: wave owns queries [qbase + 32*wave, +32) ----
   const int qt = (qbase >> 5) + wave;
   const int my_q = qbase + wave * 32 + (lane & 31);
   const bool q_ok = my_q < a.nq;
+  // Loaded 16 k-steps at a time (16 loads in flight), then pinned to AGPRs:
+  // MFMA reads B from AGPRs, which leaves the arch VGPRs for the A-fragment
+  // ring, the accumulators and the epilogue.
   half8 qb[KS];
+  const bool qt_ok = qt < a.n_qtiles;
+  const u32x4* qsrc = a.qtiles + int64_t(qt_ok ? qt : 0) * KS * 64 + lane;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    u32x4 v = qt < a.n_qtiles ? a.qtiles[(int64_t(qt) * KS + s) * 64 + lane] : u32x4{0, 0, 0, 0};
-    half8 h = __builtin_bit_cast(half8, v);
-    // Pin the resident operand to an AGPR (MFMA reads B from AGPRs), leaving
-    // the arch VGPRs for stage loads, the A-fragment ring and accumulators.
-    asm volatile("" : "+a"(h));
-    qb[s] = h;
+  for (int c = 0; c < KS; c += 16) {
+    constexpr int CH = KS < 16 ? KS : 16;
+    u32x4 tmp[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) tmp[i] = qsrc[(c + i) * 64];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      half8 h = __builtin_bit_cast(half8, qt_ok ? tmp[i] : u32x4{0, 0, 0, 0});
+      asm volatile("" : "+a"(h));
+      qb[c + i] = h;
+    }
   }
   const float qn = q_ok ? a.qnorms[my_q] : INFINITY;
   const int qw = wave * 32 + (lane & 31);  // this lane's query slot in the workgroup
@@ -208,23 +255,6 @@ void bf_scan_kernel(ScanArgs a) {
     }
   }
 
-  // ---- stage loads: HBM -> registers -> LDS ----
-  u32x4 ra[kLoadsPerThread], rb[kLoadsPerThread];
-  f32x4 na = {0, 0, 0, 0}, nb = {0, 0, 0, 0};
-  const bool norm_loader = tid < TPS * 8;
-  auto gload = [&](u32x4 (&r)[kLoadsPerThread], f32x4& nr, int64_t st) CVS_INLINE {
-    const u32x4* src = a.tiles + st * kStageVecs + tid;
-#pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) r[i] = __builtin_nontemporal_load(src + i * kThreads);
-    const int64_t tile0 = KS >= 32 ? st / SPT : st * TPS;
-    if (norm_loader) nr = a.norms[tile0 * 8 + tid];
-  };
-  auto lstore = [&](int buf, const u32x4 (&r)[kLoadsPerThread], const f32x4& nr) CVS_INLINE {
-#pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) s_stage[buf][tid + i * kThreads] = r[i];
-    if (norm_loader) *reinterpret_cast<f32x4*>(&s_dn[buf][tid * 4]) = nr;
-  };
-
   // Compacts every list of this wave whose count exceeds `limit`, then
   // tightens this lane's threshold.
   auto compact_wave = [&](uint32_t limit) CVS_INLINE {
@@ -234,22 +264,23 @@ void bf_scan_kernel(ScanArgs a) {
       const int i = __builtin_ctzll(over);
       over &= over - 1;
       const int m = wave * 32 + i;
-      compact_query(s_buf + m * kCap, &s_cnt[m], &s_thr[m], kp);
+      compact_query(s_buf + m * CAP, &s_cnt[m], &s_thr[m], KP);
     }
     thr = fminf(thr, s_thr[qw]);
   };
 
+  // Accumulators live in arch VGPRs so that all 256 AGPRs hold query operands.
   f32x16 acc0, acc1;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.f;
+  asm volatile("" : "+v"(acc0), "+v"(acc1));
 
   // Epilogue for one finished 32-row tile: this lane holds query `my_q`
   // against rows row0 + 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
-  auto epilogue = [&](int buf, int tis, int64_t row0, int j) CVS_INLINE {
+  auto epilogue = [&](const float* dn, int64_t row0, int j) CVS_INLINE {
     f32x4 dn4[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      dn4[g] = *reinterpret_cast<const f32x4*>(&s_dn[buf][tis * 32 + 8 * g + 4 * (lane >> 5)]);
+    for (int g = 0; g < 4; ++g) dn4[g] = *reinterpret_cast<const f32x4*>(dn + 8 * g + 4 * (lane >> 5));
     if (MODE == kModeSample) {
       if (q_ok) {
         const int64_t i = i0 + (j >> 1);
@@ -265,93 +296,125 @@ void bf_scan_kernel(ScanArgs a) {
         }
       }
     } else {
+      // Fast path: branch-free pass mask over the 16 rows.
+      float dv[16];
+      uint32_t pass = 0;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      for (int r = 0; r < 16; ++r) {
+        dv[r] = qn + dn4[r >> 2][r & 3] - 2.0f * (acc0[r] + acc1[r]);
+        pass |= (dv[r] < thr ? 1u : 0u) << r;
+      }
+      if (__ballot(pass != 0) != 0) {
+        // Rare path: each lane reserves slots for all its passing keys of H
+        // rows with one atomic, writes them, and the atomic's return value
+        // tells whether the list needs compacting (no extra LDS read).
+        constexpr int H = L::H;
 #pragma unroll
-        for (int r = half * 8; r < half * 8 + 8; ++r) {
-          const float d = qn + dn4[r >> 2][r & 3] - 2.0f * (acc0[r] + acc1[r]);
-          if (d < thr) {
-            const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
-            const uint32_t slot = atomicAdd(&s_cnt[qw], 1u);
-            s_buf[qw * kCap + slot] = (uint64_t(ord_f32(d)) << 32) | row;
+        for (int h = 0; h < 16; h += H) {
+          const uint32_t hp = (pass >> h) & ((1u << H) - 1u);
+          const int np = popc(hp);
+          uint32_t slot = 0;
+          if (np) slot = atomicAdd(&s_cnt[qw], uint32_t(np));
+#pragma unroll
+          for (int r = h; r < h + H; ++r) {
+            if (hp & (1u << (r - h))) {
+              const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
+              s_buf[qw * CAP + slot] = (uint64_t(ord_f32(dv[r])) << 32) | row;
+              ++slot;
+            }
+          }
+          const uint64_t over = __ballot(np != 0 && slot > uint32_t(CAP - 2 * H));
+          if (over != 0) {
+            compact_wave(uint32_t(CAP - 2 * H));
+            // Keys above the lowered threshold are dropped from later groups.
+#pragma unroll
+            for (int r = h + H; r < 16; ++r)
+              if (!(dv[r] < thr)) pass &= ~(1u << r);
           }
         }
-        // At most 16 keys per query per half tile: keep that much room.
-        compact_wave(uint32_t(kCap - 16));
       }
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.f;
+    asm volatile("" : "+v"(acc0), "+v"(acc1));
   };
 
   // MFMA over NB consecutive 1 KiB blocks at `sb` (k-steps KOFF .. KOFF+NB-1),
   // A fragments through a PF-deep register ring, alternating two chains.
   auto mfma_run = [&](const u32x4* sb, auto nb_c, auto koff_c) CVS_INLINE {
-    constexpr int NB = decltype(nb_c)::value, KOFF = decltype(koff_c)::value;
-    constexpr int PF = NB < 4 ? NB : 4;
+    constexpr int NBLK = decltype(nb_c)::value, KOFF = decltype(koff_c)::value;
+    constexpr int PF = NBLK < 8 ? NBLK : 8;
     half8 ring[PF];
 #pragma unroll
     for (int p = 0; p < PF; ++p) ring[p] = __builtin_bit_cast(half8, sb[p * 64]);
 #pragma unroll
-    for (int blk = 0; blk < NB; ++blk) {
+    for (int blk = 0; blk < NBLK; ++blk) {
       const half8 av = ring[blk % PF];
-      if (blk + PF < NB) ring[blk % PF] = __builtin_bit_cast(half8, sb[(blk + PF) * 64]);
+      if (blk + PF < NBLK) ring[blk % PF] = __builtin_bit_cast(half8, sb[(blk + PF) * 64]);
       if (blk & 1)
         acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + blk], acc1, 0, 0, 0);
       else
         acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + blk], acc0, 0, 0, 0);
     }
+    // Schedule: PF LDS reads up front, then (MFMA, read) pairs, then drain.
+#pragma unroll
+    for (int p = 0; p < PF; ++p) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int p = 0; p < NBLK - PF; ++p) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
   };
 
-  auto compute = [&](auto buf_c, int j) CVS_INLINE {
-    constexpr int BUF = decltype(buf_c)::value;
+  // Stage j in LDS buffer `buf`; PAR = j & 1 (static) selects the k-offset.
+  auto compute = [&](auto par_c, int buf, int j) CVS_INLINE {
+    constexpr int PAR = decltype(par_c)::value;
     const int64_t st = stage_of(j);
+    const u32x4* sb = s_stage[buf] + lane;
+    const float* dn = s_dn[buf];
+    (void)st;
     if constexpr (KS >= 32) {
       // One stage is 32 k-steps of a single tile.
-      constexpr int KOFF = (BUF * kStageBlocks) % KS;
-      mfma_run(s_stage[BUF] + lane, std::integral_constant<int, kStageBlocks>{},
-               std::integral_constant<int, KOFF>{});
-      if constexpr (KOFF + kStageBlocks == KS) epilogue(BUF, 0, (st / SPT) * 32, j);
+      constexpr int KOFF = (PAR * kStageBlocks) % KS;
+      mfma_run(sb, std::integral_constant<int, kStageBlocks>{}, std::integral_constant<int, KOFF>{});
+      if constexpr (KOFF + kStageBlocks == KS) epilogue(dn, (st / SPT) * 32, j);
     } else {
       // One stage holds TPS whole tiles.
 #pragma unroll 1
       for (int t = 0; t < TPS; ++t) {
-        mfma_run(s_stage[BUF] + t * KS * 64 + lane, std::integral_constant<int, KS>{},
-                 std::integral_constant<int, 0>{});
-        epilogue(BUF, t, (st * TPS + t) * 32, j);
+        mfma_run(sb + t * KS * 64, std::integral_constant<int, KS>{}, std::integral_constant<int, 0>{});
+        epilogue(dn + t * 32, (st * TPS + t) * 32, j);
       }
     }
   };
 
-  // ---- software pipeline over this workgroup's stages ----
-  if (n_stages > 0) {
-    gload(ra, na, stage_of(0));
-    gload(rb, nb, stage_of(1));
-    lstore(0, ra, na);
-    if (2 < n_stages) gload(ra, na, stage_of(2));
-  }
-  __syncthreads();
+  // ---- pipeline: per stage, registers -> LDS, reload the registers two
+  // stages ahead, one barrier, compute.  One barrier per stage suffices with
+  // two LDS buffers: buffer j&1 was last read in stage j-2, and every wave
+  // has passed stage j-1's barrier since.
+  auto step = [&](auto par_c, u32x4 (&r)[kLoadsPerThread], float (&nr)[NPT], int j) CVS_INLINE {
+    constexpr int PAR = decltype(par_c)::value;
+    lstore(PAR, r, nr);
+    gload(r, nr, j + 2);
+    __syncthreads();
+    compute(par_c, PAR, j);
+  };
   for (int j = 0; j < n_stages; j += 2) {
-    compute(std::integral_constant<int, 0>{}, j);
-    lstore(1, rb, nb);
-    if (j + 3 < n_stages) gload(rb, nb, stage_of(j + 3));
-    __syncthreads();
-    compute(std::integral_constant<int, 1>{}, j + 1);
-    if (j + 2 < n_stages) lstore(0, ra, na);
-    if (j + 4 < n_stages) gload(ra, na, stage_of(j + 4));
-    __syncthreads();
+    step(std::integral_constant<int, 0>{}, ra, na, j);
+    step(std::integral_constant<int, 1>{}, rb, nb, j + 1);
   }
 
   if (MODE == kModeScan) {
-    compact_wave(uint32_t(kp));
+    compact_wave(uint32_t(KP));
     const int64_t G64 = G;
     for (int i = 0; i < 32; ++i) {
       const int m = wave * 32 + i;
       const int q = qbase + m;
       if (q >= a.nq) break;
       const uint32_t c = s_cnt[m];
-      for (int e = lane; e < kp; e += 64)
-        a.part[(int64_t(q) * G64 + x) * kp + e] = uint32_t(e) < c ? s_buf[m * kCap + e] : kSentinel;
+      for (int e = lane; e < KP; e += 64)
+        a.part[(int64_t(q) * G64 + x) * KP + e] = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
     }
   }
 }
@@ -439,15 +502,23 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
     }
   }
   const uint32_t kth_hi = pre;
-  uint32_t pre2 = 0;
-  for (int b = 31; b >= 0; --b) {
-    int c = 0;
+  // Select on the id only if several keys share the kp-th distance word.
+  int eq = 0;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) c += (hi[i] == kth_hi && ((lo[i] ^ pre2) >> b) == 0) ? 1 : 0;
-    c = block_sum(c, s_red, b & 1);
-    if (c < need) {
-      need -= c;
-      pre2 |= 1u << b;
+  for (int i = 0; i < EPT; ++i) eq += hi[i] == kth_hi ? 1 : 0;
+  eq = block_sum(eq, s_red, 0);
+  uint32_t pre2 = 0xffffffffu;
+  if (eq > need) {
+    pre2 = 0;
+    for (int b = 31; b >= 0; --b) {
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) c += (hi[i] == kth_hi && ((lo[i] ^ pre2) >> b) == 0) ? 1 : 0;
+      c = block_sum(c, s_red, (b + 1) & 1);
+      if (c < need) {
+        need -= c;
+        pre2 |= 1u << b;
+      }
     }
   }
   const uint64_t kth = (uint64_t(kth_hi) << 32) | pre2;
@@ -462,20 +533,39 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
   __syncthreads();
   const int n_sel = s_n < kp ? s_n : kp;
 
-  // Exact fp32 distances: one wave per candidate.
+  // Exact fp32 distances: one wave per candidate, two candidates in flight.
   const int wave = tid >> 6, lane = tid & 63;
   const float* qv = queries + q * d;
-  for (int c = wave; c < n_sel; c += kWaves) {
-    const uint32_t row = uint32_t(s_sel[c]);
-    const float* xv = rows + int64_t(row) * d;
-    float acc = 0.f;
-    for (int64_t i = lane; i < d; i += 64) {
-      const float t = qv[i] - xv[i];
-      acc += t * t;
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
+  for (int c0 = wave * 2; c0 < n_sel; c0 += 2 * kWaves) {
+    const int nc = c0 + 1 < n_sel ? 2 : 1;
+    float acc[2] = {0.f, 0.f};
+    for (int u = 0; u < nc; ++u) {
+      const float* xv = rows + int64_t(uint32_t(s_sel[c0 + u])) * d;
+      if (vec) {
+        for (int64_t i = int64_t(lane) * 4; i < d; i += 256) {
+          const float4 a = *reinterpret_cast<const float4*>(qv + i);
+          const float4 b = *reinterpret_cast<const float4*>(xv + i);
+          const float t0 = a.x - b.x, t1 = a.y - b.y, t2 = a.z - b.z, t3 = a.w - b.w;
+          acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+        }
+      } else {
+        for (int64_t i = lane; i < d; i += 64) {
+          const float t = qv[i] - xv[i];
+          acc[u] += t * t;
+        }
+      }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
-    if (lane == 0) s_ex[c] = acc;
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) acc[u] += __shfl_xor(acc[u], o);
+    }
+    if (lane == 0) {
+      s_ex[c0] = acc[0];
+      if (nc == 2) s_ex[c0 + 1] = acc[1];
+    }
   }
   __syncthreads();
 
@@ -509,13 +599,27 @@ int choose_kp(int64_t k) {
   return 64;
 }
 
+template <int KS, int KP>
+void launch_scan_kp(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode) {
+  if (mode == kModeScan)
+    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeScan, KP>), grid, dim3(kThreads), 0, ctx->stream, args);
+  else
+    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeSample, KP>), grid, dim3(kThreads), 0, ctx->stream,
+                       args);
+}
+
 template <int KS>
 void launch_scan_ks(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode) {
-  if (mode == kModeScan)
-    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeScan>), grid, dim3(kThreads), 0, ctx->stream, args);
-  else
-    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeSample>), grid, dim3(kThreads), 0, ctx->stream,
-                       args);
+  if (mode == kModeSample) {
+    launch_scan_kp<KS, 16>(ctx, grid, args, mode);  // list geometry unused when sampling
+    return;
+  }
+  switch (args.kp) {
+    case 16: launch_scan_kp<KS, 16>(ctx, grid, args, mode); break;
+    case 32: launch_scan_kp<KS, 32>(ctx, grid, args, mode); break;
+    case 64: launch_scan_kp<KS, 64>(ctx, grid, args, mode); break;
+    default: fail(CVS_ERR_RUNTIME, "unsupported candidate count");
+  }
 }
 
 void launch_scan(cvs_context* ctx, int ks, dim3 grid, const ScanArgs& args, int mode) {

@@ -124,6 +124,7 @@ constexpr int kTileRows = 32;
 constexpr int kStepCols = 16;
 constexpr int kStepBytes = 1024;
 constexpr int kTilePad = 64;
+constexpr int kNormSlack = 256;  // floats allocated past the last tile's norms
 
 inline int64_t padded_dim(int64_t d) {
   int64_t p = 32;

@@ -70,31 +70,45 @@ void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin) {
 
 // ---------------------------------------------------------------------------
 // fp32 rows -> fp16 32-row tiles + squared norms of the fp16-rounded rows.
-// One 64-lane wave per tile.  Lane l owns row 32t + l%32 and, for every
-// k-step s, the 8 columns 16s + 8*(l/32) + [0,8); the two lanes sharing a
-// row combine their partial norms with one xor-shuffle.  Rows >= n and
-// columns >= d are written as zeros; padding rows get norm +inf so that no
-// distance involving them can pass a candidate filter.
+// One 256-thread workgroup per tile; wave w converts k-steps w, w+4, ...
+// Lane l owns row 32t + l%32 and, in k-step s, the 8 columns
+// 16s + 8*(l/32) + [0,8).  Partial norms are combined across the two lanes of
+// a row with one xor-shuffle and across the waves in a fixed order through
+// LDS, so the result does not depend on scheduling.  Rows >= n and columns
+// >= d are written as zeros; padding rows get norm +inf so that no distance
+// involving them can pass a candidate filter.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void to_tiles_kernel(const float* __restrict__ rows,
-                                                      int64_t n, int64_t d, int ksteps,
-                                                      uint4* __restrict__ tiles,
-                                                      float* __restrict__ norms) {
+__global__ __launch_bounds__(256) void to_tiles_kernel(const float* __restrict__ rows,
+                                                       int64_t n, int64_t d, int ksteps,
+                                                       uint4* __restrict__ tiles,
+                                                       float* __restrict__ norms) {
+  __shared__ float s_part[4][32];
   const int64_t t = blockIdx.x;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t r = t * kTileRows + (lane & 31);
   const int cgrp = lane >> 5;
   const bool row_ok = r < n;
   const float* src = rows + (row_ok ? r : 0) * d;
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
   float acc = 0.f;
-  for (int s = 0; s < ksteps; ++s) {
+#pragma unroll 4
+  for (int s = wave; s < ksteps; s += 4) {
     const int64_t c0 = int64_t(s) * kStepCols + cgrp * 8;
+    float v[8];
+    if (vec && row_ok && c0 + 8 <= d) {
+      const float4 a = *reinterpret_cast<const float4*>(src + c0);
+      const float4 b = *reinterpret_cast<const float4*>(src + c0 + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (row_ok && c0 + i < d) ? src[c0 + i] : 0.f;
+    }
     _Float16 h[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t c = c0 + i;
-      const float v = (row_ok && c < d) ? src[c] : 0.f;
-      h[i] = static_cast<_Float16>(v);
+      h[i] = static_cast<_Float16>(v[i]);
       const float hv = static_cast<float>(h[i]);
       acc += hv * hv;
     }
@@ -103,13 +117,19 @@ __global__ __launch_bounds__(64) void to_tiles_kernel(const float* __restrict__ 
     tiles[(t * ksteps + s) * 64 + lane] = packed;
   }
   acc += __shfl_xor(acc, 32);
-  if (cgrp == 0) norms[t * kTileRows + (lane & 31)] = row_ok ? acc : INFINITY;
+  if (cgrp == 0) s_part[wave][lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    const float sum = ((s_part[0][threadIdx.x] + s_part[1][threadIdx.x]) + s_part[2][threadIdx.x]) +
+                      s_part[3][threadIdx.x];
+    norms[t * kTileRows + threadIdx.x] = (t * kTileRows + threadIdx.x < n) ? sum : INFINITY;
+  }
 }
 
 void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp,
                      int64_t n_tiles, uint16_t* tiles, float* norms) {
   if (n_tiles <= 0) return;
-  hipLaunchKernelGGL(to_tiles_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(64), 0,
+  hipLaunchKernelGGL(to_tiles_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0,
                      ctx->stream, rows, n, d, static_cast<int>(dp / kStepCols),
                      reinterpret_cast<uint4*>(tiles), norms);
   after_launch("to_tiles_kernel");
@@ -294,7 +314,10 @@ int cvs_dataset_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d
       const size_t row_bytes = size_t(n) * size_t(d) * sizeof(float);
       CVS_HIP(hipMalloc(&ds->rows, row_bytes));
       CVS_HIP(hipMalloc(&ds->tiles, size_t(ds->n_tiles) * size_t(ds->dp / kStepCols) * kStepBytes));
-      CVS_HIP(hipMalloc(&ds->norms, size_t(ds->n_tiles) * kTileRows * sizeof(float)));
+      // + kNormSlack: stage copies read whole 64-float windows past the last tile.
+      CVS_HIP(hipMalloc(&ds->norms, (size_t(ds->n_tiles) * kTileRows + kNormSlack) * sizeof(float)));
+      CVS_HIP(hipMemsetAsync(ds->norms, 0, (size_t(ds->n_tiles) * kTileRows + kNormSlack) * sizeof(float),
+                             ctx->stream));
       CVS_HIP(hipMemcpyAsync(ds->rows, rows, row_bytes,
                              rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                              ctx->stream));
