@@ -57,6 +57,10 @@ constexpr int kStageBlocks = 32;                        // 1 KiB blocks per stag
 constexpr int kStageVecs = kStageBlocks * 64;           // 16-byte vectors per stage
 constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 8 16-byte loads per thread and stage
 constexpr uint64_t kSentinel = ~0ull;
+// Buffer resource word 3 for raw (untyped) buffer access on gfx9-family
+// targets, and the non-temporal cache policy for the streamed dataset.
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kAuxNT = 2;
 
 enum { kModeScan = 0, kModeSample = 1 };
 
@@ -171,6 +175,8 @@ void bf_scan_kernel(ScanArgs a) {
   using L = Lists<KP, MODE>;
   constexpr int TPS = C::TPS, SPT = C::SPT, RPU = C::RPU, NF = C::NF;
   constexpr int CAP = L::CAP;
+  // Scans over 32 or 64 k-steps per tile run the software-pipelined loop.
+  constexpr bool PIPE = MODE == kModeScan && KS >= 32;
 
   __shared__ u32x4 s_stage[2][kStageVecs];
   __shared__ float s_dn[2][NF];
@@ -218,8 +224,27 @@ void bf_scan_kernel(ScanArgs a) {
     for (int i = 0; i < NPT; ++i)
       if (tid + i * kThreads < NF) s_dn[buf][tid + i * kThreads] = nr[i];
   };
-  gload(ra, na, 0);
-  gload(rb, nb, 1);
+  // Pipelined loop: buffer loads over this workgroup's contiguous stage
+  // range; an offset past the range returns zeros without a memory access,
+  // so loads beyond the last stage need no branch.
+  constexpr uint32_t kStageBytes = kStageVecs * 16;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(reinterpret_cast<const char*>(a.tiles) + stage_of(0) * int64_t(kStageBytes)), 0,
+      int(uint32_t(n_stages) * kStageBytes), kRsrcWord3);
+  auto gload_b = [&](u32x4 (&r)[kLoadsPerThread], int j) CVS_INLINE {
+    const uint32_t off = uint32_t(j) * kStageBytes + uint32_t(tid) * 16;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i)
+      r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rsrc, off + uint32_t(i * kThreads * 16), 0, kAuxNT));
+  };
+  if constexpr (PIPE) {
+    gload_b(ra, 0);
+    gload_b(rb, 1);
+  } else {
+    gload(ra, na, 0);
+    gload(rb, nb, 1);
+  }
 
   // ---- resident query operands: wave owns queries [qbase + 32*wave, +32) ----
   const int qt = (qbase >> 5) + wave;
@@ -275,6 +300,39 @@ void bf_scan_kernel(ScanArgs a) {
   for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.f;
   asm volatile("" : "+v"(acc0), "+v"(acc1));
 
+  // Appends the passing (distance, row) keys of one finished tile to this
+  // lane's query list.  Rare after the first tiles: each lane reserves slots
+  // for all its passing keys of H rows with one atomic, writes them, and the
+  // atomic's return value tells whether the list needs compacting (no extra
+  // LDS read).  Keys above a threshold lowered by a compaction are dropped
+  // from the later groups.
+  auto commit = [&](const float (&dv)[16], uint32_t pass, int64_t row0) CVS_INLINE {
+    if (__ballot(pass != 0) == 0) return;
+    constexpr int H = L::H;
+#pragma unroll
+    for (int h = 0; h < 16; h += H) {
+      const uint32_t hp = (pass >> h) & ((1u << H) - 1u);
+      const int np = popc(hp);
+      uint32_t slot = 0;
+      if (np) slot = atomicAdd(&s_cnt[qw], uint32_t(np));
+#pragma unroll
+      for (int r = h; r < h + H; ++r) {
+        if (hp & (1u << (r - h))) {
+          const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
+          s_buf[qw * CAP + slot] = (uint64_t(ord_f32(dv[r])) << 32) | row;
+          ++slot;
+        }
+      }
+      const uint64_t over = __ballot(np != 0 && slot > uint32_t(CAP - 2 * H));
+      if (over != 0) {
+        compact_wave(uint32_t(CAP - 2 * H));
+#pragma unroll
+        for (int r = h + H; r < 16; ++r)
+          if (!(dv[r] < thr)) pass &= ~(1u << r);
+      }
+    }
+  };
+
   // Epilogue for one finished 32-row tile: this lane holds query `my_q`
   // against rows row0 + 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
   auto epilogue = [&](const float* dn, int64_t row0, int j) CVS_INLINE {
@@ -296,7 +354,7 @@ void bf_scan_kernel(ScanArgs a) {
         }
       }
     } else {
-      // Fast path: branch-free pass mask over the 16 rows.
+      // Branch-free pass mask over the 16 rows, then the rare append.
       float dv[16];
       uint32_t pass = 0;
 #pragma unroll
@@ -304,35 +362,7 @@ void bf_scan_kernel(ScanArgs a) {
         dv[r] = qn + dn4[r >> 2][r & 3] - 2.0f * (acc0[r] + acc1[r]);
         pass |= (dv[r] < thr ? 1u : 0u) << r;
       }
-      if (__ballot(pass != 0) != 0) {
-        // Rare path: each lane reserves slots for all its passing keys of H
-        // rows with one atomic, writes them, and the atomic's return value
-        // tells whether the list needs compacting (no extra LDS read).
-        constexpr int H = L::H;
-#pragma unroll
-        for (int h = 0; h < 16; h += H) {
-          const uint32_t hp = (pass >> h) & ((1u << H) - 1u);
-          const int np = popc(hp);
-          uint32_t slot = 0;
-          if (np) slot = atomicAdd(&s_cnt[qw], uint32_t(np));
-#pragma unroll
-          for (int r = h; r < h + H; ++r) {
-            if (hp & (1u << (r - h))) {
-              const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
-              s_buf[qw * CAP + slot] = (uint64_t(ord_f32(dv[r])) << 32) | row;
-              ++slot;
-            }
-          }
-          const uint64_t over = __ballot(np != 0 && slot > uint32_t(CAP - 2 * H));
-          if (over != 0) {
-            compact_wave(uint32_t(CAP - 2 * H));
-            // Keys above the lowered threshold are dropped from later groups.
-#pragma unroll
-            for (int r = h + H; r < 16; ++r)
-              if (!(dv[r] < thr)) pass &= ~(1u << r);
-          }
-        }
-      }
+      commit(dv, pass, row0);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.f;
@@ -400,9 +430,118 @@ void bf_scan_kernel(ScanArgs a) {
     __syncthreads();
     compute(par_c, PAR, j);
   };
-  for (int j = 0; j < n_stages; j += 2) {
-    step(std::integral_constant<int, 0>{}, ra, na, j);
-    step(std::integral_constant<int, 1>{}, rb, nb, j + 1);
+  if constexpr (!PIPE) {
+    for (int j = 0; j < n_stages; j += 2) {
+      step(std::integral_constant<int, 0>{}, ra, na, j);
+      step(std::integral_constant<int, 1>{}, rb, nb, j + 1);
+    }
+  } else {
+    // ---- software-pipelined scan (32 or 64 k-steps per tile) ----
+    // Stage j sits in LDS buffer j&1 and register set j&1 (ra / rb).  Per
+    // stage, after one barrier, a single scheduling region interleaves with
+    // the stage's 32 MFMAs: the previous tile's distance/threshold test
+    // (VALU), the LDS store of stage j+1 (its buffer was last read in stage
+    // j-1, which every wave finished before the barrier), the HBM load of
+    // stage j+3 into the registers just stored, and the norms of the current
+    // tile.  Only the rare list append after the MFMAs branches.
+    auto lstore_b = [&](int buf, const u32x4 (&r)[kLoadsPerThread]) CVS_INLINE {
+#pragma unroll
+      for (int i = 0; i < kLoadsPerThread; ++i) s_stage[buf][tid + i * kThreads] = r[i];
+    };
+    // Turns the dot products of a finished tile (in `dv`) into distances and
+    // its pass mask.
+    auto prepare = [&](float (&dv)[16], const f32x4 (&dn)[4]) CVS_INLINE -> uint32_t {
+      uint32_t pass = 0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dv[r] = qn + dn[r >> 2][r & 3] - 2.0f * dv[r];
+        pass |= (dv[r] < thr ? 1u : 0u) << r;
+      }
+      return pass;
+    };
+    float dv[16];
+    f32x4 dn[2][4];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[r] = 0.f;
+
+    // One stage as 32 slots separated by scheduling fences, so that the
+    // interleave is fixed: slot i issues MFMA i, the LDS read of block i+8
+    // (8-deep A ring, two accumulation chains), and one piece of the side
+    // work.  Slot 0 of a tile's first stage first sums the previous tile's
+    // two chains; slots 8-11 of its last stage load this tile's norms ahead
+    // of the stage loads (so waiting for them never waits for newer loads);
+    // slots 12-19 store stage j+1 to LDS and reuse each register for stage
+    // j+3; slots 16-31 of a first stage turn the previous tile's dot
+    // products into distances and pass bits.
+    auto pstep = [&](auto par_c, u32x4 (&r)[kLoadsPerThread], int j) CVS_INLINE {
+      constexpr int PAR = decltype(par_c)::value;
+      constexpr bool FIRST = SPT == 1 || PAR == 0;  // first stage of its tile
+      constexpr bool LAST = SPT == 1 || PAR == 1;   // last stage of its tile
+      constexpr int KOFF = (PAR * kStageBlocks) % KS;
+      constexpr int DN_USE = SPT == 1 ? (PAR ^ 1) : 0;  // norms of the previous tile
+      constexpr int DN_LOAD = SPT == 1 ? PAR : 0;       // norms of this tile
+      constexpr int PF = 8;
+      const int64_t tile = (stage_of(0) + j) / SPT;
+      const u32x4* sb = s_stage[PAR] + lane;
+      const uint32_t off = uint32_t(j + 3) * kStageBytes + uint32_t(tid) * 16;
+      __syncthreads();
+      if constexpr (FIRST) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) dv[q] = acc0[q] + acc1[q];
+      }
+      half8 ring[PF];
+#pragma unroll
+      for (int p = 0; p < PF; ++p) ring[p] = __builtin_bit_cast(half8, sb[p * 64]);
+      uint32_t pass = 0;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kStageBlocks; ++i) {
+        const half8 av = ring[i % PF];
+        if (i + PF < kStageBlocks) ring[i % PF] = __builtin_bit_cast(half8, sb[(i + PF) * 64]);
+        const f32x16 zero = {};
+        if (i & 1)
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + i], (FIRST && i < 2) ? zero : acc1, 0, 0, 0);
+        else
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + i], (FIRST && i < 2) ? zero : acc0, 0, 0, 0);
+        if constexpr (LAST) {
+          if (i >= 8 && i < 12) {
+            const int g = i - 8;
+            dn[DN_LOAD][g] = a.norms[tile * 8 + 2 * g + (lane >> 5)];
+          }
+        }
+        if (i >= 12 && i < 12 + kLoadsPerThread) {
+          const int e = i - 12;
+          s_stage[PAR ^ 1][tid + e * kThreads] = r[e];  // past the last stage: zeros, never read
+          r[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rsrc, off + uint32_t(e * kThreads * 16), 0, kAuxNT));
+        }
+        if constexpr (FIRST) {
+          if (i >= 16) {
+            const int q = i - 16;
+            dv[q] = qn + dn[DN_USE][q >> 2][q & 3] - 2.0f * dv[q];
+            pass |= (dv[q] < thr ? 1u : 0u) << q;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (FIRST) {
+        // No previous tile before the first stage.
+        pass &= 0u - uint32_t(j > 0);
+        commit(dv, pass, (tile - 1) * 32);
+      }
+    };
+    lstore_b(0, ra);
+    gload_b(ra, 2);
+    for (int j = 0; j < n_stages; j += 2) {
+      pstep(std::integral_constant<int, 0>{}, rb, j);
+      pstep(std::integral_constant<int, 1>{}, ra, j + 1);
+    }
+    // Last tile.
+    constexpr int DN_LAST = SPT == 1 ? 1 : 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) dv[q] = acc0[q] + acc1[q];
+    const uint32_t pass = prepare(dv, dn[DN_LAST]);
+    commit(dv, pass, ((stage_of(0) + n_stages) / SPT - 1) * 32);
   }
 
   if (MODE == kModeScan) {
