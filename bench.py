@@ -106,6 +106,24 @@ def read_traffic(name: str):
     return None
 
 
+def calibrate_copy(mib: int) -> int:
+    """Copies `mib` MiB device-to-device with torch's copy_, which the HIP
+    runtime serves with its blit kernel `__amd_rocclr_copyBuffer` (reads mib
+    MiB, writes mib MiB per launch).  rocprofv3's FETCH_SIZE and
+    WRITE_SIZE of that kernel, divided by mib MiB, give the factor by which
+    the counters over- or under-report bytes on this device."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,8 +137,12 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=12, help="queries timed on the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB a few times (PMC byte-counter calibration)")
     args = ap.parse_args()
 
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
               "the N-sharded multi-GPU design is described in DESIGN.md but not built.", file=sys.stderr)
@@ -202,7 +224,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": read_traffic("bf_scan_c2_traffic.txt"),
+            "traffic": read_traffic("bf_scan_n1M_d1024_q100_k10_traffic.txt"),
             "algorithmic_bytes_per_launch": alg_bytes,
             "avg_launch_ms": scan_ms,
             "step_frac": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,

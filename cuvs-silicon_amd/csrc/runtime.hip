@@ -172,7 +172,8 @@ int cvs_context_create(int device, cvs_context** out_ctx) {
     ctx->device = device;
     ctx->compute_units = prop.multiProcessorCount;
     ctx->total_mem = static_cast<int64_t>(prop.totalGlobalMem);
-    ctx->name = prop.name;
+    ctx->name = prop.name[0] ? std::string(prop.name) + " (" + prop.gcnArchName + ")"
+                             : std::string(prop.gcnArchName);
     try {
       CVS_HIP(hipSetDevice(device));
       CVS_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
