@@ -31,6 +31,9 @@ CVS_ERR_UNSUPPORTED = 5
 
 BF_MAX_DIM = 1024
 BF_MAX_K = 48
+CAGRA_MAX_DIM = 1024
+CAGRA_MAX_ITOPK = 256
+CAGRA_MAX_WIDTH = 16
 
 # Every extern "C" symbol declared in include/cvs_hip.h: name -> (restype, argtypes).
 _SIGNATURES = {
@@ -54,6 +57,13 @@ _SIGNATURES = {
     "cvs_dataset_rows": (c_int, [c_void_p, POINTER(c_void_p)]),
     "cvs_bf_search": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "cvs_bf_search_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "cvs_cagra_index_create": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_uint32, c_int,
+                                       c_void_p, c_uint32, POINTER(c_void_p)]),
+    "cvs_cagra_index_destroy": (c_int, [c_void_p]),
+    "cvs_cagra_search": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
+                                 c_void_p, c_void_p]),
+    "cvs_cagra_search_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
+                                       c_void_p, c_void_p, c_void_p]),
 }
 
 _lib = None
@@ -199,6 +209,9 @@ class Context:
     def dataset(self, rows) -> "Dataset":
         return Dataset(self, rows)
 
+    def cagra_index(self, rows, graph, seeds=None) -> "CagraIndex":
+        return CagraIndex(self, rows, graph, seeds)
+
 
 class Dataset:
     """Device-resident dataset (C: cvs_dataset)."""
@@ -244,6 +257,72 @@ class Dataset:
     def bf_search_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray) -> None:
         _check(load().cvs_bf_search_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0], int(k),
                                           nbr.ptr, dist.ptr))
+
+
+class CagraIndex:
+    """Device-resident graph index (C: cvs_cagra_index): rows, neighbour lists
+    and seed (navigation) node ids."""
+
+    def __init__(self, ctx: Context, rows, graph, seeds=None):
+        self.ctx = ctx
+        h = c_void_p()
+        graph_dev = isinstance(graph, DeviceArray)
+        if graph_dev:
+            n_g, degree = graph.shape
+            gptr = graph.ptr
+        else:
+            graph = np.ascontiguousarray(graph, np.uint32)
+            if graph.ndim != 2:
+                raise ValueError("graph must be a 2-D array")
+            n_g, degree = graph.shape
+            gptr = graph.ctypes.data_as(c_void_p)
+        seeds = np.ascontiguousarray(seeds if seeds is not None else np.zeros(0, np.uint32), np.uint32)
+        if isinstance(rows, DeviceArray):
+            n, d = rows.shape
+            rptr, rdev = rows.ptr, 1
+        else:
+            rows = _f32(rows)
+            if rows.ndim != 2:
+                raise ValueError("dataset must be a 2-D array")
+            n, d = rows.shape
+            rptr, rdev = rows.ctypes.data_as(c_void_p), 0
+        if n_g != n:
+            raise ValueError("graph must have one row per dataset row")
+        _check(load().cvs_cagra_index_create(ctx.handle, rptr, n, d, rdev, gptr, degree, 1 if graph_dev else 0,
+                                             seeds.ctypes.data_as(c_void_p) if len(seeds) else None, len(seeds),
+                                             byref(h)))
+        self.handle = h
+        self.n, self.d, self.degree = int(n), int(d), int(degree)
+
+    def close(self) -> None:
+        if self.handle is not None:
+            _check(load().cvs_cagra_index_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def search(self, queries, k: int, itopk_size: int = 64, search_width: int = 1, max_iterations: int = 0):
+        """Graph search of host queries; returns (neighbors u32 [q,k], distances f32 [q,k])."""
+        queries = _f32(queries)
+        if queries.ndim != 2 or queries.shape[1] != self.d:
+            raise ValueError("queries must be (q, d)")
+        q = queries.shape[0]
+        nbr = np.empty((q, k), dtype=np.uint32)
+        dist = np.empty((q, k), dtype=np.float32)
+        _check(load().cvs_cagra_search(self.ctx.handle, self.handle, queries.ctypes.data_as(c_void_p), q, int(k),
+                                       int(itopk_size), int(search_width), int(max_iterations),
+                                       nbr.ctypes.data_as(c_void_p), dist.ctypes.data_as(c_void_p)))
+        return nbr, dist
+
+    def search_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray, itopk_size: int = 64,
+                     search_width: int = 1, max_iterations: int = 0, stats: DeviceArray | None = None) -> None:
+        _check(load().cvs_cagra_search_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0], int(k),
+                                             int(itopk_size), int(search_width), int(max_iterations), nbr.ptr,
+                                             dist.ptr, stats.ptr if stats is not None else None))
 
 
 # ---- synthetic data (lib/libcvs_synth.so) ---------------------------------

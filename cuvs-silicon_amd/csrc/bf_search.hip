@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "cvs_internal.hpp"
+#include "device_util.hpp"
 
 namespace cvs {
 namespace {
@@ -63,22 +64,6 @@ constexpr int kRsrcWord3 = 0x00020000;
 constexpr int kAuxNT = 2;
 
 enum { kModeScan = 0, kModeSample = 1 };
-
-// Order-preserving map float -> uint32 (total order for non-NaN values).
-__device__ __forceinline__ uint32_t ord_f32(float f) {
-  const uint32_t u = __float_as_uint(f + 0.0f);  // -0 -> +0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float unord_f32(uint32_t o) {
-  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
-}
-
-__device__ __forceinline__ int popc(uint64_t m) { return __builtin_popcountll(m); }
-
-// Index of this lane among the set lanes of `mask` below it.
-__device__ __forceinline__ int mbcnt(uint64_t mask) {
-  return __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0));
-}
 
 template <int KS>
 struct Cfg {

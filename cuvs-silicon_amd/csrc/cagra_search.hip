@@ -1,0 +1,449 @@
+// CAGRA graph search for gfx950: one 64-lane wave per query.
+//
+// Replaces the reference's `cagra_beam_search` kernel
+// (shaders/cagra_kernels.metal:28-199, host src/metal_context.mm:918-1111)
+// and its host-side entry-point selection (src/cagra.cpp:128-178).  The
+// reference keeps an unsorted beam in device memory that thread 0 scans
+// serially per neighbour, and a Q x N visited bitfield.  Here everything a
+// query touches between iterations stays on chip:
+//
+//  - itopk list: sorted ascending 64-bit keys in registers, E = itopk/64 per
+//    lane (position i = 64*slot + lane).  A key is
+//        ord(distance) << 32 | id << 1 | expanded
+//    so the order is (distance, id) and marking an entry expanded never
+//    reorders the list.
+//  - visited set: an open-addressing hash of 2^hash_bits ids in LDS, filled to
+//    at most one half.  When the next iteration could overflow that, the
+//    table is cleared and the ids of the itopk list re-inserted: an id that
+//    left the list can be evaluated again, but can never re-enter it (its key
+//    is above the list's current worst), so the list never holds duplicates.
+//  - candidates: processed 64 at a time (one id per lane).  New ids pass the
+//    hash, are compacted into LDS, and their distances are computed by four
+//    16-lane teams (each lane reads 16 bytes at a stride of 256 bytes, so a
+//    row is gathered in coalesced 256-byte segments and one load instruction
+//    serves four rows).  The 64 keys are sorted with a wave bitonic sort and
+//    merged into the itopk list with a bitonic merge.
+//
+// Iteration: pick the first `width` unexpanded entries of the list as
+// parents, mark them, evaluate their neighbours.  Stop when the list holds no
+// unexpanded entry or after max_iterations.  The list is seeded with the
+// index's seed nodes (the reference's navigation nodes, src/cagra.cpp:63-82:
+// the reference starts from the single nearest one; here all of them enter
+// the list, which contains that one), or, without seed nodes, with 64
+// hashed ids led by the reference's fallback (q * 2654435761) mod n
+// (shaders/cagra_kernels.metal:65-67).
+//
+// Distances are exact fp32 sums of squared differences (summation order of
+// four 16-lane partial sums); outputs are sorted by (distance, id) and padded
+// with UINT32_MAX / +inf (src/cagra.cpp:240-251).
+#include <algorithm>
+#include <cmath>
+
+#include "cvs_internal.hpp"
+#include "device_util.hpp"
+
+namespace cvs {
+namespace {
+
+constexpr uint32_t kInvalidId = 0xffffffffu;
+constexpr uint64_t kEmptyKey = ~0ull;
+constexpr int kMaxDv = CVS_CAGRA_MAX_DIM / 64;  // float4 per lane and row
+
+struct SearchArgs {
+  const float4* rows;     // n rows of dq float4, zero-padded
+  const uint32_t* graph;  // n x g
+  const uint32_t* seeds;  // n_seeds seed ids, or null
+  const float* queries;   // q x d fp32
+  uint32_t* out_nbr;      // q x k
+  float* out_dist;        // q x k
+  uint32_t* stats;        // q x 2: distance evaluations, iterations (or null)
+  int64_t d;
+  uint32_t n;
+  int g;
+  int dq;  // float4 per padded row (16 * dv)
+  int dv;  // float4 per lane and row
+  int n_seeds;
+  int k;
+  int itopk;
+  int width;
+  int max_iter;
+  int hash_bits;
+};
+
+// Ascending bitonic sort of one 64-bit key per lane.
+__device__ __forceinline__ uint64_t wave_sort(uint64_t x) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t y = shfl_xor_u64(x, stride);
+      const bool lower = (lane & stride) == 0;
+      const bool asc = (lane & size) == 0;
+      x = (lower == asc) ? (x < y ? x : y) : (x < y ? y : x);
+    }
+  }
+  return x;
+}
+
+// Merges 64 sorted keys `c` (one per lane) into the sorted list `top` of
+// 64*E keys, keeping the 64*E smallest.  min(top[i], c'[N-1-i]) with c'
+// = c padded by empty keys is bitonic; half-cleaners then sort it.
+template <int E>
+__device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
+  const int lane = __lane_id();
+  const uint64_t cr = shfl_u64(c, 63 - lane);
+  top[E - 1] = top[E - 1] < cr ? top[E - 1] : cr;
+#pragma unroll
+  for (int s = E / 2; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if ((e & s) == 0) {
+        const uint64_t lo = top[e] < top[e + s] ? top[e] : top[e + s];
+        const uint64_t hi = top[e] < top[e + s] ? top[e + s] : top[e];
+        top[e] = lo;
+        top[e + s] = hi;
+      }
+    }
+  }
+#pragma unroll
+  for (int stride = 32; stride >= 1; stride >>= 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint64_t y = shfl_xor_u64(top[e], stride);
+      const bool lower = (lane & stride) == 0;
+      top[e] = lower ? (top[e] < y ? top[e] : y) : (top[e] < y ? y : top[e]);
+    }
+  }
+}
+
+template <int E>
+__global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
+  extern __shared__ uint32_t s_mem[];
+  const int H = 1 << a.hash_bits;
+  const uint32_t hmask = uint32_t(H) - 1u;
+  const int hcap = H / 2;
+  uint32_t* s_hash = s_mem;
+  uint32_t* s_ids = s_mem + H;                           // 64 fresh ids
+  float* s_dist = reinterpret_cast<float*>(s_ids + 64);  // their distances
+  uint32_t* s_par = s_ids + 128;                         // parents of this iteration
+
+  const int lane = threadIdx.x;
+  const int64_t qi = blockIdx.x;
+  const int team = lane >> 4, tp = lane & 15;
+
+  for (int i = lane; i < H; i += 64) s_hash[i] = kInvalidId;
+
+  // Query slice of this lane: float4 columns tp + 16 j of the padded row.
+  float4 qv[kMaxDv];
+  const float* qsrc = a.queries + qi * a.d;
+#pragma unroll
+  for (int j = 0; j < kMaxDv; ++j) {
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j < a.dv) {
+      const int64_t c = int64_t(tp + 16 * j) * 4;
+      if (c + 0 < a.d) t.x = qsrc[c + 0];
+      if (c + 1 < a.d) t.y = qsrc[c + 1];
+      if (c + 2 < a.d) t.z = qsrc[c + 2];
+      if (c + 3 < a.d) t.w = qsrc[c + 3];
+    }
+    qv[j] = t;
+  }
+
+  uint64_t top[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) top[e] = kEmptyKey;
+  int count = 0;       // ids in the hash table (wave-uniform)
+  uint32_t evals = 0;  // distance evaluations
+  __syncthreads();
+
+  auto hash_insert = [&](uint32_t id) -> bool {
+    uint32_t h = (id * 0x9E3779B1u) >> (32 - a.hash_bits);
+    for (;;) {
+      const uint32_t old = atomicCAS(&s_hash[h], kInvalidId, id);
+      if (old == kInvalidId) return true;
+      if (old == id) return false;
+      h = (h + 1u) & hmask;
+    }
+  };
+
+  auto reset_hash = [&]() {
+    __syncthreads();
+    for (int i = lane; i < H; i += 64) s_hash[i] = kInvalidId;
+    __syncthreads();
+    count = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const bool v = top[e] != kEmptyKey;
+      if (v) hash_insert(uint32_t(top[e]) >> 1);
+      count += popc(__ballot(v));
+    }
+    __syncthreads();
+  };
+
+  // Evaluates one id per lane (kInvalidId for none) and merges the new ones.
+  auto process = [&](uint32_t id) {
+    const bool fresh = id < a.n && hash_insert(id);
+    const uint64_t m = __ballot(fresh);
+    const int nf = popc(m);
+    if (nf == 0) return;
+    if (fresh) s_ids[mbcnt(m)] = id;
+    count += nf;
+    evals += uint32_t(nf);
+    __syncthreads();
+    for (int r0 = 0; r0 < nf; r0 += 4) {
+      const int r = r0 + team;
+      const bool ok = r < nf;
+      const uint32_t rid = s_ids[ok ? r : 0];
+      const float4* row = a.rows + int64_t(rid) * a.dq + tp;
+      float4 x[kMaxDv];
+#pragma unroll
+      for (int j = 0; j < kMaxDv; ++j)
+        if (j < a.dv) x[j] = row[16 * j];
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxDv; ++j) {
+        if (j < a.dv) {
+          const float dx = qv[j].x - x[j].x, dy = qv[j].y - x[j].y;
+          const float dz = qv[j].z - x[j].z, dw = qv[j].w - x[j].w;
+          acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        }
+      }
+      acc += __shfl_xor(acc, 8);
+      acc += __shfl_xor(acc, 4);
+      acc += __shfl_xor(acc, 2);
+      acc += __shfl_xor(acc, 1);
+      if (ok && tp == 0) s_dist[r] = acc;
+    }
+    __syncthreads();
+    const uint64_t key =
+        lane < nf ? (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1) : kEmptyKey;
+    merge_into<E>(top, wave_sort(key));
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (e * 64 + lane >= a.itopk) top[e] = kEmptyKey;
+    __syncthreads();
+  };
+
+  // Seeds.
+  if (a.n_seeds > 0) {
+    for (int c = 0; c < a.n_seeds; c += 64) {
+      if (count + 64 > hcap) reset_hash();
+      const int i = c + lane;
+      process(i < a.n_seeds ? a.seeds[i] : kInvalidId);
+    }
+  } else {
+    const uint32_t h0 = uint32_t(qi) * 2654435761u;
+    const uint32_t id = (h0 + uint32_t(lane) * 0x9E3779B9u) % a.n;
+    process(uint32_t(lane) < a.n ? id : kInvalidId);
+  }
+
+  // Iterations.
+  int it = 0;
+  for (; it < a.max_iter; ++it) {
+    if (count + a.width * a.g > hcap) reset_hash();
+    int np = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      uint64_t m = __ballot(top[e] != kEmptyKey && (top[e] & 1ull) == 0);
+      while (m != 0 && np < a.width) {
+        const int b = __builtin_ctzll(m);
+        m &= m - 1;
+        if (lane == b) {
+          s_par[np] = uint32_t(top[e]) >> 1;
+          top[e] |= 1ull;
+        }
+        ++np;
+      }
+    }
+    if (np == 0) break;
+    __syncthreads();
+    const int total = np * a.g;
+    for (int c = 0; c < total; c += 64) {
+      const int f = c + lane;
+      uint32_t id = kInvalidId;
+      if (f < total) {
+        const int p = f / a.g;
+        const int j = f - p * a.g;
+        id = a.graph[int64_t(s_par[p]) * a.g + j];
+      }
+      process(id);
+    }
+  }
+
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int pos = e * 64 + lane;
+    if (pos < a.k) {
+      const uint64_t key = top[e];
+      a.out_nbr[qi * a.k + pos] = key == kEmptyKey ? kInvalidId : uint32_t(key) >> 1;
+      a.out_dist[qi * a.k + pos] = key == kEmptyKey ? INFINITY : unord_f32(uint32_t(key >> 32));
+    }
+  }
+  if (a.stats && lane == 0) {
+    a.stats[2 * qi] = evals;
+    a.stats[2 * qi + 1] = uint32_t(it);
+  }
+}
+
+int ceil_log2(int64_t v) {
+  int b = 0;
+  while ((int64_t(1) << b) < v) ++b;
+  return b;
+}
+
+void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const float* queries,
+                         int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                         uint32_t max_iterations, uint32_t* nbr, float* dist, uint32_t* stats) {
+  if (!idx || idx->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
+  if (!queries || !nbr || !dist) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
+  if (q <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count must be positive");
+  if (k <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "k must be positive");
+  if (q > int64_t(INT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "too many queries in one call");
+  const int64_t itopk = std::max<int64_t>(itopk_size ? itopk_size : 128, k);
+  if (itopk > CVS_CAGRA_MAX_ITOPK)
+    fail(CVS_ERR_UNSUPPORTED, "itopk_size (or k) exceeds CVS_CAGRA_MAX_ITOPK");
+  const int64_t width = search_width ? search_width : 1;
+  if (width > CVS_CAGRA_MAX_WIDTH) fail(CVS_ERR_UNSUPPORTED, "search_width exceeds CVS_CAGRA_MAX_WIDTH");
+  const int64_t per_iter = width * int64_t(idx->degree);
+  if (per_iter > 2048) fail(CVS_ERR_UNSUPPORTED, "search_width * graph_degree exceeds 2048");
+  const int e_slots = itopk <= 64 ? 1 : (itopk <= 128 ? 2 : 4);
+  int64_t iters = max_iterations;
+  if (iters == 0) iters = std::max<int64_t>(200, 2 * itopk / width);
+  const int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
+  const size_t lds = (size_t(1) << hash_bits) * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH) * 4;
+
+  SearchArgs a{};
+  a.rows = reinterpret_cast<const float4*>(idx->rows);
+  a.graph = idx->graph;
+  a.seeds = idx->seeds;
+  a.queries = queries;
+  a.out_nbr = nbr;
+  a.out_dist = dist;
+  a.stats = stats;
+  a.d = idx->d;
+  a.n = uint32_t(idx->n);
+  a.g = int(idx->degree);
+  a.dq = int(idx->dpad / 4);
+  a.dv = int(idx->dpad / 64);
+  a.n_seeds = int(idx->n_seeds);
+  a.k = int(k);
+  a.itopk = int(itopk);
+  a.width = int(width);
+  a.max_iter = int(std::min<int64_t>(iters, INT32_MAX));
+  a.hash_bits = hash_bits;
+
+  hipEvent_t t0 = timer_begin(ctx, "cagra_search");
+  const dim3 grid(static_cast<unsigned>(q)), block(64);
+  switch (e_slots) {
+    case 1: hipLaunchKernelGGL(cagra_search_kernel<1>, grid, block, lds, ctx->stream, a); break;
+    case 2: hipLaunchKernelGGL(cagra_search_kernel<2>, grid, block, lds, ctx->stream, a); break;
+    default: hipLaunchKernelGGL(cagra_search_kernel<4>, grid, block, lds, ctx->stream, a); break;
+  }
+  after_launch("cagra_search_kernel");
+  timer_end(ctx, "cagra_search", t0);
+}
+
+}  // namespace
+}  // namespace cvs
+
+using namespace cvs;
+
+extern "C" {
+
+int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
+                           int rows_on_device, const uint32_t* graph, uint32_t degree,
+                           int graph_on_device, const uint32_t* seeds, uint32_t n_seeds,
+                           cvs_cagra_index** out_index) {
+  return guarded([&] {
+    bind(ctx);
+    if (!out_index) fail(CVS_ERR_INVALID_ARGUMENT, "null out_index");
+    *out_index = nullptr;
+    if (!rows || n <= 0 || d <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "dataset must be non-null and non-empty");
+    if (!graph || degree == 0) fail(CVS_ERR_INVALID_ARGUMENT, "graph must be non-null with degree > 0");
+    if (n_seeds > 0 && !seeds) fail(CVS_ERR_INVALID_ARGUMENT, "null seed ids");
+    if (n > int64_t(INT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "graph search needs n < 2^31");
+    if (d > CVS_CAGRA_MAX_DIM) fail(CVS_ERR_UNSUPPORTED, "dimension exceeds CVS_CAGRA_MAX_DIM");
+    if (degree > 1024) fail(CVS_ERR_UNSUPPORTED, "graph degree exceeds 1024");
+    for (uint32_t i = 0; i < n_seeds; ++i)
+      if (seeds[i] >= uint64_t(n)) fail(CVS_ERR_INVALID_ARGUMENT, "seed id out of range");
+    auto* ix = new cvs_cagra_index();
+    ix->ctx = ctx;
+    ix->n = n;
+    ix->d = d;
+    ix->dpad = (d + 63) / 64 * 64;
+    ix->degree = degree;
+    ix->n_seeds = n_seeds;
+    try {
+      const size_t row_bytes = size_t(n) * size_t(ix->dpad) * sizeof(float);
+      CVS_HIP(hipMalloc(&ix->rows, row_bytes));
+      CVS_HIP(hipMalloc(&ix->graph, size_t(n) * degree * sizeof(uint32_t)));
+      if (n_seeds) CVS_HIP(hipMalloc(&ix->seeds, size_t(n_seeds) * sizeof(uint32_t)));
+      if (ix->dpad != d) CVS_HIP(hipMemsetAsync(ix->rows, 0, row_bytes, ctx->stream));
+      CVS_HIP(hipMemcpy2DAsync(ix->rows, size_t(ix->dpad) * sizeof(float), rows, size_t(d) * sizeof(float),
+                               size_t(d) * sizeof(float), size_t(n),
+                               rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream));
+      CVS_HIP(hipMemcpyAsync(ix->graph, graph, size_t(n) * degree * sizeof(uint32_t),
+                             graph_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream));
+      if (n_seeds)
+        CVS_HIP(hipMemcpyAsync(ix->seeds, seeds, size_t(n_seeds) * sizeof(uint32_t), hipMemcpyHostToDevice,
+                               ctx->stream));
+      CVS_HIP(hipStreamSynchronize(ctx->stream));
+    } catch (...) {
+      if (ix->rows) (void)hipFree(ix->rows);
+      if (ix->graph) (void)hipFree(ix->graph);
+      if (ix->seeds) (void)hipFree(ix->seeds);
+      delete ix;
+      throw;
+    }
+    *out_index = ix;
+  });
+}
+
+int cvs_cagra_index_destroy(cvs_cagra_index* index) {
+  return guarded([&] {
+    if (!index) return;
+    bind(index->ctx);
+    (void)hipStreamSynchronize(index->ctx->stream);
+    (void)hipFree(index->rows);
+    (void)hipFree(index->graph);
+    if (index->seeds) (void)hipFree(index->seeds);
+    delete index;
+  });
+}
+
+int cvs_cagra_search_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                           int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                           uint32_t max_iterations, uint32_t* out_neighbors_dev,
+                           float* out_distances_dev, uint32_t* out_stats_dev) {
+  return guarded([&] {
+    bind(ctx);
+    cagra_search_device(ctx, index, queries_dev, q, k, itopk_size, search_width, max_iterations,
+                        out_neighbors_dev, out_distances_dev, out_stats_dev);
+  });
+}
+
+int cvs_cagra_search(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
+                     int64_t k, uint32_t itopk_size, uint32_t search_width, uint32_t max_iterations,
+                     uint32_t* out_neighbors, float* out_distances) {
+  return guarded([&] {
+    bind(ctx);
+    if (!index || !queries || !out_neighbors || !out_distances) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
+    if (index->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
+    if (q <= 0 || k <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count and k must be positive");
+    const size_t qbytes = size_t(q) * size_t(index->d) * sizeof(float);
+    const size_t obytes = size_t(q) * size_t(k) * sizeof(float);
+    ctx->ws_io.reserve(qbytes + 2 * obytes + 256);
+    char* base = ctx->ws_io.as<char>();
+    float* dq = reinterpret_cast<float*>(base);
+    uint32_t* dn = reinterpret_cast<uint32_t*>(base + (qbytes + 127) / 128 * 128);
+    float* dd = reinterpret_cast<float*>(reinterpret_cast<char*>(dn) + (obytes + 127) / 128 * 128);
+    CVS_HIP(hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, ctx->stream));
+    cagra_search_device(ctx, index, dq, q, k, itopk_size, search_width, max_iterations, dn, dd, nullptr);
+    CVS_HIP(hipMemcpyAsync(out_neighbors, dn, obytes, hipMemcpyDeviceToHost, ctx->stream));
+    CVS_HIP(hipMemcpyAsync(out_distances, dd, obytes, hipMemcpyDeviceToHost, ctx->stream));
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+}  // extern "C"

@@ -98,6 +98,18 @@ struct cvs_dataset {
   float* norms = nullptr;         // n_tiles*32 squared norms of fp16 rows (+inf pad)
 };
 
+struct cvs_cagra_index {
+  cvs_context* ctx = nullptr;
+  int64_t n = 0;
+  int64_t d = 0;
+  int64_t dpad = 0;        // row stride in floats (d rounded up to 64)
+  uint32_t degree = 0;
+  uint32_t n_seeds = 0;
+  float* rows = nullptr;     // n x dpad fp32, zero-padded
+  uint32_t* graph = nullptr; // n x degree
+  uint32_t* seeds = nullptr; // n_seeds ids
+};
+
 namespace cvs {
 
 // Makes the context's device current for the calling thread.

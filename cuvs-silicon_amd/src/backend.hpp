@@ -50,6 +50,18 @@ struct DatasetHandle {
   }
 };
 
+// Owning handle of a device graph index.
+struct GraphIndexHandle {
+  cvs_cagra_index* ix = nullptr;
+  GraphIndexHandle() = default;
+  explicit GraphIndexHandle(cvs_cagra_index* i) : ix(i) {}
+  GraphIndexHandle(const GraphIndexHandle&) = delete;
+  GraphIndexHandle& operator=(const GraphIndexHandle&) = delete;
+  ~GraphIndexHandle() {
+    if (ix) cvs_cagra_index_destroy(ix);
+  }
+};
+
 // Uploads host rows (n x d) to the device.
 std::shared_ptr<DatasetHandle> upload_dataset(const float* rows, std::int64_t n, std::int64_t d);
 

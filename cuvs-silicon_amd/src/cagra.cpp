@@ -43,7 +43,8 @@ namespace cuvs::neighbors::cagra {
 
 namespace detail {
 struct device_state {
-  std::shared_ptr<cuvs_silicon_amd::DatasetHandle> dataset;
+  std::shared_ptr<cuvs_silicon_amd::DatasetHandle> dataset;          // exact search
+  std::shared_ptr<cuvs_silicon_amd::GraphIndexHandle> graph_index;   // graph search
 };
 std::shared_ptr<device_state> make_device_state() { return std::make_shared<device_state>(); }
 }  // namespace detail
@@ -94,15 +95,31 @@ void validate_search(const index<float, std::uint32_t>& index,
     throw std::invalid_argument("CAGRA search output shape mismatch");
 }
 
-// Device copy of the index's dataset, uploaded on first use.
-detail::device_state& device_state_of(const index<float, std::uint32_t>& index) {
+// Device copies of the index, uploaded on first use: the brute-force layout
+// for an index without a graph, the graph index (rows, neighbour lists,
+// navigation nodes as seeds) otherwise.
+detail::device_state& device_state_of(const index<float, std::uint32_t>& index, bool graph) {
   auto& cache = index.device_cache();
   if (!cache) cache = detail::make_device_state();
-  if (!cache->dataset) {
-    if (index.dataset().empty())
-      throw std::invalid_argument("CAGRA search requires an index with an attached dataset");
+  if (index.dataset().empty())
+    throw std::invalid_argument("CAGRA search requires an index with an attached dataset");
+  if (!graph && !cache->dataset) {
     cache->dataset =
         cuvs_silicon_amd::upload_dataset(index.dataset().data(), index.rows(), index.cols());
+  }
+  if (graph && !cache->graph_index) {
+    if (index.knn_graph().size() !=
+        static_cast<std::size_t>(index.rows()) * static_cast<std::size_t>(index.graph_degree()))
+      throw std::invalid_argument("CAGRA index graph does not match rows x graph_degree");
+    cvs_cagra_index* ix = nullptr;
+    const auto& nav = index.nav_nodes();
+    counted([&] {
+      return cvs_cagra_index_create(Backend::instance().ctx(), index.dataset().data(), index.rows(),
+                                    index.cols(), 0, index.knn_graph().data(), index.graph_degree(), 0,
+                                    nav.empty() ? nullptr : nav.data(),
+                                    static_cast<std::uint32_t>(nav.size()), &ix);
+    });
+    cache->graph_index = std::make_shared<cuvs_silicon_amd::GraphIndexHandle>(ix);
   }
   return *cache;
 }
@@ -117,17 +134,32 @@ void search<float, std::uint32_t, std::int64_t>(
     raft::device_matrix_view<std::uint32_t, std::int64_t> neighbors,
     raft::device_matrix_view<float, std::int64_t> distances) {
   (void)resources;
-  (void)params;
   validate_search(index, queries, neighbors, distances);
   const std::int64_t q = queries.extent(0);
   const std::int64_t k = neighbors.extent(1);
   if (q == 0) return;
   if (k <= 0) throw std::invalid_argument("CAGRA search requires k > 0");
 
-  detail::device_state& dev = device_state_of(index);
-  cvs_context* ctx = Backend::instance().ctx();
+  // Routing as in the reference (src/cagra.cpp:125-126): graph search when
+  // the index has a graph, exact search otherwise.
   const bool has_graph = index.graph_degree() > 0 && !index.knn_graph().empty();
-  if (has_graph) throw std::runtime_error("CAGRA graph search is not available in this build");
+  detail::device_state& dev = device_state_of(index, has_graph);
+  cvs_context* ctx = Backend::instance().ctx();
+  if (has_graph) {
+    // itopk_size 0 -> 128 and max_iterations 0 -> the kernel's cap follow
+    // src/cagra.cpp:182-185.  The reference's clamp of the beam to 32 for
+    // q <= 4 (:186-189) is not applied: it only lowers recall.
+    auto clamp32 = [](std::uint64_t v) {
+      return static_cast<std::uint32_t>(std::min<std::uint64_t>(v, 0xffffffffu));
+    };
+    counted([&] {
+      return cvs_cagra_search(ctx, dev.graph_index->ix, queries.data_handle(), q, k,
+                              clamp32(params.itopk_size), clamp32(params.search_width),
+                              clamp32(params.max_iterations), neighbors.data_handle(),
+                              distances.data_handle());
+    });
+    return;
+  }
   counted([&] {
     return cvs_bf_search(ctx, dev.dataset->ds, queries.data_handle(), q, k,
                          neighbors.data_handle(), distances.data_handle());

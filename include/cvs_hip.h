@@ -45,10 +45,16 @@ enum cvs_status {
 
 typedef struct cvs_context cvs_context; /* one device + one HIP stream */
 typedef struct cvs_dataset cvs_dataset; /* device-resident dataset (fp32 rows, fp16 tiles, norms) */
+typedef struct cvs_cagra_index cvs_cagra_index; /* device-resident graph index (rows, graph, seeds) */
 
 /* Limits of the fused brute-force kernel (checked by cvs_bf_search*). */
 #define CVS_BF_MAX_DIM 1024
 #define CVS_BF_MAX_K 48
+
+/* Limits of the graph search kernel (checked by cvs_cagra_search*). */
+#define CVS_CAGRA_MAX_DIM 1024
+#define CVS_CAGRA_MAX_ITOPK 256
+#define CVS_CAGRA_MAX_WIDTH 16
 
 /* ---- errors, counters ---------------------------------------------------- */
 
@@ -123,6 +129,41 @@ int cvs_bf_search(cvs_context* ctx, const cvs_dataset* ds,
 int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds,
                         const float* queries_dev, int64_t q, int64_t k,
                         uint32_t* out_neighbors_dev, float* out_distances_dev);
+
+/* ---- CAGRA graph search -------------------------------------------------- */
+
+/* Upload a graph index: n x d fp32 rows, its n x degree uint32 neighbour
+ * lists (entries >= n are ignored) and `n_seeds` seed node ids (the
+ * reference's navigation nodes, src/cagra.cpp:63-82; may be 0).  Replaces the
+ * per-call buffer wraps of MetalContext::search_cagra
+ * (src/metal_context.mm:1045-1054).  `*_on_device` = 1: the pointer is a
+ * device pointer; seeds are always host memory. */
+int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
+                           int rows_on_device, const uint32_t* graph, uint32_t degree,
+                           int graph_on_device, const uint32_t* seeds, uint32_t n_seeds,
+                           cvs_cagra_index** out_index);
+int cvs_cagra_index_destroy(cvs_cagra_index* index);
+
+/* Approximate k-NN by graph search.  Replaces MetalContext::search_cagra
+ * (metal_context.hpp:57-73; src/metal_context.mm:918-1111) and the host
+ * entry-point selection (src/cagra.cpp:128-178).  Parameters keep the
+ * reference's meaning (include/cuvs/neighbors/cagra.hpp:36-50):
+ * itopk_size = internal list length (0 -> 128, raised to k if smaller,
+ * at most CVS_CAGRA_MAX_ITOPK); search_width = parents expanded per
+ * iteration (0 -> 1); max_iterations (0 -> max(200, 2*itopk/width)).
+ * Results sorted by (distance, id), padded with UINT32_MAX / +inf.  Host
+ * pointers, blocking. */
+int cvs_cagra_search(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
+                     int64_t k, uint32_t itopk_size, uint32_t search_width, uint32_t max_iterations,
+                     uint32_t* out_neighbors, float* out_distances);
+
+/* Same, with device pointers; enqueued on the context stream.
+ * `out_stats_dev` (q x 2 uint32, may be null) receives per query the number
+ * of distance evaluations and of iterations (for byte accounting). */
+int cvs_cagra_search_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                           int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                           uint32_t max_iterations, uint32_t* out_neighbors_dev,
+                           float* out_distances_dev, uint32_t* out_stats_dev);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ from __future__ import annotations
 import ctypes
 import os
 import subprocess
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_uint32, c_void_p
+from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_int64, c_uint32, c_uint64, c_void_p
 
 import numpy as np
 
@@ -47,6 +47,17 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.restype = None
             fn.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int]
+        L.oracle_cagra_nav_nodes.restype = c_int64
+        L.oracle_cagra_nav_nodes.argtypes = [c_int64, c_void_p]
+        L.oracle_cagra_entry_points.restype = None
+        L.oracle_cagra_entry_points.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p]
+        L.oracle_cagra_search_policy.restype = None
+        L.oracle_cagra_search_policy.argtypes = [c_uint64, c_uint64, c_int64, POINTER(c_uint32), POINTER(c_uint32)]
+        L.oracle_cagra_search.restype = None
+        L.oracle_cagra_search.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int64,
+                                          c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_void_p, c_int]
+        L.oracle_knn_graph.restype = None
+        L.oracle_knn_graph.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
         _lib = L
     return _lib
 
@@ -122,3 +133,68 @@ def ref_bf_search(base, queries, k: int):
     if rc != 0:
         raise RuntimeError("reference raised an exception")
     return nbr, dist
+
+
+# ---- CAGRA search (oracle/cagra_oracle.c) ----------------------------------
+
+def cagra_nav_nodes(n: int) -> np.ndarray:
+    """Navigation node ids of an n-row index (src/cagra.cpp:65-72)."""
+    m = int(lib().oracle_cagra_nav_nodes(int(n), None))
+    out = np.empty(m, np.uint32)
+    lib().oracle_cagra_nav_nodes(int(n), _p(out))
+    return out
+
+
+def cagra_entry_points(queries, nav_ids, nav_vectors) -> np.ndarray:
+    """Per-query entry node: nearest navigation node (src/cagra.cpp:133-177)."""
+    queries = np.ascontiguousarray(queries, np.float32)
+    nav_ids = np.ascontiguousarray(nav_ids, np.uint32)
+    nav_vectors = np.ascontiguousarray(nav_vectors, np.float32)
+    q, d = queries.shape
+    out = np.empty(q, np.uint32)
+    lib().oracle_cagra_entry_points(_p(queries), q, d, _p(nav_ids), _p(nav_vectors), len(nav_ids), _p(out))
+    return out
+
+
+def cagra_search_policy(itopk_size: int, max_iterations: int, q: int):
+    """(beam, iterations) chosen by the reference (src/cagra.cpp:182-189)."""
+    b, it = c_uint32(0), c_uint32(0)
+    lib().oracle_cagra_search_policy(int(itopk_size), int(max_iterations), int(q), byref(b), byref(it))
+    return b.value, it.value
+
+
+def cagra_search(base, graph, queries, k: int, beam: int, max_iter: int, entry=None, threads: int = 1):
+    """The reference's beam search (shaders/cagra_kernels.metal:28-199)."""
+    base = np.ascontiguousarray(base, np.float32)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    queries = np.ascontiguousarray(queries, np.float32)
+    n, d = base.shape
+    q = queries.shape[0]
+    g = graph.shape[1] if graph.ndim == 2 else 0
+    ent = None if entry is None else np.ascontiguousarray(entry, np.uint32)
+    nbr = np.empty((q, k), np.uint32)
+    dist = np.empty((q, k), np.float32)
+    lib().oracle_cagra_search(_p(base), n, d, _p(graph), g, _p(queries), q, None if ent is None else _p(ent),
+                              int(k), int(beam), int(max_iter), _p(nbr), _p(dist), int(threads))
+    return nbr, dist
+
+
+def cagra_reference_search(base, graph, nav_ids, queries, k: int, itopk_size: int = 64,
+                           max_iterations: int = 0, threads: int = 1):
+    """The reference's whole search route for an index with a graph: entry
+    points from the navigation nodes, the beam/iteration policy, beam search
+    (src/cagra.cpp:128-196)."""
+    base = np.ascontiguousarray(base, np.float32)
+    nav_ids = np.ascontiguousarray(nav_ids, np.uint32)
+    entry = cagra_entry_points(queries, nav_ids, base[nav_ids]) if len(nav_ids) else None
+    beam, iters = cagra_search_policy(itopk_size, max_iterations, len(queries))
+    return cagra_search(base, graph, queries, k, beam, iters, entry, threads)
+
+
+def knn_graph(base, g: int, threads: int = 1) -> np.ndarray:
+    """Exact degree-g kNN graph without self edges."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    out = np.empty((n, g), np.uint32)
+    lib().oracle_knn_graph(_p(base), n, d, int(g), _p(out), int(threads))
+    return out

@@ -36,6 +36,51 @@ void oracle_bf_exact(const float* base, int64_t n, int64_t d, const float* queri
 void oracle_bf_fp64(const float* base, int64_t n, int64_t d, const float* queries, int64_t q,
                     int64_t k, uint32_t* out_nbr, double* out_dist, int threads);
 
+
+/* ---- CAGRA search (oracle/cagra_oracle.c) ------------------------------- */
+
+/* Navigation nodes of a built index (src/cagra.cpp:65-72): returns
+ * n_nav = min(200, floor(sqrt(n))) and, if out_ids is non-null, writes
+ * out_ids[i] = (uint32)(i * (n / n_nav)).  Pinned: closed form at n = 1, 10,
+ * 40,000 and 100,000 (tests/test_oracle_cagra.py). */
+int64_t oracle_cagra_nav_nodes(int64_t n, uint32_t* out_ids);
+
+/* Per-query entry point (src/cagra.cpp:133-177): argmin over the navigation
+ * vectors of |q|^2 - 2 q.v + |v|^2 in fp32 (first minimum wins; cross terms
+ * as sequential dot products where the reference uses cblas_sgemm).
+ * Pinned: equals the exact nearest navigation node on well-separated data,
+ * and the first-minimum tie rule on duplicated vectors. */
+void oracle_cagra_entry_points(const float* queries, int64_t q, int64_t d, const uint32_t* nav_ids,
+                               const float* nav_vectors, int64_t n_nav, uint32_t* out_entry);
+
+/* Beam size and iteration cap (src/cagra.cpp:182-189): itopk 0 -> 128,
+ * max_iterations 0 -> 200, and for q <= 4 the beam is clamped to 32.
+ * Pinned: every branch against its closed form. */
+void oracle_cagra_search_policy(uint64_t itopk_size, uint64_t max_iterations, int64_t q,
+                                uint32_t* out_beam, uint32_t* out_iters);
+
+/* The reference's beam search (shaders/cagra_kernels.metal:28-199): seed =
+ * entry[q] if < n else (q * 2654435761) mod n; per iteration expand the
+ * unexpanded entry of smallest distance (expanded entries hold -d-1),
+ * compute its g neighbours' distances, and for each unvisited one replace
+ * the first entry of largest |d| if closer; output sorted by (d, id), padded
+ * with UINT32_MAX / +inf.  `entry` may be null.  Pinned: on a complete graph
+ * it returns the exact k-NN (FAISS smoke database with g = n - 1); a
+ * hand-traced path graph; its invariants (sorted, unique, in range, distances
+ * equal to the exact fp32 distances of the returned ids); and a planted
+ * mistake (expanding the worst entry) fails them. */
+void oracle_cagra_search(const float* base, int64_t n, int64_t d, const uint32_t* graph,
+                         uint32_t g, const float* queries, int64_t q, const uint32_t* entry,
+                         int64_t k, uint32_t beam, uint32_t max_iter, uint32_t* out_nbr,
+                         float* out_dist, int threads);
+
+/* Exact degree-g kNN graph without self edges, rows sorted by (d, id),
+ * missing entries UINT32_MAX (the reference's build for n <= 50,000 is exact
+ * all-pairs seeding, src/metal_context.mm:324-349).  Pinned: rows equal
+ * oracle_bf_exact's k = g + 1 results with the row itself removed. */
+void oracle_knn_graph(const float* base, int64_t n, int64_t d, uint32_t g, uint32_t* out_graph,
+                      int threads);
+
 #ifdef __cplusplus
 }
 #endif
