@@ -66,6 +66,24 @@ _SIGNATURES = {
                                        c_void_p, c_void_p, c_void_p]),
 }
 
+class BuildStats(ctypes.Structure):
+    """cvs_build_stats (include/cvs_hip.h)."""
+    _fields_ = [("iterations", c_uint32), ("intermediate_degree", c_uint32), ("graph_degree", c_uint32),
+                ("final_update_rate", c_double), ("seconds_seed", c_double), ("seconds_descent", c_double),
+                ("seconds_prune", c_double), ("seconds_total", c_double), ("join_ms", c_double),
+                ("join_bytes", c_double), ("join_members", c_uint64), ("updates_emitted", c_uint64),
+                ("updates_kept", c_uint64), ("insertions", c_uint64)]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_SIGNATURES["cvs_cagra_build"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_uint32, c_uint32,
+                                          c_float, c_uint64, c_void_p, c_int, POINTER(BuildStats)])
+
+# The bucketing permutation seed of the reference (src/metal_context.mm:803).
+DEFAULT_BUILD_SEED = 0xFEDCBA9876543210
+
 _lib = None
 
 
@@ -211,6 +229,31 @@ class Context:
 
     def cagra_index(self, rows, graph, seeds=None) -> "CagraIndex":
         return CagraIndex(self, rows, graph, seeds)
+
+    def cagra_build(self, rows, intermediate_degree: int = 128, graph_degree: int = 64, max_iterations: int = 20,
+                    termination_threshold: float = 0.001, seed: int = DEFAULT_BUILD_SEED, out: "DeviceArray" = None):
+        """GPU graph build.  Returns (graph, stats): graph is a host uint32
+        array (n, g), or `out` (a device array of that shape) when given."""
+        st = BuildStats()
+        if isinstance(rows, DeviceArray):
+            n, d = rows.shape
+            rptr, rdev = rows.ptr, 1
+        else:
+            rows = _f32(rows)
+            n, d = rows.shape
+            rptr, rdev = rows.ctypes.data_as(c_void_p), 0
+        g = min(int(graph_degree), max(int(intermediate_degree), int(graph_degree)), n - 1)
+        if out is not None:
+            if out.shape != (n, g) or out.dtype != np.uint32:
+                raise ValueError(f"out must be a uint32 device array of shape {(n, g)}")
+            gptr, gdev, host = out.ptr, 1, None
+        else:
+            host = np.empty((n, max(g, 1)), np.uint32)
+            gptr, gdev = host.ctypes.data_as(c_void_p), 0
+        _check(load().cvs_cagra_build(self.handle, rptr, n, d, rdev, int(intermediate_degree), int(graph_degree),
+                                      int(max_iterations), float(termination_threshold), int(seed), gptr, gdev,
+                                      byref(st)))
+        return (out if out is not None else host), st.as_dict()
 
 
 class Dataset:

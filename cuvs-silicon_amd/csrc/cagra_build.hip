@@ -1,0 +1,828 @@
+// CAGRA graph build for gfx950: random bucketing -> nn-descent -> pruning.
+//
+// Replaces the reference's build_knn_graph (src/metal_context.mm:289-914):
+// CPU IVF k-means + per-cluster BLAS seeding, a `random_bucketing` kernel
+// (shaders/cagra_kernels.metal:403-462) and a racy `nn_descent` kernel
+// (:334-395) that recomputes full 2-hop distance sets per node.  Here every
+// phase runs on the GPU and no update is lost to a race:
+//
+//  1. convert   fp32 rows -> fp16 rows (row stride dp = d rounded up to 64)
+//               + fp32 squared norms of the fp16-rounded rows.
+//  2. bucket    rows are split into buckets of 256 consecutive entries of a
+//               random permutation (the reference's LCG Fisher-Yates,
+//               src/metal_context.mm:802-810).  One workgroup per bucket forms
+//               the 256 x 256 Gram matrix on v_mfma_f32_32x32x16_f16 (fp32
+//               accumulate) over LDS-staged 64-dimension chunks and gives each
+//               row the `kd` nearest of its 255 bucket mates: the initial
+//               degree-kd ("intermediate degree") list.
+//  3. nn-descent, per iteration:
+//     sample    per node, up to 16 "new" (never joined) and 16 "old"
+//               neighbours; new ones are marked old.  Each sampled edge
+//               u -> v also appends u to v's reverse new/old list (16 each).
+//     join      per node, its sampled forward + reverse neighbours (at most
+//               64 rows) are gathered into LDS chunk by chunk and their 64 x 64
+//               Gram matrix is formed on MFMA: the local join.  For every
+//               member, the 8 best partners (at least one of the pair new)
+//               that beat the member's current worst neighbour are appended
+//               to the member's update bin.
+//     apply     per node, the bin is deduplicated, filtered against the
+//               list, sorted and merged into the sorted list (wave bitonic
+//               merge); inserted entries are marked new and counted.
+//     The loop stops after max_iterations or when the number of insertions
+//     falls below termination_threshold * n * kd.
+//  4. prune     CAGRA's rank-based detour count (Ootomo et al., 2023): an
+//               edge u -> v_j (rank j) is detourable via v_i if rank
+//               max(i, rank of v_j in v_i's list) < j.  Each node keeps the g
+//               edges of fewest detours (ties by rank), then reverse edges
+//               are added: the final list is the closest g/2 kept edges, then
+//               up to g/2 reverse edges, then the remaining kept edges.
+//
+// Lists are sorted 64-bit keys ord(distance) << 32 | id << 1 | new, so the
+// order is (distance, id) and the new flag never reorders a list.  Distances
+// in the build are fp16-input expanded-form estimates; they only rank
+// candidates (the search computes exact fp32 distances).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <numeric>
+#include <vector>
+
+#include "cvs_internal.hpp"
+#include "device_util.hpp"
+
+namespace cvs {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint64_t kEmpty = ~0ull;
+constexpr uint32_t kInvalid = 0xffffffffu;
+constexpr int kChunkBytes = 128;  // 64 fp16 dimensions per staged chunk
+constexpr int kStageStride = 144; // bytes per staged row (128 + 16 against bank conflicts)
+constexpr int kSample = 16;       // sampled forward/reverse new/old neighbours
+constexpr int kJoinM = 4 * kSample;
+constexpr int kBin = 64;          // update bin capacity per node
+constexpr int kEmit = 8;          // partners emitted per member and join
+constexpr int kBucket = 256;
+constexpr int kBucketRounds = 4;   // random bucketings merged into the initial lists
+constexpr int kBucketEmit = 32;    // mates per row merged by the rounds after the first
+constexpr int kMaxKd = 256;       // intermediate degree limit (4 keys per lane)
+
+// ---------------------------------------------------------------------------
+// Wave-level sorting of 64*E keys (position i = 64*slot + lane).
+// ---------------------------------------------------------------------------
+template <int E>
+__device__ __forceinline__ void wave_sort_e(uint64_t (&v)[E]) {
+  const int lane = __lane_id();
+  constexpr int N = 64 * E;
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int s = stride / 64;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          if ((e & s) == 0) {
+            const bool asc = ((e * 64) & size) == 0;
+            const uint64_t a = v[e], b = v[e + s];
+            const bool sw = asc ? (b < a) : (a < b);
+            v[e] = sw ? b : a;
+            v[e + s] = sw ? a : b;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const uint64_t y = shfl_xor_u64(v[e], stride);
+          const bool lower = (lane & stride) == 0;
+          const bool asc = ((e * 64 + lane) & size) == 0;
+          v[e] = (lower == asc) ? (v[e] < y ? v[e] : y) : (v[e] < y ? y : v[e]);
+        }
+      }
+    }
+  }
+}
+
+// Merges 64 sorted keys (one per lane) into the sorted list v of 64*E keys.
+template <int E>
+__device__ __forceinline__ void wave_merge(uint64_t (&v)[E], uint64_t c) {
+  const int lane = __lane_id();
+  const uint64_t cr = shfl_u64(c, 63 - lane);
+  v[E - 1] = v[E - 1] < cr ? v[E - 1] : cr;
+#pragma unroll
+  for (int s = E / 2; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if ((e & s) == 0) {
+        const uint64_t lo = v[e] < v[e + s] ? v[e] : v[e + s];
+        const uint64_t hi = v[e] < v[e + s] ? v[e + s] : v[e];
+        v[e] = lo;
+        v[e + s] = hi;
+      }
+    }
+  }
+#pragma unroll
+  for (int stride = 32; stride >= 1; stride >>= 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint64_t y = shfl_xor_u64(v[e], stride);
+      const bool lower = (lane & stride) == 0;
+      v[e] = lower ? (v[e] < y ? v[e] : y) : (v[e] < y ? y : v[e]);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t key_id(uint64_t k) { return uint32_t(k) >> 1; }
+
+// ---------------------------------------------------------------------------
+// Gram tiles of a set of fp16 rows.  The member rows s_ids[0..M) are staged
+// 64 dimensions at a time (M x 128 B, rows 144 B apart) and each wave
+// accumulates NT 32x32 tiles: tile t = rows 32*rt[t].., columns 32*ct[t]..
+// Loads of chunk c+1 are in flight while chunk c is multiplied.
+// ---------------------------------------------------------------------------
+template <int M, int NT>
+__device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t row_bytes, int n_chunks,
+                                           const uint32_t* s_ids, char* s_stage, const int (&rt)[NT],
+                                           const int (&ct)[NT], f32x16 (&acc)[NT]) {
+  constexpr int LPT = M * 8 / 256;  // 16-byte loads per thread and chunk
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const char* src[LPT];
+  int dst[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int idx = tid + 256 * i;
+    const int r = idx >> 3, seg = idx & 7;
+    src[i] = x16 + int64_t(s_ids[r]) * row_bytes + seg * 16;
+    dst[i] = r * kStageStride + seg * 16;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
+  u32x4 reg[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) reg[i] = *reinterpret_cast<const u32x4*>(src[i]);
+  for (int c = 0; c < n_chunks; ++c) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[i];
+    __syncthreads();
+    if (c + 1 < n_chunks) {
+#pragma unroll
+      for (int i = 0; i < LPT; ++i)
+        reg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(c + 1) * kChunkBytes);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int koff = s * 32 + 16 * (lane >> 5);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const half8 a = *reinterpret_cast<const half8*>(s_stage + (32 * rt[t] + (lane & 31)) * kStageStride + koff);
+        const half8 b = *reinterpret_cast<const half8*>(s_stage + (32 * ct[t] + (lane & 31)) * kStageStride + koff);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// fp32 rows -> fp16 rows (stride dp) + squared norms of the fp16-rounded rows.
+// One wave per row.
+__global__ __launch_bounds__(256) void to_half_rows_kernel(const float* __restrict__ rows, int64_t n, int64_t d,
+                                                           int64_t dp, _Float16* __restrict__ out,
+                                                           float* __restrict__ norms) {
+  const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n) return;
+  const float* src = rows + r * d;
+  _Float16* dst = out + r * dp;
+  float acc = 0.f;
+  for (int64_t c = lane; c < dp; c += 64) {
+    const _Float16 h = static_cast<_Float16>(c < d ? src[c] : 0.f);
+    dst[c] = h;
+    const float hv = static_cast<float>(h);
+    acc += hv * hv;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) norms[r] = acc;
+}
+
+struct BuildArgs {
+  const char* x16;       // n x dp fp16
+  const float* norms;    // n
+  int64_t row_bytes;     // dp * 2
+  int n_chunks;          // dp / 64
+  uint32_t n;
+  int kd;                // list length (intermediate degree, <= n - 1)
+  int kp;                // list stride (kd rounded up to 64)
+  uint64_t* lists;       // n x kp keys
+  uint32_t* fwd;         // n x 2*kSample: new ids, then old ids
+  uint32_t* fwd_cnt;     // n x 2
+  uint32_t* rev;         // n x 2*kSample
+  uint32_t* rev_cnt;     // n x 2
+  uint64_t* bins;        // n x kBin
+  uint32_t* bin_cnt;     // n
+  unsigned long long* counters;  // insertions, join members, updates emitted, bin entries kept
+};
+
+// One workgroup per bucket of up to 256 permuted rows.  First round
+// (to_bins = 0): each row's list becomes its kd nearest bucket mates.  Later
+// rounds (to_bins = 1): each row's kBucketEmit nearest mates go to its
+// update bin, for the apply kernel to merge into the list.
+__global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t* __restrict__ perm, int to_bins) {
+  __shared__ __attribute__((aligned(16))) char s_stage[kBucket * kStageStride];
+  __shared__ float s_dist[64 * 257];  // one 64-row block of the bucket's distances
+  __shared__ uint32_t s_ids[kBucket];
+  __shared__ float s_norm[kBucket];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t start = int64_t(blockIdx.x) * kBucket;
+  const int mb = int(std::min<int64_t>(kBucket, int64_t(a.n) - start));
+  {
+    const uint32_t id = perm[start + (tid < mb ? tid : 0)];
+    s_ids[tid] = id;
+    s_norm[tid] = a.norms[id];
+  }
+  __syncthreads();
+  for (int rb = 0; rb < 4; ++rb) {
+    if (64 * rb >= mb) break;
+    const int rt[4] = {2 * rb, 2 * rb, 2 * rb + 1, 2 * rb + 1};
+    const int ct[4] = {2 * wave, 2 * wave + 1, 2 * wave, 2 * wave + 1};
+    f32x16 acc[4];
+    gram_tiles<kBucket, 4>(a.x16, a.row_bytes, a.n_chunks, s_ids, s_stage, rt, ct, acc);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * rt[t] + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int col = 32 * ct[t] + (lane & 31);
+        s_dist[(row - 64 * rb) * 257 + col] = s_norm[row] + s_norm[col] - 2.0f * acc[t][e];
+      }
+    }
+    __syncthreads();
+    for (int i = 0; i < 16; ++i) {
+      const int row = 64 * rb + 16 * wave + i;
+      if (row >= mb) break;
+      uint64_t v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = e * 64 + lane;
+        v[e] = (c < mb && c != row)
+                   ? (uint64_t(ord_f32(s_dist[(row - 64 * rb) * 257 + c])) << 32) | (uint64_t(s_ids[c]) << 1) | 1ull
+                   : kEmpty;
+      }
+      wave_sort_e<4>(v);
+      const int64_t u = s_ids[row];
+      if (to_bins) {
+        if (lane < kBucketEmit) a.bins[u * kBin + lane] = v[0];
+        if (lane == 0) a.bin_cnt[u] = uint32_t(min(kBucketEmit, mb - 1));
+      } else {
+        uint64_t* dst = a.lists + u * a.kp;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = e * 64 + lane;
+          if (p < a.kp) dst[p] = p < a.kd ? v[e] : kEmpty;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Per node (one wave): sample new/old neighbours, mark sampled new ones old,
+// append reverse edges.
+template <int E>
+__global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t u = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (u >= a.n) return;
+  uint64_t* lst = a.lists + u * a.kp;
+  uint32_t* fw = a.fwd + u * 2 * kSample;
+  int n_new = 0, n_old = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    const uint64_t key = p < a.kd ? lst[p] : kEmpty;
+    const bool valid = key != kEmpty;
+    const bool is_new = valid && (key & 1ull);
+    const uint64_t mn = __ballot(is_new), mo = __ballot(valid && !is_new);
+    const int rn = mbcnt(mn), ro = mbcnt(mo);
+    const uint32_t id = key_id(key);
+    if (is_new && n_new + rn < kSample) {
+      fw[n_new + rn] = id;
+      lst[p] = key & ~1ull;
+      const uint32_t slot = atomicAdd(&a.rev_cnt[2 * int64_t(id)], 1u);
+      if (slot < kSample) a.rev[int64_t(id) * 2 * kSample + slot] = uint32_t(u);
+    }
+    if (valid && !is_new && n_old + ro < kSample) {
+      fw[kSample + n_old + ro] = id;
+      const uint32_t slot = atomicAdd(&a.rev_cnt[2 * int64_t(id) + 1], 1u);
+      if (slot < kSample) a.rev[int64_t(id) * 2 * kSample + kSample + slot] = uint32_t(u);
+    }
+    n_new = std::min(kSample, n_new + popc(mn));
+    n_old = std::min(kSample, n_old + popc(mo));
+  }
+  if (lane == 0) {
+    a.fwd_cnt[2 * u] = uint32_t(n_new);
+    a.fwd_cnt[2 * u + 1] = uint32_t(n_old);
+  }
+}
+
+// Per node (one workgroup): local join of its sampled neighbourhood.
+__global__ __launch_bounds__(256) void join_kernel(BuildArgs a) {
+  __shared__ __attribute__((aligned(16))) char s_stage[kJoinM * kStageStride];
+  __shared__ float s_dist[kJoinM * (kJoinM + 1)];
+  __shared__ uint32_t s_ids[kJoinM];
+  __shared__ float s_norm[kJoinM];
+  __shared__ uint64_t s_worst[kJoinM];
+  __shared__ int s_m[2];  // members, new members
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t u = blockIdx.x;
+  if (tid == 0) {
+    const uint32_t fn = a.fwd_cnt[2 * u], fo = a.fwd_cnt[2 * u + 1];
+    const uint32_t rn = min(a.rev_cnt[2 * u], uint32_t(kSample));
+    const uint32_t ro = min(a.rev_cnt[2 * u + 1], uint32_t(kSample));
+    const uint32_t* fw = a.fwd + u * 2 * kSample;
+    const uint32_t* rv = a.rev + u * 2 * kSample;
+    int m = 0;
+    for (uint32_t i = 0; i < fn; ++i) s_ids[m++] = fw[i];
+    for (uint32_t i = 0; i < rn; ++i) s_ids[m++] = rv[i];
+    const int mnew = m;
+    for (uint32_t i = 0; i < fo; ++i) s_ids[m++] = fw[kSample + i];
+    for (uint32_t i = 0; i < ro; ++i) s_ids[m++] = rv[kSample + i];
+    s_m[0] = m;
+    s_m[1] = mnew;
+  }
+  __syncthreads();
+  const int m = s_m[0], mnew = s_m[1];
+  if (mnew == 0 || m < 2) return;
+  if (tid < kJoinM) {
+    const uint32_t id = s_ids[tid < m ? tid : 0];
+    if (tid >= m) s_ids[tid] = id;
+    s_norm[tid] = a.norms[id];
+    s_worst[tid] = a.lists[int64_t(id) * a.kp + a.kd - 1] | 1ull;
+  }
+  if (tid == 0) atomicAdd(&a.counters[1], (unsigned long long)m);
+  __syncthreads();
+  const int rt[1] = {wave >> 1};
+  const int ct[1] = {wave & 1};
+  f32x16 acc[1];
+  gram_tiles<kJoinM, 1>(a.x16, a.row_bytes, a.n_chunks, s_ids, s_stage, rt, ct, acc);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = 32 * rt[0] + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+    const int col = 32 * ct[0] + (lane & 31);
+    s_dist[row * (kJoinM + 1) + col] = s_norm[row] + s_norm[col] - 2.0f * acc[0][e];
+  }
+  __syncthreads();
+  for (int i = 16 * wave; i < 16 * wave + 16 && i < m; ++i) {
+    const uint32_t xi = s_ids[i];
+    const int j = lane;
+    const bool valid = j < m && (i < mnew || j < mnew) && s_ids[j] != xi;
+    const uint64_t key =
+        valid ? (uint64_t(ord_f32(s_dist[i * (kJoinM + 1) + j])) << 32) | (uint64_t(s_ids[j]) << 1) | 1ull : kEmpty;
+    const bool pass = valid && key < s_worst[i];
+    const uint64_t pm = __ballot(pass);
+    if (pm == 0) continue;
+    int cnt = popc(pm);
+    uint64_t k2 = pass ? key : kEmpty;
+    int rank = mbcnt(pm);
+    if (cnt > kEmit) {
+      uint64_t v1[1] = {k2};
+      wave_sort_e<1>(v1);
+      k2 = v1[0];
+      rank = lane;
+      cnt = kEmit;
+    }
+    uint32_t base = 0;
+    if (lane == 0) {
+      base = atomicAdd(&a.bin_cnt[xi], uint32_t(cnt));
+      atomicAdd(&a.counters[2], (unsigned long long)cnt);
+    }
+    base = uint32_t(__shfl(int(base), 0));
+    if (k2 != kEmpty && rank < cnt && base + rank < kBin) a.bins[int64_t(xi) * kBin + base + rank] = k2;
+  }
+}
+
+// Per node (one wave): merge the update bin into the list.
+template <int E>
+__global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
+  __shared__ uint32_t s_hash[4][512];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t u = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (u >= a.n) return;
+  const uint32_t cnt = a.bin_cnt[u];
+  if (cnt == 0) return;
+  const int c = int(min(cnt, uint32_t(kBin)));
+  uint32_t* h = s_hash[wave];
+  for (int i = lane; i < 512; i += 64) h[i] = kInvalid;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  uint64_t* lst = a.lists + u * a.kp;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    v[e] = p < a.kd ? lst[p] : kEmpty;
+  }
+  auto insert = [&](uint32_t id) -> bool {  // true if newly inserted
+    uint32_t s = (id * 0x9E3779B1u) >> 23;
+    for (;;) {
+      const uint32_t old = atomicCAS(&h[s], kInvalid, id);
+      if (old == kInvalid) return true;
+      if (old == id) return false;
+      s = (s + 1u) & 511u;
+    }
+  };
+  auto contains = [&](uint32_t id) -> bool {
+    uint32_t s = (id * 0x9E3779B1u) >> 23;
+    for (;;) {
+      const uint32_t cur = h[s];
+      if (cur == kInvalid) return false;
+      if (cur == id) return true;
+      s = (s + 1u) & 511u;
+    }
+  };
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (v[e] != kEmpty) insert(key_id(v[e]));
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  // Bin: keep the closest copy of each id that is not in the list yet.
+  uint64_t b = lane < c ? a.bins[u * kBin + lane] : kEmpty;
+  uint64_t by_id[1] = {b == kEmpty ? kEmpty : (uint64_t(key_id(b)) << 32) | (b >> 32)};
+  wave_sort_e<1>(by_id);
+  const uint64_t prev = shfl_u64(by_id[0], lane > 0 ? lane - 1 : 0);
+  const uint32_t bid = uint32_t(by_id[0] >> 32);
+  const bool keep = by_id[0] != kEmpty && (lane == 0 || uint32_t(prev >> 32) != bid) && !contains(bid);
+  uint64_t nk[1] = {keep ? ((by_id[0] & 0xffffffffull) << 32) | (uint64_t(bid) << 1) | 1ull : kEmpty};
+  const int n_keep = popc(__ballot(keep));
+  wave_sort_e<1>(nk);
+  wave_merge<E>(v, nk[0]);
+  int inserted = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    if (p >= a.kd) v[e] = kEmpty;
+    const bool ins = v[e] != kEmpty && !contains(key_id(v[e]));
+    inserted += popc(__ballot(ins));
+    if (p < a.kd) lst[p] = v[e];
+  }
+  if (lane == 0) {
+    a.bin_cnt[u] = 0;
+    if (inserted) atomicAdd(&a.counters[0], (unsigned long long)inserted);
+    if (n_keep) atomicAdd(&a.counters[3], (unsigned long long)n_keep);
+  }
+}
+
+// Lists -> id rows (n x kd) for pruning.
+__global__ __launch_bounds__(256) void list_ids_kernel(const uint64_t* __restrict__ lists, int64_t n, int kd, int kp,
+                                                       uint32_t* __restrict__ ids) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n * kd) return;
+  const int64_t r = i / kd, j = i - r * kd;
+  const uint64_t k = lists[r * kp + j];
+  ids[i] = k == kEmpty ? kInvalid : key_id(k);
+}
+
+// Per node (one wave): detour counts, keep g edges, append reverse edges.
+template <int E>
+__global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__ ids, int64_t n, int kd, int g,
+                                                    uint32_t* __restrict__ kept, uint32_t* __restrict__ rev,
+                                                    uint32_t* __restrict__ rev_cnt) {
+  __shared__ uint32_t s_hkey[4][512];
+  __shared__ uint32_t s_hval[4][512];
+  __shared__ uint32_t s_det[4][kMaxKd];
+  __shared__ uint32_t s_nb[4][kMaxKd];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t u = int64_t(blockIdx.x) * 4 + wave;
+  if (u >= n) return;
+  uint32_t* hk = s_hkey[wave];
+  uint32_t* hv = s_hval[wave];
+  for (int i = lane; i < 512; i += 64) hk[i] = kInvalid;
+  for (int i = lane; i < kMaxKd; i += 64) s_det[wave][i] = 0;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  const uint32_t* row = ids + u * kd;
+  int valid_n = 0;
+  for (int j = lane; j < kd; j += 64) {
+    const uint32_t w = row[j];
+    s_nb[wave][j] = w;
+    if (w != kInvalid) {
+      uint32_t s = (w * 0x9E3779B1u) >> 23;
+      while (atomicCAS(&hk[s], kInvalid, w) != kInvalid) s = (s + 1u) & 511u;
+      hv[s] = uint32_t(j);
+    }
+  }
+  for (int j = 0; j < kd; j += 64) valid_n += popc(__ballot(j + lane < kd && row[j + lane] != kInvalid));
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  // Edge u -> v_j is detourable via v_i when max(i, rank of v_j in v_i's list) < j.
+  for (int i = 0; i < valid_n; ++i) {
+    const uint32_t vi = s_nb[wave][i];
+    const uint32_t* li = ids + int64_t(vi) * kd;
+    for (int p = lane; p < kd; p += 64) {
+      const uint32_t w = li[p];
+      if (w == kInvalid) continue;
+      uint32_t s = (w * 0x9E3779B1u) >> 23;
+      for (;;) {
+        const uint32_t cur = hk[s];
+        if (cur == kInvalid) break;
+        if (cur == w) {
+          const int j = int(hv[s]);
+          if (i < j && p < j) atomicAdd(&s_det[wave][j], 1u);
+          break;
+        }
+        s = (s + 1u) & 511u;
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  // Keep the g edges of fewest detours (ties by rank), in rank order.
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int j = e * 64 + lane;
+    v[e] = j < valid_n ? (uint64_t(s_det[wave][j]) << 32) | uint32_t(j) : kEmpty;
+  }
+  wave_sort_e<E>(v);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    v[e] = (p < g && v[e] != kEmpty) ? (v[e] & 0xffffffffull) : kEmpty;  // rank only
+  }
+  wave_sort_e<E>(v);
+  uint32_t* out = kept + u * g;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    if (p < g) {
+      const uint32_t w = v[e] == kEmpty ? kInvalid : s_nb[wave][uint32_t(v[e])];
+      out[p] = w;
+      if (w != kInvalid) {
+        const uint32_t slot = atomicAdd(&rev_cnt[w], 1u);
+        if (slot < uint32_t(g)) rev[int64_t(w) * g + slot] = uint32_t(u);
+      }
+    }
+  }
+}
+
+// Per node (one wave): closest g/2 kept edges, then up to g/2 reverse
+// edges, then the remaining kept edges; no duplicates.
+__global__ __launch_bounds__(256) void merge_reverse_kernel(const uint32_t* __restrict__ kept,
+                                                            const uint32_t* __restrict__ rev,
+                                                            const uint32_t* __restrict__ rev_cnt, int64_t n, int g,
+                                                            uint32_t* __restrict__ out) {
+  __shared__ uint32_t s_out[4][1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t u = int64_t(blockIdx.x) * 4 + wave;
+  if (u >= n) return;
+  uint32_t* so = s_out[wave];
+  if (lane == 0) {
+    const uint32_t* kr = kept + u * g;
+    const uint32_t* rr = rev + u * g;
+    const int rc = int(min(rev_cnt[u], uint32_t(g)));
+    int m = 0;
+    auto has = [&](uint32_t w) {
+      for (int i = 0; i < m; ++i)
+        if (so[i] == w) return true;
+      return false;
+    };
+    const int half = g / 2;
+    for (int i = 0; i < half; ++i)
+      if (kr[i] != kInvalid && !has(kr[i])) so[m++] = kr[i];
+    int added = 0;
+    for (int i = 0; i < rc && added < g - half && m < g; ++i)
+      if (!has(rr[i])) {
+        so[m++] = rr[i];
+        ++added;
+      }
+    for (int i = half; i < g && m < g; ++i)
+      if (kr[i] != kInvalid && !has(kr[i])) so[m++] = kr[i];
+    for (int i = m; i < g; ++i) so[i] = kInvalid;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  for (int i = lane; i < g; i += 64) out[u * g + i] = so[i];
+}
+
+template <typename K>
+void launch_e(int e, dim3 grid, hipStream_t s, BuildArgs a) {
+  switch (e) {
+    case 1: hipLaunchKernelGGL(K::template fn<1>(), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(K::template fn<2>(), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(K::template fn<4>(), grid, dim3(256), 0, s, a); break;
+  }
+}
+struct SampleK {
+  template <int E>
+  static constexpr auto fn() { return sample_kernel<E>; }
+};
+struct ApplyK {
+  template <int E>
+  static constexpr auto fn() { return apply_kernel<E>; }
+};
+
+struct DevMem {
+  std::vector<void*> ptrs;
+  template <typename T>
+  T* alloc(size_t count) {
+    void* p = nullptr;
+    check_hip(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), "hipMalloc(build)");
+    ptrs.push_back(p);
+    return static_cast<T*>(p);
+  }
+  ~DevMem() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+};
+
+double elapsed_s(std::chrono::steady_clock::time_point t0) {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+
+void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                        uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
+                        float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
+                        cvs_build_stats* stats) {
+  const auto t_start = std::chrono::steady_clock::now();
+  if (!rows || n <= 0 || d <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "dataset must be non-null and non-empty");
+  if (!out_graph) fail(CVS_ERR_INVALID_ARGUMENT, "null out_graph");
+  if (n < 2) fail(CVS_ERR_INVALID_ARGUMENT, "a graph needs at least 2 rows");
+  if (n > int64_t(INT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "graph build needs n < 2^31");
+  if (graph_degree == 0) fail(CVS_ERR_INVALID_ARGUMENT, "graph_degree must be positive");
+  if (intermediate_degree > uint32_t(kMaxKd)) fail(CVS_ERR_UNSUPPORTED, "intermediate_graph_degree exceeds 256");
+  const int kd = int(std::min<int64_t>(std::max<uint32_t>(intermediate_degree, graph_degree), n - 1));
+  if (kd > kMaxKd) fail(CVS_ERR_UNSUPPORTED, "graph_degree exceeds 256");
+  const int g = int(std::min<int64_t>(graph_degree, kd));
+  const int kp = (kd + 63) / 64 * 64;
+  const int e_slots = kp / 64 == 3 ? 4 : kp / 64;
+  const int64_t dp = (d + 63) / 64 * 64;
+  hipStream_t st = ctx->stream;
+  cvs_build_stats s{};
+
+  DevMem mem;
+  _Float16* x16 = mem.alloc<_Float16>(size_t(n) * dp);
+  float* norms = mem.alloc<float>(size_t(n));
+  {
+    const float* src = rows;
+    if (!rows_on_device) {
+      float* tmp = mem.alloc<float>(size_t(n) * d);
+      CVS_HIP(hipMemcpyAsync(tmp, rows, size_t(n) * d * sizeof(float), hipMemcpyHostToDevice, st));
+      src = tmp;
+    }
+    hipLaunchKernelGGL(to_half_rows_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, src, n, d, dp, x16,
+                       norms);
+    after_launch("to_half_rows_kernel");
+  }
+  // Random permutations: the reference's LCG Fisher-Yates
+  // (src/metal_context.mm:802-810); later rounds continue the sequence.
+  std::vector<uint32_t> perm(static_cast<size_t>(n));
+  uint64_t r = seed;
+  auto next_perm = [&] {
+    std::iota(perm.begin(), perm.end(), 0u);
+    for (int64_t i = n - 1; i > 0; --i) {
+      r = r * 6364136223846793005ULL + 1442695040888963407ULL;
+      const int64_t j = int64_t(r >> 33) % (i + 1);
+      std::swap(perm[size_t(i)], perm[size_t(j)]);
+    }
+  };
+  uint32_t* d_perm = mem.alloc<uint32_t>(size_t(n));
+
+  BuildArgs a{};
+  a.x16 = reinterpret_cast<const char*>(x16);
+  a.norms = norms;
+  a.row_bytes = dp * 2;
+  a.n_chunks = int(dp / 64);
+  a.n = uint32_t(n);
+  a.kd = kd;
+  a.kp = kp;
+  a.lists = mem.alloc<uint64_t>(size_t(n) * kp);
+  a.fwd = mem.alloc<uint32_t>(size_t(n) * 2 * kSample);
+  a.fwd_cnt = mem.alloc<uint32_t>(size_t(n) * 2);
+  a.rev = mem.alloc<uint32_t>(size_t(n) * 2 * kSample);
+  a.rev_cnt = mem.alloc<uint32_t>(size_t(n) * 2);
+  a.bins = mem.alloc<uint64_t>(size_t(n) * kBin);
+  a.bin_cnt = mem.alloc<uint32_t>(size_t(n));
+  a.counters = mem.alloc<unsigned long long>(4);
+  CVS_HIP(hipMemsetAsync(a.bin_cnt, 0, size_t(n) * sizeof(uint32_t), st));
+  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * sizeof(unsigned long long), st));
+
+  const int64_t n_buckets = (n + kBucket - 1) / kBucket;
+  const dim3 wave_grid(unsigned((n + 3) / 4));
+  const int rounds = n <= kBucket ? 1 : kBucketRounds;
+  for (int round = 0; round < rounds; ++round) {
+    next_perm();
+    CVS_HIP(hipMemcpyAsync(d_perm, perm.data(), size_t(n) * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    hipLaunchKernelGGL(bucket_kernel, dim3(unsigned(n_buckets)), dim3(256), 0, st, a,
+                       static_cast<const uint32_t*>(d_perm), round > 0 ? 1 : 0);
+    after_launch("bucket_kernel");
+    if (round > 0) {
+      launch_e<ApplyK>(e_slots, wave_grid, st, a);
+      after_launch("apply_kernel");
+    }
+    // The host permutation buffer is reused: wait for its copy.
+    CVS_HIP(hipStreamSynchronize(st));
+  }
+  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * sizeof(unsigned long long), st));
+  CVS_HIP(hipStreamSynchronize(st));
+  s.seconds_seed = elapsed_s(t_start);
+
+  // nn-descent.
+  const auto t_nd = std::chrono::steady_clock::now();
+  hipEvent_t ev0, ev1;
+  CVS_HIP(hipEventCreate(&ev0));
+  CVS_HIP(hipEventCreate(&ev1));
+  double join_ms = 0.0;
+  uint32_t it = 0;
+  double rate = 1.0;
+  unsigned long long prev[4] = {0, 0, 0, 0};
+  for (; it < max_iterations; ++it) {
+    CVS_HIP(hipMemsetAsync(a.rev_cnt, 0, size_t(n) * 2 * sizeof(uint32_t), st));
+    launch_e<SampleK>(e_slots, wave_grid, st, a);
+    after_launch("sample_kernel");
+    CVS_HIP(hipEventRecord(ev0, st));
+    hipLaunchKernelGGL(join_kernel, dim3(unsigned(n)), dim3(256), 0, st, a);
+    after_launch("join_kernel");
+    CVS_HIP(hipEventRecord(ev1, st));
+    launch_e<ApplyK>(e_slots, wave_grid, st, a);
+    after_launch("apply_kernel");
+    unsigned long long cnt[4];
+    CVS_HIP(hipMemcpyAsync(cnt, a.counters, sizeof(cnt), hipMemcpyDeviceToHost, st));
+    CVS_HIP(hipStreamSynchronize(st));
+    float ms = 0.f;
+    CVS_HIP(hipEventElapsedTime(&ms, ev0, ev1));
+    join_ms += ms;
+    const unsigned long long ins = cnt[0] - prev[0];
+    s.join_members += cnt[1] - prev[1];
+    s.updates_emitted += cnt[2] - prev[2];
+    s.updates_kept += cnt[3] - prev[3];
+    s.insertions += ins;
+    for (int i = 0; i < 4; ++i) prev[i] = cnt[i];
+    rate = double(ins) / (double(n) * double(kd));
+    if (rate < double(termination_threshold)) {
+      ++it;
+      break;
+    }
+  }
+  (void)hipEventDestroy(ev0);
+  (void)hipEventDestroy(ev1);
+  s.iterations = it;
+  s.final_update_rate = it ? rate : 0.0;
+  s.join_ms = join_ms;
+  s.join_bytes = double(s.join_members) * double(dp) * 2.0;
+  s.seconds_descent = elapsed_s(t_nd);
+
+  // Prune + reverse edges.
+  const auto t_pr = std::chrono::steady_clock::now();
+  uint32_t* ids = mem.alloc<uint32_t>(size_t(n) * kd);
+  hipLaunchKernelGGL(list_ids_kernel, dim3(unsigned((n * kd + 255) / 256)), dim3(256), 0, st,
+                     static_cast<const uint64_t*>(a.lists), n, kd, kp, ids);
+  after_launch("list_ids_kernel");
+  uint32_t* kept = mem.alloc<uint32_t>(size_t(n) * g);
+  uint32_t* rev = mem.alloc<uint32_t>(size_t(n) * g);
+  uint32_t* rev_cnt = mem.alloc<uint32_t>(size_t(n));
+  CVS_HIP(hipMemsetAsync(rev_cnt, 0, size_t(n) * sizeof(uint32_t), st));
+  switch (e_slots) {
+    case 1: hipLaunchKernelGGL(prune_kernel<1>, wave_grid, dim3(256), 0, st, ids, n, kd, g, kept, rev, rev_cnt); break;
+    case 2: hipLaunchKernelGGL(prune_kernel<2>, wave_grid, dim3(256), 0, st, ids, n, kd, g, kept, rev, rev_cnt); break;
+    default: hipLaunchKernelGGL(prune_kernel<4>, wave_grid, dim3(256), 0, st, ids, n, kd, g, kept, rev, rev_cnt); break;
+  }
+  after_launch("prune_kernel");
+  uint32_t* final_graph = graph_on_device ? out_graph : mem.alloc<uint32_t>(size_t(n) * g);
+  hipLaunchKernelGGL(merge_reverse_kernel, wave_grid, dim3(256), 0, st, static_cast<const uint32_t*>(kept),
+                     static_cast<const uint32_t*>(rev), static_cast<const uint32_t*>(rev_cnt), n, g, final_graph);
+  after_launch("merge_reverse_kernel");
+  if (!graph_on_device)
+    CVS_HIP(hipMemcpyAsync(out_graph, final_graph, size_t(n) * g * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  CVS_HIP(hipStreamSynchronize(st));
+  s.seconds_prune = elapsed_s(t_pr);
+  s.graph_degree = uint32_t(g);
+  s.intermediate_degree = uint32_t(kd);
+  s.seconds_total = elapsed_s(t_start);
+  if (stats) *stats = s;
+}
+
+}  // namespace
+}  // namespace cvs
+
+using namespace cvs;
+
+extern "C" {
+
+int cvs_cagra_build(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                    uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
+                    float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
+                    cvs_build_stats* stats) {
+  return guarded([&] {
+    bind(ctx);
+    cagra_build_device(ctx, rows, n, d, rows_on_device, intermediate_degree, graph_degree, max_iterations,
+                       termination_threshold, seed, out_graph, graph_on_device, stats);
+  });
+}
+
+}  // extern "C"

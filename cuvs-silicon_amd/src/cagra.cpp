@@ -71,10 +71,37 @@ index<float, std::uint32_t> build<float, std::int64_t>(
   if (params.attach_dataset_on_build) storage.assign(data, data + n * d);
   index<float, std::uint32_t> idx{std::move(storage), n, d};
 
+  // G = min(graph_degree, N - 1) (src/cagra.cpp:47-48); 0 keeps an exact
+  // brute-force index.
   const std::uint32_t degree =
       std::min<std::uint32_t>(params.graph_degree, static_cast<std::uint32_t>(n - 1));
   if (n > 1 && degree > 0) {
-    throw std::runtime_error("CAGRA graph build is not available in this build");
+    cvs_build_stats stats{};
+    std::vector<std::uint32_t> graph(static_cast<std::size_t>(n) * degree);
+    counted([&] {
+      return cvs_cagra_build(Backend::instance().ctx(), data, n, d, 0,
+                             std::max(params.intermediate_graph_degree, degree), degree,
+                             params.nn_descent_niter, params.nn_descent_termination_threshold,
+                             0xFEDCBA9876543210ULL, graph.data(), 0, &stats);
+    });
+    if (stats.graph_degree != degree)
+      throw std::runtime_error("CAGRA build returned an unexpected graph degree");
+    idx.set_knn_graph(std::move(graph), degree);
+
+    // Navigation nodes: min(200, floor(sqrt(N))) evenly spaced rows and
+    // their vectors (src/cagra.cpp:63-82); search seeds from them.
+    const std::int64_t n_nav =
+        std::min<std::int64_t>(200, static_cast<std::int64_t>(std::sqrt(static_cast<double>(n))));
+    std::vector<std::uint32_t> nav(static_cast<std::size_t>(n_nav));
+    std::vector<float> nav_vectors(static_cast<std::size_t>(n_nav * d));
+    const double step = static_cast<double>(n) / static_cast<double>(n_nav);
+    for (std::int64_t i = 0; i < n_nav; ++i) {
+      nav[static_cast<std::size_t>(i)] = static_cast<std::uint32_t>(static_cast<double>(i) * step);
+      std::copy_n(data + static_cast<std::int64_t>(nav[static_cast<std::size_t>(i)]) * d,
+                  static_cast<std::size_t>(d), nav_vectors.data() + i * d);
+    }
+    idx.set_nav_nodes(std::move(nav));
+    idx.set_nav_vectors(std::move(nav_vectors));
   }
   return idx;
 }

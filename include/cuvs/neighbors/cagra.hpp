@@ -48,6 +48,11 @@ struct index_params {
   bool attach_dataset_on_build = true;
   bool guarantee_connectivity = false;
   cuvs::distance::DistanceType metric = cuvs::distance::DistanceType::L2Expanded;
+  // Added after the reference's fields (cuVS names them the same way):
+  // nn-descent iteration cap and early-stop threshold on the fraction of
+  // list entries replaced in one iteration.
+  std::uint32_t nn_descent_niter = 20;
+  float nn_descent_termination_threshold = 0.001F;
 };
 
 struct search_params {

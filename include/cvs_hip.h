@@ -165,6 +165,41 @@ int cvs_cagra_search_async(cvs_context* ctx, const cvs_cagra_index* index, const
                            uint32_t max_iterations, uint32_t* out_neighbors_dev,
                            float* out_distances_dev, uint32_t* out_stats_dev);
 
+/* ---- CAGRA graph build --------------------------------------------------- */
+
+/* Phase timings and work counters of one cvs_cagra_build call. */
+typedef struct cvs_build_stats {
+  uint32_t iterations;          /* nn-descent iterations run */
+  uint32_t intermediate_degree; /* list length used (<= n - 1) */
+  uint32_t graph_degree;        /* output degree (<= intermediate_degree) */
+  double final_update_rate;     /* insertions / (n * intermediate_degree), last iteration */
+  double seconds_seed;          /* upload + fp16 conversion + random bucketing */
+  double seconds_descent;       /* all nn-descent iterations */
+  double seconds_prune;         /* detour pruning + reverse edges + copy-out */
+  double seconds_total;
+  double join_ms;               /* summed local-join kernel time (HIP events) */
+  double join_bytes;            /* rows gathered by the local joins x 2*dp (fp16 row bytes) */
+  uint64_t join_members;        /* rows gathered by the local joins */
+  uint64_t updates_emitted;     /* candidate neighbours the joins appended to update bins */
+  uint64_t updates_kept;        /* bin entries left after deduplication against the lists */
+  uint64_t insertions;          /* entries that entered a list */
+} cvs_build_stats;
+
+/* Builds a fixed-degree search graph of an n x d fp32 dataset on the GPU:
+ * random bucketing seeds a degree-`intermediate_degree` kNN list per row,
+ * nn-descent refines it (at most `max_iterations` iterations; stops early
+ * when insertions / (n * intermediate_degree) < termination_threshold), and
+ * rank-based detour pruning plus reverse edges reduce it to `graph_degree`
+ * (clamped to n - 1).  Writes n x min(graph_degree, n - 1) uint32 ids to
+ * out_graph (host memory, or device memory if graph_on_device = 1); rows
+ * with fewer neighbours end in UINT32_MAX.  `seed` drives the bucketing
+ * permutation.  Replaces MetalContext::build_knn_graph
+ * (metal_context.hpp:47-55; src/metal_context.mm:289-914). */
+int cvs_cagra_build(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                    uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
+                    float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
+                    cvs_build_stats* stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,107 @@
+"""GPU graph build (C ABI: cvs_cagra_build).
+
+Gates:
+  - invariants of the returned graph: n x min(graph_degree, n - 1) ids, all
+    in range, no self edges, no duplicate edges in a row (the reference's
+    build allows duplicates; this one must not);
+  - neighbour quality: the share of each row's exact 10 nearest neighbours
+    that appear in its list (the build keeps the closest half of the pruned
+    list first);
+  - downstream recall: graph search on the built graph reaches at least the
+    recall of the restated reference search on the reference's own graph
+    for n <= 50,000 (exact all-pairs seeding, src/metal_context.mm:324-349,
+    which the oracle's exact kNN graph stands for) at equal degree and itopk,
+    minus 0.01;
+  - nn-descent convergence: the last iteration's insertion rate is below the
+    threshold unless the iteration cap was reached.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+INV = 0xFFFFFFFF
+
+
+def clustered(rng, n, d, centers=16, sigma=0.5):
+    c = rng.standard_normal((centers, d)).astype(np.float32)
+    return c[rng.integers(0, centers, n)] + sigma * rng.standard_normal((n, d)).astype(np.float32)
+
+
+def check_graph(graph, n, g):
+    assert graph.shape == (n, g)
+    for i in range(n):
+        row = graph[i]
+        valid = row[row != INV]
+        assert (valid < n).all()
+        assert i not in set(valid.tolist())
+        assert len(set(valid.tolist())) == len(valid)
+
+
+def recall(nbr, gt, k):
+    return float(np.mean([len(set(nbr[i, :k].tolist()) & set(gt[i, :k].tolist())) / k for i in range(len(nbr))]))
+
+
+@pytest.mark.parametrize("n,d", [(2, 3), (40, 8), (200, 16)])
+def test_single_bucket_graphs(ctx, oracle, n, d):
+    """n <= 256: one bucket holds every row, so lists start exact."""
+    rng = np.random.default_rng(n)
+    base = rng.standard_normal((n, d)).astype(np.float32)
+    graph, st = ctx.cagra_build(base, intermediate_degree=32, graph_degree=16)
+    g = min(16, n - 1)
+    check_graph(graph, n, g)
+    assert st["graph_degree"] == g and st["intermediate_degree"] == min(32, n - 1)
+    # every row is full and holds its exact nearest neighbour
+    assert (graph != INV).all()
+    exact = oracle.knn_graph(base, 1, threads=8)
+    assert np.mean([exact[i, 0] in set(graph[i].tolist()) for i in range(n)]) >= 0.97
+
+
+def test_neighbour_quality_and_convergence(ctx, oracle):
+    rng = np.random.default_rng(21)
+    n, d = 6000, 64
+    base = clustered(rng, n, d)
+    graph, st = ctx.cagra_build(base, intermediate_degree=64, graph_degree=32, max_iterations=30)
+    check_graph(graph, n, 32)
+    print("build stats:", st)
+    assert st["iterations"] >= 2
+    assert st["iterations"] == 30 or st["final_update_rate"] < 0.001
+    exact = oracle.knn_graph(base, 10, threads=16)
+    share = np.mean([len(set(exact[i].tolist()) & set(graph[i].tolist())) / 10 for i in range(n)])
+    print(f"share of exact 10-NN in the built lists: {share:.4f}")
+    assert share > 0.9
+
+
+@pytest.mark.parametrize("n,d,g,itopk", [(8000, 128, 32, 64), (5000, 1024, 64, 64)])
+def test_downstream_recall_at_least_reference(ctx, oracle, n, d, g, itopk):
+    rng = np.random.default_rng(n + d)
+    base = clustered(rng, n, d)
+    qs = clustered(np.random.default_rng(7), 300, d)
+    graph, st = ctx.cagra_build(base, intermediate_degree=2 * g, graph_degree=g)
+    check_graph(graph, n, g)
+    nav = oracle.cagra_nav_nodes(n)
+    gt, _ = oracle.bf_exact(base, qs, 10, threads=16)
+    ours, _ = ctx.cagra_index(base, graph, nav).search(qs, 10, itopk_size=itopk)
+    ref_graph = oracle.knn_graph(base, g, threads=16)
+    ref, _ = oracle.cagra_reference_search(base, ref_graph, nav, qs, 10, itopk_size=itopk, threads=16)
+    r_ours, r_ref = recall(ours, gt, 10), recall(ref, gt, 10)
+    print(f"recall@10 built graph + GPU search {r_ours:.4f}; exact graph + restated reference search {r_ref:.4f}")
+    assert r_ours >= r_ref - 0.01
+
+
+def test_device_output_matches_shape(ctx, cvs):
+    rng = np.random.default_rng(3)
+    base = rng.standard_normal((1000, 32)).astype(np.float32)
+    out = cvs.DeviceArray(ctx, (1000, 24), np.uint32)
+    dev = cvs.DeviceArray.from_host(ctx, base)
+    g, st = ctx.cagra_build(dev, intermediate_degree=48, graph_degree=24, out=out)
+    check_graph(g.to_host(), 1000, 24)
+
+
+def test_build_argument_errors(ctx):
+    with pytest.raises(ValueError):
+        ctx.cagra_build(np.ones((1, 4), np.float32))
+    with pytest.raises(ValueError):
+        ctx.cagra_build(np.ones((10, 4), np.float32), intermediate_degree=300)
+    with pytest.raises(ValueError):
+        ctx.cagra_build(np.ones((10, 4), np.float32), graph_degree=0)
