@@ -139,16 +139,29 @@ def main() -> int:
     ap.add_argument("--no-recall", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (PMC byte-counter calibration)")
+    ap.add_argument("--workload", choices=["bf", "cagra-search", "cagra-build"], default="bf",
+                    help="bf: the headline brute-force line (default); cagra-search: graph search at "
+                         "N=100K D=1024 Q=10,000 degree 64; cagra-build: graph build at N=1M D=1024")
+    ap.add_argument("--itopk", type=int, default=64)
+    ap.add_argument("--degree", type=int, default=64)
     args = ap.parse_args()
 
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the N-sharded multi-GPU design is described in DESIGN.md but not built.", file=sys.stderr)
+              "how the search would shard over several GPUs is described in the design notes, "
+              "but only the one-GPU path is built.", file=sys.stderr)
         return 2
-    rank = int(os.environ.get("RANK", "0"))
+    if args.workload == "cagra-search":
+        return run_cagra_search(args)
+    if args.workload == "cagra-build":
+        return run_cagra_build(args)
+    return run_bf(args)
 
+
+def run_bf(args) -> int:
+    rank = int(os.environ.get("RANK", "0"))
     cvs = load_package()
     n, d, q, k = args.n, args.d, args.q, args.k
     log(f"generating clustered data N={n} D={d} Q={q}")
@@ -245,6 +258,149 @@ def main() -> int:
     ctx.close()
     if rank == 0:
         print(json.dumps(result), flush=True)
+    return 0
+
+
+def gpu_exact_knn(cvs, ctx, base, qs, k):
+    """Exact k-NN by the fused brute-force path (recall 1.0 against fp64 at
+    N=1M; its own parity tests cover it), in batches of 1000 queries."""
+    ds = ctx.dataset(base)
+    out = np.empty((qs.shape[0], k), np.uint32)
+    for s in range(0, qs.shape[0], 1000):
+        out[s:s + 1000] = ds.bf_search(qs[s:s + 1000], k)[0]
+    ds.close()
+    return out
+
+
+def run_cagra_search(args) -> int:
+    """Graph search, N=100,000 D=1024 fp32, degree-64 graph built on the GPU,
+    itopk 64, search_width 1 and 4, K=10: QPS at Q=10,000 (device-resident
+    queries and outputs), Q=1 latency, recall@10 against exact k-NN, and the
+    restated reference search (nav-node entry, beam of itopk) on the same
+    graph and the host's cores for the recall floor and the CPU baseline."""
+    import oracle
+
+    cvs = load_package()
+    n = 100_000 if args.n == 1_000_000 else args.n
+    d, k, q = args.d, 10, 10_000 if args.q == 100 else args.q
+    log(f"generating clustered data N={n} D={d} Q={q}")
+    base = cvs.synth_clustered(args.seed, cvs.STREAM_BASE, n, d)
+    qs = cvs.synth_clustered(args.seed, cvs.STREAM_QUERIES, q, d)
+    ctx = cvs.Context(0)
+    t = time.perf_counter()
+    graph, bst = ctx.cagra_build(base, intermediate_degree=2 * args.degree, graph_degree=args.degree)
+    log(f"graph built in {time.perf_counter() - t:.2f}s ({bst['iterations']} nn-descent iterations)")
+    nav = oracle.cagra_nav_nodes(n)
+    idx = ctx.cagra_index(base, graph, nav)
+    gt = gpu_exact_knn(cvs, ctx, base, qs, k)
+    dq = cvs.DeviceArray.from_host(ctx, qs)
+    dn = cvs.DeviceArray(ctx, (q, k), np.uint32)
+    dd = cvs.DeviceArray(ctx, (q, k), np.float32)
+    st = cvs.DeviceArray(ctx, (q, 2), np.uint32)
+    results = []
+    for width in (1, 4):
+        for _ in range(2):
+            idx.search_async(dq, k, dn, dd, itopk_size=args.itopk, search_width=width)
+        ctx.synchronize()
+        steps = max(1, args.steps // 50)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            idx.search_async(dq, k, dn, dd, itopk_size=args.itopk, search_width=width)
+        ctx.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        ctx.set_timing(True)
+        idx.search_async(dq, k, dn, dd, itopk_size=args.itopk, search_width=width, stats=st)
+        kms, _ = ctx.kernel_time("cagra_search")
+        ctx.set_timing(False)
+        stats = st.to_host().astype(np.int64)
+        nbr = dn.to_host()
+        if width == 1:
+            nbr_w1 = nbr.copy()
+        # algorithmic bytes per query: distance evaluations x D*4 + expanded
+        # nodes x degree*4 (graph rows) + D*4 (the query)
+        expanded = stats[:, 1] * width
+        alg_bytes = float((stats[:, 0] * d * 4 + expanded * args.degree * 4 + d * 4).sum())
+        # Q=1 latency
+        dq1 = cvs.DeviceArray.from_host(ctx, qs[:1])
+        dn1 = cvs.DeviceArray(ctx, (1, k), np.uint32)
+        dd1 = cvs.DeviceArray(ctx, (1, k), np.float32)
+        lat = []
+        for _ in range(20):
+            t1 = time.perf_counter()
+            idx.search_async(dq1, k, dn1, dd1, itopk_size=args.itopk, search_width=width)
+            ctx.synchronize()
+            lat.append(time.perf_counter() - t1)
+        res = {
+            "search_width": width, "qps": q / dt, "ms_per_batch": dt * 1e3, "kernel_ms": kms,
+            "recall_at_10": recall_at_k(nbr, gt, k), "q1_latency_ms_p50": 1e3 * sorted(lat)[len(lat) // 2],
+            "mean_distance_evaluations": float(stats[:, 0].mean()), "mean_iterations": float(stats[:, 1].mean()),
+            "algorithmic_bytes_per_batch": alg_bytes,
+            "achieved_gbs": alg_bytes / (kms * 1e-3) / 1e9, "hbm_frac": alg_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        }
+        log(json.dumps(res))
+        results.append(res)
+    # restated reference search on the same graph, all host cores, sampled queries
+    sample = min(q, args.cpu_sample * 50)
+    threads = os.cpu_count() or 1
+    t0 = time.perf_counter()
+    ref_nbr, _ = oracle.cagra_reference_search(base, graph, nav, qs[:sample], k, itopk_size=args.itopk,
+                                               threads=threads)
+    cpu_dt = time.perf_counter() - t0
+    ref_recall = recall_at_k(ref_nbr, gt[:sample], k)
+    gpu_recall_sample = recall_at_k(nbr_w1[:sample], gt[:sample], k)
+    out = {
+        "metric": "CAGRA search QPS at recall@10, N=100K D=1024 degree 64 itopk 64 K=10 Q=10,000",
+        "value": results[0]["qps"], "unit": "queries/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"CAGRA graph search, N={n} D={d} Q={q} K={k} itopk={args.itopk} "
+                               f"degree={args.degree}, graph built on the GPU", "seed": args.seed},
+        "widths": results,
+        "build": bst,
+        "reference_search_same_graph": {"recall_at_10": ref_recall, "queries": sample,
+                                        "gpu_recall_at_10_same_queries": gpu_recall_sample},
+        "cpu_baseline": {"value": sample / cpu_dt, "unit": "queries/s", "cores": threads, "kind": "port",
+                         "sample": f"restated reference beam search, {sample} queries, itopk {args.itopk}, "
+                                   f"OpenMP over queries"},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_cagra_build(args) -> int:
+    """Graph build, N=1,000,000 D=1024 fp32, intermediate degree 128 ->
+    degree 64: seconds per phase, local-join GB/s (rows gathered x fp16 row
+    bytes / join kernel time), downstream recall@10 at itopk 64 on 1,000
+    queries against exact k-NN."""
+    cvs = load_package()
+    n, d, k = args.n, args.d, 10
+    q = 1000
+    log(f"generating clustered data N={n} D={d}")
+    base = cvs.synth_clustered(args.seed, cvs.STREAM_BASE, n, d)
+    qs = cvs.synth_clustered(args.seed, cvs.STREAM_QUERIES, q, d)
+    ctx = cvs.Context(0)
+    drows = cvs.DeviceArray.from_host(ctx, base)
+    g = cvs.DeviceArray(ctx, (n, args.degree), np.uint32)
+    log("building")
+    t = time.perf_counter()
+    _, bst = ctx.cagra_build(drows, intermediate_degree=2 * args.degree, graph_degree=args.degree, out=g)
+    wall = time.perf_counter() - t
+    log(json.dumps(bst))
+    import oracle
+    nav = oracle.cagra_nav_nodes(n)
+    idx = ctx.cagra_index(drows, g, nav)
+    gt = gpu_exact_knn(cvs, ctx, base, qs, k)
+    nbr, _ = idx.search(qs, k, itopk_size=args.itopk)
+    out = {
+        "metric": "CAGRA build seconds, N=1M D=1024 degree 128 -> 64; local-join HBM GB/s; recall@10 at itopk 64",
+        "value": wall, "unit": "s", "n_gpus": 1, "higher_is_better": False, "dtype": "f16 (build distances)",
+        "data": "synthetic",
+        "config": {"workload": f"CAGRA graph build N={n} D={d}, random bucketing + nn-descent + pruning",
+                   "seed": args.seed},
+        "build": bst,
+        "join_gbs": bst["join_bytes"] / (bst["join_ms"] * 1e-3) / 1e9 if bst["join_ms"] else None,
+        "recall_at_10_itopk": {"itopk": args.itopk, "recall": recall_at_k(nbr, gt, k), "queries": q},
+    }
+    print(json.dumps(out), flush=True)
     return 0
 
 
