@@ -14,17 +14,20 @@
 //               the 256 x 256 Gram matrix on v_mfma_f32_32x32x16_f16 (fp32
 //               accumulate) over LDS-staged 64-dimension chunks and gives each
 //               row the `kd` nearest of its 255 bucket mates: the initial
-//               degree-kd ("intermediate degree") list.
+//               degree-kd ("intermediate degree") list.  Three more rounds with
+//               fresh permutations merge each row's 32 nearest mates of another
+//               bucket into its list, so that lists span several buckets
+//               before the first local join.
 //  3. nn-descent, per iteration:
-//     sample    per node, up to 16 "new" (never joined) and 16 "old"
+//     sample    per node, up to 32 "new" (never joined) and 32 "old"
 //               neighbours; new ones are marked old.  Each sampled edge
-//               u -> v also appends u to v's reverse new/old list (16 each).
+//               u -> v also appends u to v's reverse new/old list (32 each).
 //     join      per node, its sampled forward + reverse neighbours (at most
-//               64 rows) are gathered into LDS chunk by chunk and their 64 x 64
-//               Gram matrix is formed on MFMA: the local join.  For every
-//               member, the 8 best partners (at least one of the pair new)
-//               that beat the member's current worst neighbour are appended
-//               to the member's update bin.
+//               128 rows) are gathered into LDS chunk by chunk and their
+//               128 x 128 Gram matrix is formed on MFMA: the local join.  For
+//               every member, the 8 best partners (at least one of the pair
+//               new) that beat the member's current worst neighbour are
+//               appended to the member's update bin (128 slots).
 //     apply     per node, the bin is deduplicated, filtered against the
 //               list, sorted and merged into the sorted list (wave bitonic
 //               merge); inserted entries are marked new and counted.
@@ -61,9 +64,10 @@ constexpr uint64_t kEmpty = ~0ull;
 constexpr uint32_t kInvalid = 0xffffffffu;
 constexpr int kChunkBytes = 128;  // 64 fp16 dimensions per staged chunk
 constexpr int kStageStride = 144; // bytes per staged row (128 + 16 against bank conflicts)
-constexpr int kSample = 16;       // sampled forward/reverse new/old neighbours
+constexpr int kSample = 32;       // sampled forward/reverse new/old neighbours
 constexpr int kJoinM = 4 * kSample;
-constexpr int kBin = 64;          // update bin capacity per node
+constexpr int kBin = 128;         // update bin capacity per node
+constexpr int kSlots = 256;       // spread of the global work counters
 constexpr int kEmit = 8;          // partners emitted per member and join
 constexpr int kBucket = 256;
 constexpr int kBucketRounds = 4;   // random bucketings merged into the initial lists
@@ -138,13 +142,14 @@ __device__ __forceinline__ void wave_merge(uint64_t (&v)[E], uint64_t c) {
 __device__ __forceinline__ uint32_t key_id(uint64_t k) { return uint32_t(k) >> 1; }
 
 // ---------------------------------------------------------------------------
-// Gram tiles of a set of fp16 rows.  The member rows s_ids[0..M) are staged
-// 64 dimensions at a time (M x 128 B, rows 144 B apart) and each wave
-// accumulates NT 32x32 tiles: tile t = rows 32*rt[t].., columns 32*ct[t]..
-// Loads of chunk c+1 are in flight while chunk c is multiplied.
+// Gram tiles of a set of fp16 rows.  The member rows s_ids[0..m) (m <= M)
+// are staged 64 dimensions at a time (M x 128 B, rows 144 B apart; rows >= m
+// are neither loaded nor used) and each wave accumulates NT 32x32 tiles:
+// tile t = rows 32*rt[t].., columns 32*ct[t]..  Loads run DEPTH chunks ahead
+// of the multiply.
 // ---------------------------------------------------------------------------
-template <int M, int NT>
-__device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t row_bytes, int n_chunks,
+template <int M, int NT, int DEPTH>
+__device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t row_bytes, int n_chunks, int m,
                                            const uint32_t* s_ids, char* s_stage, const int (&rt)[NT],
                                            const int (&ct)[NT], f32x16 (&acc)[NT]) {
   constexpr int LPT = M * 8 / 256;  // 16-byte loads per thread and chunk
@@ -152,38 +157,54 @@ __device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t
   const int lane = tid & 63;
   const char* src[LPT];
   int dst[LPT];
+  bool live[LPT];
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
     const int idx = tid + 256 * i;
     const int r = idx >> 3, seg = idx & 7;
-    src[i] = x16 + int64_t(s_ids[r]) * row_bytes + seg * 16;
+    live[i] = r < m;
+    src[i] = x16 + int64_t(s_ids[live[i] ? r : 0]) * row_bytes + seg * 16;
     dst[i] = r * kStageStride + seg * 16;
   }
+  bool tile_live[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < NT; ++t) {
+    tile_live[t] = 32 * rt[t] < m && 32 * ct[t] < m;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
-  u32x4 reg[LPT];
+  }
+  u32x4 reg[DEPTH][LPT];
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) reg[i] = *reinterpret_cast<const u32x4*>(src[i]);
-  for (int c = 0; c < n_chunks; ++c) {
-    __syncthreads();
+  for (int c = 0; c < DEPTH; ++c)
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[i];
-    __syncthreads();
-    if (c + 1 < n_chunks) {
+    for (int i = 0; i < LPT; ++i)
+      if (live[i] && c < n_chunks)
+        reg[c][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(c) * kChunkBytes);
+  for (int c0 = 0; c0 < n_chunks; c0 += DEPTH) {
+#pragma unroll
+    for (int cc = 0; cc < DEPTH; ++cc) {
+      const int c = c0 + cc;
+      if (c >= n_chunks) break;
+      __syncthreads();
 #pragma unroll
       for (int i = 0; i < LPT; ++i)
-        reg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(c + 1) * kChunkBytes);
-    }
+        if (live[i]) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[cc][i];
+      __syncthreads();
+      if (c + DEPTH < n_chunks) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int koff = s * 32 + 16 * (lane >> 5);
+        for (int i = 0; i < LPT; ++i)
+          if (live[i]) reg[cc][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(c + DEPTH) * kChunkBytes);
+      }
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const half8 a = *reinterpret_cast<const half8*>(s_stage + (32 * rt[t] + (lane & 31)) * kStageStride + koff);
-        const half8 b = *reinterpret_cast<const half8*>(s_stage + (32 * ct[t] + (lane & 31)) * kStageStride + koff);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
+      for (int s = 0; s < 4; ++s) {
+        const int koff = s * 32 + 16 * (lane >> 5);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (!tile_live[t]) continue;
+          const half8 a = *reinterpret_cast<const half8*>(s_stage + (32 * rt[t] + (lane & 31)) * kStageStride + koff);
+          const half8 b = *reinterpret_cast<const half8*>(s_stage + (32 * ct[t] + (lane & 31)) * kStageStride + koff);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
+        }
       }
     }
   }
@@ -226,7 +247,9 @@ struct BuildArgs {
   uint32_t* rev_cnt;     // n x 2
   uint64_t* bins;        // n x kBin
   uint32_t* bin_cnt;     // n
-  unsigned long long* counters;  // insertions, join members, updates emitted, bin entries kept
+  // Work counters, each spread over kSlots addresses:
+  // [0] insertions, [1] join members, [2] updates emitted, [3] bin entries kept.
+  unsigned long long* counters;
 };
 
 // One workgroup per bucket of up to 256 permuted rows.  First round
@@ -252,7 +275,7 @@ __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t
     const int rt[4] = {2 * rb, 2 * rb, 2 * rb + 1, 2 * rb + 1};
     const int ct[4] = {2 * wave, 2 * wave + 1, 2 * wave, 2 * wave + 1};
     f32x16 acc[4];
-    gram_tiles<kBucket, 4>(a.x16, a.row_bytes, a.n_chunks, s_ids, s_stage, rt, ct, acc);
+    gram_tiles<kBucket, 4, 1>(a.x16, a.row_bytes, a.n_chunks, mb, s_ids, s_stage, rt, ct, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -331,79 +354,143 @@ __global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
   }
 }
 
-// Per node (one workgroup): local join of its sampled neighbourhood.
-__global__ __launch_bounds__(256) void join_kernel(BuildArgs a) {
+// Per node (one workgroup): local join of its sampled neighbourhood.  The
+// members (forward + reverse samples, new ones first, at most 128) form a
+// symmetric Gram matrix; wave w owns the 32 columns [32w, 32w+32) over all
+// row tiles, so a lane holds 64 of its column's 128 entries and the partner
+// lane (lane ^ 32) the other 64.  Each column member keeps its 8 best
+// partners in registers (at least one of the pair new, below the member's
+// current worst key), merges them with the partner lane's, and appends them
+// to its update bin.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void join_kernel(BuildArgs a) {
   __shared__ __attribute__((aligned(16))) char s_stage[kJoinM * kStageStride];
-  __shared__ float s_dist[kJoinM * (kJoinM + 1)];
   __shared__ uint32_t s_ids[kJoinM];
   __shared__ float s_norm[kJoinM];
   __shared__ uint64_t s_worst[kJoinM];
   __shared__ int s_m[2];  // members, new members
+  __shared__ unsigned int s_emit;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t u = blockIdx.x;
-  if (tid == 0) {
+  if (tid < 64) {
+    // Lane-parallel member list: new forward, new reverse, old forward, old reverse.
     const uint32_t fn = a.fwd_cnt[2 * u], fo = a.fwd_cnt[2 * u + 1];
     const uint32_t rn = min(a.rev_cnt[2 * u], uint32_t(kSample));
     const uint32_t ro = min(a.rev_cnt[2 * u + 1], uint32_t(kSample));
     const uint32_t* fw = a.fwd + u * 2 * kSample;
     const uint32_t* rv = a.rev + u * 2 * kSample;
-    int m = 0;
-    for (uint32_t i = 0; i < fn; ++i) s_ids[m++] = fw[i];
-    for (uint32_t i = 0; i < rn; ++i) s_ids[m++] = rv[i];
-    const int mnew = m;
-    for (uint32_t i = 0; i < fo; ++i) s_ids[m++] = fw[kSample + i];
-    for (uint32_t i = 0; i < ro; ++i) s_ids[m++] = rv[kSample + i];
-    s_m[0] = m;
-    s_m[1] = mnew;
+    const int o1 = int(fn), o2 = o1 + int(rn), o3 = o2 + int(fo);
+    if (tid < kSample) {
+      if (uint32_t(tid) < fn) s_ids[tid] = fw[tid];
+      if (uint32_t(tid) < rn) s_ids[o1 + tid] = rv[tid];
+      if (uint32_t(tid) < fo) s_ids[o2 + tid] = fw[kSample + tid];
+      if (uint32_t(tid) < ro) s_ids[o3 + tid] = rv[kSample + tid];
+    }
+    if (tid == 0) {
+      s_m[0] = o3 + int(ro);
+      s_m[1] = o2;
+      s_emit = 0;
+    }
   }
   __syncthreads();
   const int m = s_m[0], mnew = s_m[1];
   if (mnew == 0 || m < 2) return;
-  if (tid < kJoinM) {
-    const uint32_t id = s_ids[tid < m ? tid : 0];
-    if (tid >= m) s_ids[tid] = id;
+  if (tid < m) {
+    const uint32_t id = s_ids[tid];
     s_norm[tid] = a.norms[id];
     s_worst[tid] = a.lists[int64_t(id) * a.kp + a.kd - 1] | 1ull;
   }
-  if (tid == 0) atomicAdd(&a.counters[1], (unsigned long long)m);
   __syncthreads();
-  const int rt[1] = {wave >> 1};
-  const int ct[1] = {wave & 1};
-  f32x16 acc[1];
-  gram_tiles<kJoinM, 1>(a.x16, a.row_bytes, a.n_chunks, s_ids, s_stage, rt, ct, acc);
+  const int rt[4] = {0, 1, 2, 3};
+  const int ct[4] = {wave, wave, wave, wave};
+  f32x16 acc[4];
+  gram_tiles<kJoinM, 4, 1>(a.x16, a.row_bytes, a.n_chunks, m, s_ids, s_stage, rt, ct, acc);
+
+  const int col = 32 * wave + (lane & 31);
+  const int half = lane >> 5;
+  unsigned int emitted = 0;
+  if (32 * wave < m) {
+    const bool col_ok = col < m;
+    const uint32_t cid = s_ids[col_ok ? col : 0];
+    const float cn = s_norm[col_ok ? col : 0];
+    const uint64_t worst = s_worst[col_ok ? col : 0];
+    const bool col_new = col < mnew;
+    uint64_t best[kEmit];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int row = 32 * rt[0] + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-    const int col = 32 * ct[0] + (lane & 31);
-    s_dist[row * (kJoinM + 1) + col] = s_norm[row] + s_norm[col] - 2.0f * acc[0][e];
+    for (int p = 0; p < kEmit; ++p) best[p] = kEmpty;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (32 * t >= m) break;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * t + 8 * (e >> 2) + 4 * half + (e & 3);
+        if (!col_ok || row >= m || !(col_new || row < mnew)) continue;
+        const uint32_t rid = s_ids[row];
+        if (rid == cid) continue;
+        const float dist = cn + s_norm[row] - 2.0f * acc[t][e];
+        const uint64_t key = (uint64_t(ord_f32(dist)) << 32) | (uint64_t(rid) << 1) | 1ull;
+        if (key < worst && key < best[kEmit - 1]) {
+          best[kEmit - 1] = key;
+#pragma unroll
+          for (int p = kEmit - 1; p > 0; --p) {
+            if (best[p] < best[p - 1]) {
+              const uint64_t tmp = best[p];
+              best[p] = best[p - 1];
+              best[p - 1] = tmp;
+            }
+          }
+        }
+      }
+    }
+    // Merge with the partner lane's list (same column, the other 64 rows):
+    // min against the reversed list gives the 8 smallest as a bitonic
+    // sequence, three half-cleaner steps sort it.
+    uint64_t mg[kEmit];
+#pragma unroll
+    for (int p = 0; p < kEmit; ++p) {
+      const uint64_t o = shfl_xor_u64(best[kEmit - 1 - p], 32);
+      mg[p] = best[p] < o ? best[p] : o;
+    }
+#pragma unroll
+    for (int stride = kEmit / 2; stride >= 1; stride >>= 1) {
+#pragma unroll
+      for (int p = 0; p < kEmit; ++p) {
+        if ((p & stride) == 0) {
+          const uint64_t lo = mg[p] < mg[p + stride] ? mg[p] : mg[p + stride];
+          const uint64_t hi = mg[p] < mg[p + stride] ? mg[p + stride] : mg[p];
+          mg[p] = lo;
+          mg[p + stride] = hi;
+        }
+      }
+    }
+    // Equal keys are the same partner seen twice (a member sampled both
+    // forward and reverse): keep one.
+    bool keep[kEmit];
+    int cnt = 0;
+#pragma unroll
+    for (int p = 0; p < kEmit; ++p) {
+      keep[p] = mg[p] != kEmpty && !(p > 0 && mg[p] == mg[p - 1]);
+      cnt += keep[p] ? 1 : 0;
+    }
+    if (half == 0 && cnt > 0) {
+      const uint32_t base = atomicAdd(&a.bin_cnt[cid], uint32_t(cnt));
+      uint64_t* bin = a.bins + int64_t(cid) * kBin;
+      uint32_t q = base;
+#pragma unroll
+      for (int p = 0; p < kEmit; ++p) {
+        if (keep[p]) {
+          if (q < uint32_t(kBin)) bin[q] = mg[p];
+          ++q;
+        }
+      }
+      emitted = unsigned(cnt);
+    }
   }
+  atomicAdd(&s_emit, emitted);
   __syncthreads();
-  for (int i = 16 * wave; i < 16 * wave + 16 && i < m; ++i) {
-    const uint32_t xi = s_ids[i];
-    const int j = lane;
-    const bool valid = j < m && (i < mnew || j < mnew) && s_ids[j] != xi;
-    const uint64_t key =
-        valid ? (uint64_t(ord_f32(s_dist[i * (kJoinM + 1) + j])) << 32) | (uint64_t(s_ids[j]) << 1) | 1ull : kEmpty;
-    const bool pass = valid && key < s_worst[i];
-    const uint64_t pm = __ballot(pass);
-    if (pm == 0) continue;
-    int cnt = popc(pm);
-    uint64_t k2 = pass ? key : kEmpty;
-    int rank = mbcnt(pm);
-    if (cnt > kEmit) {
-      uint64_t v1[1] = {k2};
-      wave_sort_e<1>(v1);
-      k2 = v1[0];
-      rank = lane;
-      cnt = kEmit;
-    }
-    uint32_t base = 0;
-    if (lane == 0) {
-      base = atomicAdd(&a.bin_cnt[xi], uint32_t(cnt));
-      atomicAdd(&a.counters[2], (unsigned long long)cnt);
-    }
-    base = uint32_t(__shfl(int(base), 0));
-    if (k2 != kEmpty && rank < cnt && base + rank < kBin) a.bins[int64_t(xi) * kBin + base + rank] = k2;
+  if (tid == 0) {
+    const int slot = int(u & (kSlots - 1));
+    atomicAdd(&a.counters[1 * kSlots + slot], (unsigned long long)m);
+    atomicAdd(&a.counters[2 * kSlots + slot], (unsigned long long)s_emit);
   }
 }
 
@@ -451,17 +538,31 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
     if (v[e] != kEmpty) insert(key_id(v[e]));
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  // Bin: keep the closest copy of each id that is not in the list yet.
-  uint64_t b = lane < c ? a.bins[u * kBin + lane] : kEmpty;
-  uint64_t by_id[1] = {b == kEmpty ? kEmpty : (uint64_t(key_id(b)) << 32) | (b >> 32)};
-  wave_sort_e<1>(by_id);
-  const uint64_t prev = shfl_u64(by_id[0], lane > 0 ? lane - 1 : 0);
-  const uint32_t bid = uint32_t(by_id[0] >> 32);
-  const bool keep = by_id[0] != kEmpty && (lane == 0 || uint32_t(prev >> 32) != bid) && !contains(bid);
-  uint64_t nk[1] = {keep ? ((by_id[0] & 0xffffffffull) << 32) | (uint64_t(bid) << 1) | 1ull : kEmpty};
-  const int n_keep = popc(__ballot(keep));
-  wave_sort_e<1>(nk);
+  // Bin (up to 128 keys, two per lane): keep the closest copy of each id
+  // that is not in the list yet.
+  uint64_t by_id[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int pos = e * 64 + lane;
+    const uint64_t b = pos < c ? a.bins[u * kBin + pos] : kEmpty;
+    by_id[e] = b == kEmpty ? kEmpty : (uint64_t(key_id(b)) << 32) | (b >> 32);
+  }
+  wave_sort_e<2>(by_id);
+  uint64_t nk[2];
+  int n_keep = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint64_t up = shfl_u64(by_id[e], lane > 0 ? lane - 1 : 0);
+    const uint64_t prev = lane > 0 ? up : (e > 0 ? shfl_u64(by_id[e - 1], 63) : kEmpty);
+    const uint32_t bid = uint32_t(by_id[e] >> 32);
+    const bool first = (e == 0 && lane == 0) || uint32_t(prev >> 32) != bid;
+    const bool keep = by_id[e] != kEmpty && first && !contains(bid);
+    nk[e] = keep ? ((by_id[e] & 0xffffffffull) << 32) | (uint64_t(bid) << 1) | 1ull : kEmpty;
+    n_keep += popc(__ballot(keep));
+  }
+  wave_sort_e<2>(nk);
   wave_merge<E>(v, nk[0]);
+  wave_merge<E>(v, nk[1]);
   int inserted = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -473,8 +574,9 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
   }
   if (lane == 0) {
     a.bin_cnt[u] = 0;
-    if (inserted) atomicAdd(&a.counters[0], (unsigned long long)inserted);
-    if (n_keep) atomicAdd(&a.counters[3], (unsigned long long)n_keep);
+    const int slot = int(u & (kSlots - 1));
+    if (inserted) atomicAdd(&a.counters[0 * kSlots + slot], (unsigned long long)inserted);
+    if (n_keep) atomicAdd(&a.counters[3 * kSlots + slot], (unsigned long long)n_keep);
   }
 }
 
@@ -708,9 +810,9 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   a.rev_cnt = mem.alloc<uint32_t>(size_t(n) * 2);
   a.bins = mem.alloc<uint64_t>(size_t(n) * kBin);
   a.bin_cnt = mem.alloc<uint32_t>(size_t(n));
-  a.counters = mem.alloc<unsigned long long>(4);
+  a.counters = mem.alloc<unsigned long long>(4 * kSlots);
   CVS_HIP(hipMemsetAsync(a.bin_cnt, 0, size_t(n) * sizeof(uint32_t), st));
-  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * sizeof(unsigned long long), st));
+  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * kSlots * sizeof(unsigned long long), st));
 
   const int64_t n_buckets = (n + kBucket - 1) / kBucket;
   const dim3 wave_grid(unsigned((n + 3) / 4));
@@ -728,7 +830,7 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
     // The host permutation buffer is reused: wait for its copy.
     CVS_HIP(hipStreamSynchronize(st));
   }
-  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * sizeof(unsigned long long), st));
+  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * kSlots * sizeof(unsigned long long), st));
   CVS_HIP(hipStreamSynchronize(st));
   s.seconds_seed = elapsed_s(t_start);
 
@@ -751,9 +853,13 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
     CVS_HIP(hipEventRecord(ev1, st));
     launch_e<ApplyK>(e_slots, wave_grid, st, a);
     after_launch("apply_kernel");
-    unsigned long long cnt[4];
-    CVS_HIP(hipMemcpyAsync(cnt, a.counters, sizeof(cnt), hipMemcpyDeviceToHost, st));
+    std::vector<unsigned long long> slots(4 * kSlots);
+    CVS_HIP(hipMemcpyAsync(slots.data(), a.counters, slots.size() * sizeof(unsigned long long),
+                           hipMemcpyDeviceToHost, st));
     CVS_HIP(hipStreamSynchronize(st));
+    unsigned long long cnt[4] = {0, 0, 0, 0};
+    for (int k = 0; k < 4; ++k)
+      for (int i = 0; i < kSlots; ++i) cnt[k] += slots[size_t(k) * kSlots + i];
     float ms = 0.f;
     CVS_HIP(hipEventElapsedTime(&ms, ev0, ev1));
     join_ms += ms;
