@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_cagra_search.restype = None
         L.oracle_cagra_search.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int64,
                                           c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_void_p, c_int]
+        L.oracle_cagra_build_ref.restype = c_int
+        L.oracle_cagra_build_ref.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
         L.oracle_knn_graph.restype = None
         L.oracle_knn_graph.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
         _lib = L
@@ -197,4 +199,19 @@ def knn_graph(base, g: int, threads: int = 1) -> np.ndarray:
     n, d = base.shape
     out = np.empty((n, g), np.uint32)
     lib().oracle_knn_graph(_p(base), n, d, int(g), _p(out), int(threads))
+    return out
+
+
+def cagra_build_reference(base, graph_degree: int = 64, threads: int = 1) -> np.ndarray:
+    """The reference's graph build restated (src/metal_context.mm:289-914,
+    n <= 200,000): returns n x min(graph_degree, n - 1) uint32 ids."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    g = min(int(graph_degree), n - 1)
+    out = np.empty((n, max(g, 0)), np.uint32)
+    rc = lib().oracle_cagra_build_ref(_p(base), n, d, int(graph_degree), _p(out), int(threads))
+    if rc == 2:
+        raise ValueError("the reference's N > 200,000 build path is not restated")
+    if rc != 0:
+        raise ValueError("invalid arguments")
     return out

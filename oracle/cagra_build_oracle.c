@@ -1,0 +1,380 @@
+/*
+ * CPU restatement of the reference's CAGRA graph build (TEST INFRASTRUCTURE
+ * ONLY; see oracle.h): cagra::build (src/cagra.cpp:47-59) ->
+ * MetalContext::build_knn_graph (src/metal_context.mm:289-914) for
+ * N <= 200,000.  Compiled with -ffp-contract=off.
+ *
+ * Where the reference's arithmetic order is unspecified (cblas_sgemm cross
+ * products, Metal's float4 dot), a fixed order is chosen and stated.  The
+ * reference's nn-descent kernel runs one threadgroup per node concurrently
+ * and races on the lists (src/metal_context.mm:870-871); this restatement
+ * runs the schedule in which each node's reads of other nodes' lists see the
+ * lists as they were at the start of the iteration, which makes it
+ * deterministic under any thread count.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+#define INVALID_ID 0xffffffffu
+
+/* Cross product in place of cblas_sgemm: eight interleaved fp32 partial sums
+ * combined pairwise (the BLAS order is unspecified). */
+static float dot_blk(const float* a, const float* b, int64_t d) {
+  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t i = 0;
+  for (; i + 8 <= d; i += 8)
+    for (int j = 0; j < 8; ++j) s[j] += a[i + j] * b[i + j];
+  for (; i < d; ++i) s[i & 7] += a[i] * b[i];
+  return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
+/* Metal kernels' distance (shaders/cagra_kernels.metal:369-375, :435-440):
+ * dist += dot(delta4, delta4) over D/4 float4 steps (a remainder of D % 4
+ * columns is ignored, as there); dot taken left to right. */
+static float l2_f4(const float* a, const float* b, int64_t d) {
+  float dist = 0.f;
+  for (int64_t i = 0; i + 4 <= d; i += 4) {
+    const float x = a[i] - b[i], y = a[i + 1] - b[i + 1];
+    const float z = a[i + 2] - b[i + 2], w = a[i + 3] - b[i + 3];
+    dist += ((x * x + y * y) + z * z) + w * w;
+  }
+  return dist;
+}
+
+/* Four independent l2_f4 distances (same values, interleaved for speed). */
+static void l2_f4_x4(const float* a, const float* const* b, int64_t d, float* out) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  for (int64_t i = 0; i + 4 <= d; i += 4) {
+    float t[4];
+    for (int c = 0; c < 4; ++c) {
+      const float* bc = b[c];
+      const float x = a[i] - bc[i], y = a[i + 1] - bc[i + 1];
+      const float z = a[i + 2] - bc[i + 2], w = a[i + 3] - bc[i + 3];
+      t[c] = ((x * x + y * y) + z * z) + w * w;
+    }
+    s0 += t[0];
+    s1 += t[1];
+    s2 += t[2];
+    s3 += t[3];
+  }
+  out[0] = s0;
+  out[1] = s1;
+  out[2] = s2;
+  out[3] = s3;
+}
+
+static float sq_norm(const float* v, int64_t d) {
+  float s = 0.f;
+  for (int64_t i = 0; i < d; ++i) s += v[i] * v[i];
+  return s;
+}
+
+/* insert_neighbor (src/metal_context.mm:315-322): replace the first slot of
+ * largest distance if closer; no duplicate check. */
+static void insert_neighbor(uint32_t* graph, float* gdist, uint32_t g, int64_t vi, uint32_t nbr, float dist) {
+  const int64_t row = vi * g;
+  float worst = gdist[row];
+  uint32_t wg = 0;
+  for (uint32_t j = 1; j < g; ++j)
+    if (gdist[row + j] > worst) {
+      worst = gdist[row + j];
+      wg = j;
+    }
+  if (dist < worst) {
+    graph[row + wg] = nbr;
+    gdist[row + wg] = dist;
+  }
+}
+
+/* Selection of the `take` smallest of idx[0..m) by key[idx] (ties by
+ * position, where std::partial_sort's tie order is unspecified), sorted. */
+static void select_smallest(uint32_t* idx, int64_t m, int64_t take, const float* key) {
+  for (int64_t t = 0; t < take && t < m; ++t) {
+    int64_t best = t;
+    for (int64_t j = t + 1; j < m; ++j)
+      if (key[idx[j]] < key[idx[best]]) best = j;
+    const uint32_t tmp = idx[t];
+    idx[t] = idx[best];
+    idx[best] = tmp;
+  }
+}
+
+int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
+                           uint32_t* out_graph, int threads) {
+  if (!data || !out_graph || n <= 0 || d <= 0) return 1;
+  if (n > 200000) return 2; /* the N > 200,000 PQ path is not restated */
+  const int nt = threads > 0 ? threads : 1;
+  /* src/cagra.cpp:47-59 */
+  const uint32_t g = graph_degree < (uint32_t)(n - 1) ? graph_degree : (uint32_t)(n - 1);
+  const uint32_t nd_iters = n <= 50000 ? 20u : (n <= 200000 ? 5u : 0u);
+  if (g == 0) return 0;
+
+  uint32_t* graph = out_graph;
+  float* gdist = (float*)malloc(sizeof(float) * (size_t)n * g);
+  float* norms = (float*)malloc(sizeof(float) * (size_t)n);
+  for (int64_t i = 0; i < n * (int64_t)g; ++i) {
+    graph[i] = INVALID_ID;
+    gdist[i] = INFINITY;
+  }
+  for (int64_t i = 0; i < n; ++i) norms[i] = sq_norm(data + i * d, d);
+
+  if (n <= 50000) {
+    /* Exact all-pairs seeding (:324-349), one row at a time. */
+#pragma omp parallel num_threads(nt)
+    {
+      float* key = (float*)malloc(sizeof(float) * (size_t)n);
+      uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+#pragma omp for schedule(dynamic, 8)
+      for (int64_t i = 0; i < n; ++i) {
+        const float ni = norms[i];
+        for (int64_t a = 0; a < n; ++a) key[a] = ni - 2.f * dot_blk(data + i * d, data + a * d, d) + norms[a];
+        for (int64_t a = 0; a < n; ++a) idx[a] = (uint32_t)a;
+        idx[i] = idx[n - 1];
+        const int64_t take = (int64_t)g < n - 1 ? (int64_t)g : n - 1;
+        select_smallest(idx, n - 1, take, key);
+        for (int64_t k = 0; k < take; ++k) insert_neighbor(graph, gdist, g, i, idx[k], key[idx[k]]);
+      }
+      free(key);
+      free(idx);
+    }
+  } else {
+    /* IVF k-means seeding (:351-435). */
+    int64_t K = (int64_t)sqrt((double)n);
+    if (K < (int64_t)g + 1) K = (int64_t)g + 1;
+    if (K > 2000) K = 2000;
+    float* cent = (float*)malloc(sizeof(float) * (size_t)(K * d));
+    const double stride = (double)n / (double)K;
+    for (int64_t k = 0; k < K; ++k) {
+      int64_t ix = (int64_t)((double)k * stride + stride * 0.5);
+      if (ix > n - 1) ix = n - 1;
+      memcpy(cent + k * d, data + ix * d, sizeof(float) * (size_t)d);
+    }
+    uint32_t* assign = (uint32_t*)calloc((size_t)n, sizeof(uint32_t));
+    float* cn = (float*)malloc(sizeof(float) * (size_t)K);
+    int64_t* counts = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+    for (int iter = 0; iter < 20; ++iter) {
+      for (int64_t k = 0; k < K; ++k) cn[k] = sq_norm(cent + k * d, d);
+      int changed = iter == 0;
+#pragma omp parallel for schedule(static) num_threads(nt) reduction(| : changed)
+      for (int64_t i = 0; i < n; ++i) {
+        const float ni = norms[i];
+        float best_d = INFINITY;
+        uint32_t best_k = 0;
+        for (int64_t k = 0; k < K; ++k) {
+          const float dd = ni - 2.f * dot_blk(data + i * d, cent + k * d, d) + cn[k];
+          if (dd < best_d) {
+            best_d = dd;
+            best_k = (uint32_t)k;
+          }
+        }
+        if (assign[i] != best_k) {
+          changed = 1;
+          assign[i] = best_k;
+        }
+      }
+      if (!changed) break;
+      /* M-step (:421-434): sums in row order, then scale by 1/count. */
+      memset(cent, 0, sizeof(float) * (size_t)(K * d));
+      memset(counts, 0, sizeof(int64_t) * (size_t)K);
+      for (int64_t i = 0; i < n; ++i) {
+        const uint32_t k = assign[i];
+        counts[k]++;
+        float* c = cent + (int64_t)k * d;
+        const float* x = data + i * d;
+        for (int64_t j = 0; j < d; ++j) c[j] += x[j];
+      }
+      for (int64_t k = 0; k < K; ++k)
+        if (counts[k] > 0) {
+          const float inv = 1.0f / (float)counts[k];
+          for (int64_t j = 0; j < d; ++j) cent[k * d + j] *= inv;
+        }
+    }
+    /* Cluster lists (:576-579) and the 3 nearest clusters (:583-611). */
+    int64_t* cstart = (int64_t*)calloc((size_t)K + 1, sizeof(int64_t));
+    uint32_t* members = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    for (int64_t i = 0; i < n; ++i) cstart[assign[i] + 1]++;
+    for (int64_t k = 0; k < K; ++k) cstart[k + 1] += cstart[k];
+    {
+      int64_t* fill = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+      for (int64_t k = 0; k < K; ++k) fill[k] = cstart[k];
+      for (int64_t i = 0; i < n; ++i) members[fill[assign[i]]++] = (uint32_t)i;
+      free(fill);
+    }
+    for (int64_t k = 0; k < K; ++k) cn[k] = sq_norm(cent + k * d, d);
+    const int64_t n_probe = K - 1 < 3 ? K - 1 : 3;
+    uint32_t* nearc = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(K * (n_probe > 0 ? n_probe : 1)));
+#pragma omp parallel num_threads(nt)
+    {
+      float* key = (float*)malloc(sizeof(float) * (size_t)K);
+      uint32_t* kidx = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)K);
+#pragma omp for schedule(static)
+      for (int64_t k = 0; k < K; ++k) {
+        for (int64_t a = 0; a < K; ++a) key[a] = cn[k] - 2.f * dot_blk(cent + k * d, cent + a * d, d) + cn[a];
+        for (int64_t a = 0; a < K; ++a) kidx[a] = (uint32_t)a;
+        kidx[k] = kidx[K - 1];
+        select_smallest(kidx, K - 1, n_probe, key);
+        for (int64_t t = 0; t < n_probe; ++t) nearc[k * n_probe + t] = kidx[t];
+      }
+      free(key);
+      free(kidx);
+    }
+    /* Exact per-cluster seeding (:712-792). */
+    const int64_t max_own = (n / K) * 4 + 64;
+#pragma omp parallel num_threads(nt)
+    {
+      uint32_t* probe = (uint32_t*)malloc(sizeof(uint32_t) * 8192);
+      float* key = (float*)malloc(sizeof(float) * 8192);
+      uint32_t* midx = (uint32_t*)malloc(sizeof(uint32_t) * 8192);
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t k = 0; k < K; ++k) {
+        const int64_t own_n = cstart[k + 1] - cstart[k];
+        if (own_n == 0) continue;
+        const uint32_t* own = members + cstart[k];
+        const int64_t nk = own_n < max_own ? own_n : max_own;
+        int64_t m = 0;
+        for (int64_t i = 0; i < nk && m < 8192; ++i) probe[m++] = own[i];
+        for (int64_t t = 0; t < n_probe; ++t) {
+          const uint32_t c = nearc[k * n_probe + t];
+          for (int64_t i = cstart[c]; i < cstart[c + 1] && m < 8192; ++i) probe[m++] = members[i];
+        }
+        if (m <= 1) continue;
+        const int64_t take = (int64_t)g < m - 1 ? (int64_t)g : m - 1;
+        for (int64_t i = 0; i < nk; ++i) {
+          const uint32_t vi = own[i];
+          const float ni = norms[vi];
+          for (int64_t p = 0; p < m; ++p) {
+            key[p] = probe[p] == vi ? INFINITY
+                                    : ni - 2.f * dot_blk(data + (int64_t)vi * d, data + (int64_t)probe[p] * d, d) +
+                                          norms[probe[p]];
+            midx[p] = (uint32_t)p;
+          }
+          select_smallest(midx, m, take, key);
+          for (int64_t t = 0; t < take; ++t) {
+            const uint32_t nb = probe[midx[t]];
+            if (nb == vi) continue;
+            insert_neighbor(graph, gdist, g, vi, nb, key[midx[t]]);
+          }
+        }
+      }
+      free(probe);
+      free(key);
+      free(midx);
+    }
+    free(cent);
+    free(assign);
+    free(cn);
+    free(counts);
+    free(cstart);
+    free(members);
+    free(nearc);
+
+    /* Random bucketing (:795-851; kernel shaders/cagra_kernels.metal:403-462). */
+    uint32_t* rperm = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    for (int64_t i = 0; i < n; ++i) rperm[i] = (uint32_t)i;
+    uint64_t r = 0xFEDCBA9876543210ULL;
+    for (int64_t i = n - 1; i > 0; --i) {
+      r = r * 6364136223846793005ULL + 1442695040888963407ULL;
+      const int64_t j = (int64_t)(r >> 33) % (i + 1);
+      const uint32_t tmp = rperm[i];
+      rperm[i] = rperm[j];
+      rperm[j] = tmp;
+    }
+    const int64_t rbsz = 256;
+    const uint32_t take = g < 64 ? g : 64;
+#pragma omp parallel for schedule(dynamic, 64) num_threads(nt)
+    for (int64_t v = 0; v < n; ++v) {
+      const int64_t start = (v / rbsz) * rbsz;
+      const int64_t end = start + rbsz < n ? start + rbsz : n;
+      const int64_t t = v - start;
+      const uint32_t vi = rperm[v];
+      float hd[64];
+      uint32_t hn[64];
+      for (uint32_t h = 0; h < take; ++h) {
+        hd[h] = INFINITY;
+        hn[h] = INVALID_ID;
+      }
+      for (int64_t b = 0; b < end - start; ++b) {
+        if (b == t) continue;
+        const uint32_t nb = rperm[start + b];
+        const float dist = l2_f4(data + (int64_t)vi * d, data + (int64_t)nb * d, d);
+        float worst = hd[0];
+        uint32_t wi = 0;
+        for (uint32_t h = 1; h < take; ++h)
+          if (hd[h] > worst) {
+            worst = hd[h];
+            wi = h;
+          }
+        if (dist < worst) {
+          hd[wi] = dist;
+          hn[wi] = nb;
+        }
+      }
+      for (uint32_t h = 0; h < take; ++h) {
+        if (hn[h] == INVALID_ID) continue;
+        insert_neighbor(graph, gdist, g, vi, hn[h], hd[h]);
+      }
+    }
+    free(rperm);
+  }
+
+  /* nn-descent (:853-911; kernel shaders/cagra_kernels.metal:334-395). */
+  uint32_t* snap = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n * g);
+  for (uint32_t iter = 0; iter < nd_iters; ++iter) {
+    memcpy(snap, graph, sizeof(uint32_t) * (size_t)n * g);
+    int any = 0;
+#pragma omp parallel for schedule(dynamic, 32) num_threads(nt) reduction(| : any)
+    for (int64_t node = 0; node < n; ++node) {
+      uint32_t* row = graph + node * g;
+      float* rowd = gdist + node * g;
+      const float* xv = data + node * d;
+      for (uint32_t gi = 0; gi < g; ++gi) {
+        const uint32_t nbr = row[gi];
+        if (nbr >= (uint32_t)n) continue;
+        const uint32_t* hop = snap + (int64_t)nbr * g;
+        for (uint32_t h0 = 0; h0 < g; h0 += 4) {
+          /* distances of up to four candidates, then the serial checks */
+          const float* bp[4];
+          uint32_t cand[4];
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t h = h0 + (uint32_t)c;
+            cand[c] = h < g ? hop[h] : INVALID_ID;
+            bp[c] = data + (cand[c] < (uint32_t)n ? (int64_t)cand[c] : 0) * d;
+          }
+          float dist4[4];
+          l2_f4_x4(xv, bp, d, dist4);
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t cd = cand[c];
+            if (cd >= (uint32_t)n || cd == (uint32_t)node) continue;
+            int present = 0;
+            for (uint32_t i = 0; i < g; ++i)
+              if (row[i] == cd) {
+                present = 1;
+                break;
+              }
+            if (present) continue;
+            float worst_d = 0.f;
+            uint32_t worst_g = g;
+            for (uint32_t i = 0; i < g; ++i)
+              if (rowd[i] > worst_d) {
+                worst_d = rowd[i];
+                worst_g = i;
+              }
+            if (worst_g < g && dist4[c] < worst_d) {
+              row[worst_g] = cd;
+              rowd[worst_g] = dist4[c];
+              any = 1;
+            }
+          }
+        }
+      }
+    }
+    if (!any) break;
+  }
+  free(snap);
+  free(gdist);
+  free(norms);
+  return 0;
+}

@@ -81,6 +81,27 @@ void oracle_cagra_search(const float* base, int64_t n, int64_t d, const uint32_t
 void oracle_knn_graph(const float* base, int64_t n, int64_t d, uint32_t g, uint32_t* out_graph,
                       int threads);
 
+/* ---- CAGRA build (oracle/cagra_build_oracle.c) -------------------------- */
+
+/* The reference's graph build for n <= 200,000 (src/cagra.cpp:47-59 ->
+ * src/metal_context.mm:289-914): G = min(graph_degree, n - 1); n <= 50,000:
+ * exact all-pairs seeding; otherwise IVF k-means (K = clamp(sqrt n, G+1,
+ * 2000), 20 iterations, stride initialisation), exact seeding of each
+ * cluster's rows against their own and the 3 nearest clusters' rows (at most
+ * 8,192), then one random bucketing pass (LCG Fisher-Yates, buckets of 256,
+ * top-min(G, 64) merged per row); then nn-descent for 20 (n <= 50,000) or 5
+ * iterations.  Writes n x G ids (UINT32_MAX for missing).  Cross products use
+ * a fixed 8-way summation where the reference calls cblas_sgemm; nn-descent
+ * reads other nodes' lists as of the start of each iteration (one legal
+ * schedule of the reference's racy kernel).  Returns 0, 1 on bad arguments,
+ * 2 for n > 200,000 (the PQ path is not restated).  Pinned: equals the exact
+ * kNN graph on integer data through the exact-seeding path; on the IVF path,
+ * rows are full, in range, free of self edges and hold most exact neighbours
+ * (tests/test_oracle_build.py).  Bit-exact graphs are parity unpinned (the
+ * reference's own result depends on a GPU race and on BLAS order). */
+int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
+                           uint32_t* out_graph, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -148,3 +148,29 @@ def test_argument_errors(ctx, oracle):
         ctx.cagra_index(np.ones((10, 1025), np.float32), g)
     with pytest.raises(ValueError):
         ctx.cagra_index(base, g, np.array([10], np.uint32))
+
+
+@pytest.mark.parametrize("n,d,q", [(60_000, 128, 500), (100_000, 1024, 1000)])
+def test_recall_on_reference_built_graph(ctx, cvs, oracle, n, d, q):
+    """The graph-search gate on the reference's own graph: the restated
+    reference build (IVF seeding + random bucketing + 5 nn-descent
+    iterations, the reference's path for 50,000 < N <= 200,000) of the
+    benchmark distribution (64 centres, sigma 0.3, L2-normalised), degree
+    64, itopk 64.  GPU search recall@10 (search_width 1 and 4) must be at
+    least the restated reference search's; the second case is the full
+    N=100,000 D=1024 configuration."""
+    base = cvs.synth_clustered(12345, cvs.STREAM_BASE, n, d)
+    qs = cvs.synth_clustered(12345, cvs.STREAM_QUERIES, q, d)
+    graph = oracle.cagra_build_reference(base, 64, threads=16)
+    nav = oracle.cagra_nav_nodes(n)
+    gt, _ = oracle.bf_exact(base, qs, 10, threads=16)
+    ref, _ = oracle.cagra_reference_search(base, graph, nav, qs, 10, itopk_size=64, threads=16)
+    r_ref = recall(ref, gt, 10)
+    idx = ctx.cagra_index(base, graph, nav)
+    for width in (1, 4):
+        nbr, dist = idx.search(qs, 10, itopk_size=64, search_width=width)
+        check_invariants(base, qs, nbr, dist)
+        r_gpu = recall(nbr, gt, 10)
+        print(f"N={n} D={d} reference-built graph, width {width}: recall@10 gpu {r_gpu:.4f} "
+              f"restated reference {r_ref:.4f}")
+        assert r_gpu >= r_ref - 0.01
