@@ -30,7 +30,7 @@ CVS_ERR_OUT_OF_MEMORY = 4
 CVS_ERR_UNSUPPORTED = 5
 
 BF_MAX_DIM = 1024
-BF_MAX_K = 48
+BF_MAX_K = 112
 CAGRA_MAX_DIM = 1024
 CAGRA_MAX_ITOPK = 256
 CAGRA_MAX_WIDTH = 16

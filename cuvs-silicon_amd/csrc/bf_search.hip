@@ -35,6 +35,7 @@
 // (src/cagra.cpp:218-226) up to summation order.  kp > k candidates are kept
 // because fp16 inputs perturb |q-x|^2 by up to ~1e-4 absolute at unit norm,
 // far below the gap between rank k and rank kp on the target data.
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -74,14 +75,19 @@ struct Cfg {
   static_assert(KS >= 2 && KS <= 64, "k-steps per tile");
 };
 
-// LDS list geometry per kp.  A query can receive 2 lanes x H keys between
-// two overflow checks (H rows per lane); lists keep that much room.
+// List geometry per kp.  A query can receive 2 lanes x H keys between two
+// overflow checks (H rows per lane); lists keep that much room.  Lists of
+// kp <= 64 live in LDS; kp = 128 lists (large k) live in global memory, one
+// per (query, workgroup), since 128 queries x 192 keys exceed the LDS budget
+// and appends are rare once the sampled threshold is in place.
 template <int KP, int MODE>
 struct Lists {
-  static constexpr int H = KP <= 32 ? 16 : 8;  // rows per lane between checks
-  // Beyond kp + 2H, the slack (32, 24, 8 keys) sets how many pushes one
-  // compaction is amortized over; bounded by the 160 KiB LDS budget.
-  static constexpr int CAP = MODE != 0 ? 1 : (KP == 16 ? 80 : 88);
+  static constexpr bool GL = MODE == 0 && KP > 64;  // lists in global memory
+  static constexpr int H = KP <= 32 ? 16 : 8;      // rows per lane between checks
+  // Beyond kp + 2H, the slack (32, 24, 8, 48 keys) sets how many pushes one
+  // compaction is amortized over; LDS lists are bounded by the 160 KiB budget.
+  static constexpr int CAP = MODE != 0 ? 1 : (KP == 16 ? 80 : (KP <= 64 ? 88 : 192));
+  static constexpr int NS = (CAP + 63) / 64;  // list entries per lane in a compaction
   static_assert(MODE != 0 || CAP >= KP + 2 * H + 8, "list slack");
 };
 
@@ -95,46 +101,63 @@ struct ScanArgs {
   int n_qtiles;         // number of 32-query tiles
   int kp;               // candidates kept per (workgroup, query)
   const float* thr0;    // per-query initial threshold (scan mode)
-  uint64_t* part;       // scan: [nq][gridDim.x][kp] keys
+  uint64_t* part;       // scan: [nq][n_ranges][kp] keys (LDS lists) or
+                        // [nq][n_ranges][CAP] lists, first kp valid (global lists)
+  int n_ranges;         // dataset ranges (workgroups along N)
+  int n_qblocks;        // 128-query blocks
+  int qb_fast;          // 1: linear block id = range * n_qblocks + qblock
   float* sdist;         // sample: [nq][s_rows] approximate distances
   int64_t s_units;      // sample: number of sampled units
   int64_t s_stride;     // sample: unit stride
   int64_t s_rows;       // sample: rows per query = s_units * RPU
 };
 
-// Compacts the LDS list of one query to its kp smallest keys and lowers the
+// Compacts the list of one query to its kp smallest keys and lowers the
 // query's threshold to the kp-th distance.  All 64 lanes take part (the list
-// pointer is wave-uniform); entry e lives in lane e % 64 (CAP <= 128).
+// pointer is wave-uniform); entry e lives in lane e % 64, slot e / 64
+// (CAP <= 64 * NS).
+template <int NS>
 __device__ __forceinline__ void compact_query(uint64_t* list, uint32_t* cnt_slot, float* thr_slot,
                                               int kp) {
   const int lane = __lane_id();
   const uint32_t cnt = *cnt_slot;
   if (cnt <= uint32_t(kp)) return;
-  const bool v0 = uint32_t(lane) < cnt, v1 = uint32_t(lane + 64) < cnt;
-  const uint64_t k0 = v0 ? list[lane] : kSentinel;
-  const uint64_t k1 = v1 ? list[lane + 64] : kSentinel;
-  const uint32_t h0 = uint32_t(k0 >> 32), h1 = uint32_t(k1 >> 32);
-  const uint32_t l0 = uint32_t(k0), l1 = uint32_t(k1);
+  bool v[NS];
+  uint64_t k[NS];
+  uint32_t h[NS], l[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    v[s] = uint32_t(lane + 64 * s) < cnt;
+    k[s] = v[s] ? list[lane + 64 * s] : kSentinel;
+    h[s] = uint32_t(k[s] >> 32);
+    l[s] = uint32_t(k[s]);
+  }
   int need = kp;
   uint32_t pre = 0;
   for (int b = 31; b >= 0; --b) {
-    const int c = popc(__ballot(v0 && ((h0 ^ pre) >> b) == 0)) +
-                  popc(__ballot(v1 && ((h1 ^ pre) >> b) == 0));
+    int c = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && ((h[s] ^ pre) >> b) == 0));
     if (c < need) {
       need -= c;
       pre |= 1u << b;
     }
   }
   const uint32_t kth_hi = pre;
-  const int lt = popc(__ballot(v0 && h0 < kth_hi)) + popc(__ballot(v1 && h1 < kth_hi));
-  const int eq = popc(__ballot(v0 && h0 == kth_hi)) + popc(__ballot(v1 && h1 == kth_hi));
+  int lt = 0, eq = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    lt += popc(__ballot(v[s] && h[s] < kth_hi));
+    eq += popc(__ballot(v[s] && h[s] == kth_hi));
+  }
   uint32_t kth_lo = 0xffffffffu;
   if (eq > kp - lt) {  // ties on the distance word: select on the row id
     int need2 = kp - lt;
     uint32_t pre2 = 0;
     for (int b = 31; b >= 0; --b) {
-      const int c = popc(__ballot(v0 && h0 == kth_hi && ((l0 ^ pre2) >> b) == 0)) +
-                    popc(__ballot(v1 && h1 == kth_hi && ((l1 ^ pre2) >> b) == 0));
+      int c = 0;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && h[s] == kth_hi && ((l[s] ^ pre2) >> b) == 0));
       if (c < need2) {
         need2 -= c;
         pre2 |= 1u << b;
@@ -142,11 +165,14 @@ __device__ __forceinline__ void compact_query(uint64_t* list, uint32_t* cnt_slot
     }
     kth_lo = pre2;
   }
-  const bool keep0 = v0 && (h0 < kth_hi || (h0 == kth_hi && l0 <= kth_lo));
-  const bool keep1 = v1 && (h1 < kth_hi || (h1 == kth_hi && l1 <= kth_lo));
-  const uint64_t m0 = __ballot(keep0), m1 = __ballot(keep1);
-  if (keep0) list[mbcnt(m0)] = k0;
-  if (keep1) list[popc(m0) + mbcnt(m1)] = k1;
+  int base = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool keep = v[s] && (h[s] < kth_hi || (h[s] == kth_hi && l[s] <= kth_lo));
+    const uint64_t m = __ballot(keep);
+    if (keep) list[base + mbcnt(m)] = k[s];
+    base += popc(m);
+  }
   if (lane == 0) {
     *cnt_slot = uint32_t(kp);
     *thr_slot = unord_f32(kth_hi);
@@ -167,14 +193,21 @@ void bf_scan_kernel(ScanArgs a) {
   __shared__ float s_dn[2][NF];
   __shared__ uint32_t s_cnt[kQB];
   __shared__ float s_thr[kQB];
-  __shared__ uint64_t s_buf[kQB * CAP];
+  __shared__ uint64_t s_buf[L::GL ? 1 : kQB * CAP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int G = gridDim.x;
-  const int x = blockIdx.x;
-  const int qbase = blockIdx.y * kQB;
+  const int G = a.n_ranges;
+  const int x = a.qb_fast ? int(blockIdx.x) / a.n_qblocks : int(blockIdx.x);
+  const int qbase = (a.qb_fast ? int(blockIdx.x) % a.n_qblocks : int(blockIdx.y)) * kQB;
+  // List of this workgroup's query slot m (0..127).
+  auto list_of = [&](int m) CVS_INLINE -> uint64_t* {
+    if constexpr (L::GL)
+      return a.part + (int64_t(qbase + m) * G + x) * CAP;
+    else
+      return s_buf + m * CAP;
+  };
 
   // Units of this workgroup: contiguous (scan) or a strided sample (sample).
   const int64_t total = MODE == kModeScan ? a.n_units : a.s_units;
@@ -274,7 +307,8 @@ void bf_scan_kernel(ScanArgs a) {
       const int i = __builtin_ctzll(over);
       over &= over - 1;
       const int m = wave * 32 + i;
-      compact_query(s_buf + m * CAP, &s_cnt[m], &s_thr[m], KP);
+      if constexpr (L::GL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      compact_query<L::NS>(list_of(m), &s_cnt[m], &s_thr[m], KP);
     }
     thr = fminf(thr, s_thr[qw]);
   };
@@ -304,7 +338,7 @@ void bf_scan_kernel(ScanArgs a) {
       for (int r = h; r < h + H; ++r) {
         if (hp & (1u << (r - h))) {
           const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
-          s_buf[qw * CAP + slot] = (uint64_t(ord_f32(dv[r])) << 32) | row;
+          list_of(qw)[slot] = (uint64_t(ord_f32(dv[r])) << 32) | row;
           ++slot;
         }
       }
@@ -531,14 +565,20 @@ void bf_scan_kernel(ScanArgs a) {
 
   if (MODE == kModeScan) {
     compact_wave(uint32_t(KP));
-    const int64_t G64 = G;
     for (int i = 0; i < 32; ++i) {
       const int m = wave * 32 + i;
       const int q = qbase + m;
       if (q >= a.nq) break;
       const uint32_t c = s_cnt[m];
-      for (int e = lane; e < KP; e += 64)
-        a.part[(int64_t(q) * G64 + x) * KP + e] = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
+      if constexpr (L::GL) {
+        // In place: the first kp entries of the global list, sentinel-padded.
+        uint64_t* lst = list_of(m);
+        for (int e = lane; e < KP; e += 64)
+          if (uint32_t(e) >= c) lst[e] = kSentinel;
+      } else {
+        for (int e = lane; e < KP; e += 64)
+          a.part[(int64_t(q) * G + x) * KP + e] = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
+      }
     }
   }
 }
@@ -589,24 +629,25 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
 // Merge + exact re-rank: one workgroup per query.
 template <int EPT>
 __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restrict__ part,
-                                                       int m_keys, int kp,
+                                                       int m_keys, int kp, int n_ranges, int stride,
                                                        const float* __restrict__ rows, int64_t d,
                                                        const float* __restrict__ queries, int64_t k,
                                                        uint32_t* __restrict__ out_nbr,
                                                        float* __restrict__ out_dist) {
   __shared__ int s_red[2 * kWaves];
   __shared__ int s_n;
-  __shared__ uint64_t s_sel[64];
-  __shared__ float s_ex[64];
+  __shared__ uint64_t s_sel[128];
+  __shared__ float s_ex[128];
   const int tid = threadIdx.x;
   const int64_t q = blockIdx.x;
-  const uint64_t* src = part + q * int64_t(m_keys);
+  // Key e is entry e % kp of range e / kp's list, stride keys apart.
+  const uint64_t* src = part + q * int64_t(n_ranges) * stride;
 
   uint32_t hi[EPT], lo[EPT];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = tid + i * kThreads;
-    const uint64_t key = e < m_keys ? src[e] : kSentinel;
+    const uint64_t key = e < m_keys ? src[int64_t(e / kp) * stride + e % kp] : kSentinel;
     hi[i] = uint32_t(key >> 32);
     lo[i] = uint32_t(key);
   }
@@ -651,7 +692,7 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
     const uint64_t key = (uint64_t(hi[i]) << 32) | lo[i];
     if (key <= kth && key != kSentinel) {
       const int p = atomicAdd(&s_n, 1);
-      if (p < 64) s_sel[p] = key;
+      if (p < 128) s_sel[p] = key;
     }
   }
   __syncthreads();
@@ -720,7 +761,8 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
 int choose_kp(int64_t k) {
   if (k <= 10) return 16;
   if (k <= 24) return 32;
-  return 64;
+  if (k <= 48) return 64;
+  return 128;
 }
 
 template <int KS, int KP>
@@ -742,6 +784,7 @@ void launch_scan_ks(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode)
     case 16: launch_scan_kp<KS, 16>(ctx, grid, args, mode); break;
     case 32: launch_scan_kp<KS, 32>(ctx, grid, args, mode); break;
     case 64: launch_scan_kp<KS, 64>(ctx, grid, args, mode); break;
+    case 128: launch_scan_kp<KS, 128>(ctx, grid, args, mode); break;
     default: fail(CVS_ERR_RUNTIME, "unsupported candidate count");
   }
 }
@@ -794,15 +837,24 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   const int ks = int(ds->dp / kStepCols);
   const int rpu = 2 * kStageBlocks * 32 / ks;  // rows per unit
   const int64_t n_units = ds->n_tiles * ks / (2 * kStageBlocks);
-  int G = ctx->compute_units;
-  if (G > 256) G = 256;
-  if (int64_t(G) > n_units) G = int(n_units);
   const int kp = choose_kp(k);
   const int64_t q_tiles = (q + 31) / 32;
   const unsigned qblocks = unsigned((q + kQB - 1) / kQB);
+  const bool global_lists = kp > 64;
+  // Dataset ranges (workgroups along N): one per compute unit, at most 128
+  // with kp = 128 (the merge selects from <= 16,384 keys per query), and 32
+  // for large batches, whose 128-query blocks then run range-major so that
+  // the blocks sharing a range stream it together through L2 / MALL.
+  const bool large_batch = qblocks > 8;
+  int G = ctx->compute_units;
+  if (G > 256) G = 256;
+  if (global_lists && G > 128) G = 128;
+  if (large_batch && G > 32) G = 32;
+  if (int64_t(G) > n_units) G = int(n_units);
+  const int stride = global_lists ? Lists<128, kModeScan>::CAP : kp;
 
-  // Sample: ~256*kp rows in whole units, evenly strided.
-  int64_t s_units = (256 * int64_t(kp)) / rpu;
+  // Sample: ~256*kp rows (at most 16,384) in whole units, evenly strided.
+  int64_t s_units = std::min<int64_t>(256 * int64_t(kp), 16384) / rpu;
   if (s_units < 1) s_units = 1;
   if (s_units > n_units) s_units = n_units;
   const int64_t s_stride = n_units / s_units;
@@ -822,7 +874,7 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   float* thr0 = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes);
   float* sdist = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes);
   const int m_keys = G * kp;
-  ctx->ws_partial.reserve(size_t(q) * size_t(m_keys) * sizeof(uint64_t));
+  ctx->ws_partial.reserve(size_t(q) * size_t(G) * size_t(stride) * sizeof(uint64_t));
   uint64_t* part = ctx->ws_partial.as<uint64_t>();
 
   hipEvent_t t0 = timer_begin(ctx, "bf_prep");
@@ -845,7 +897,11 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   args.s_stride = s_stride;
   args.s_rows = s_rows;
 
+  args.n_qblocks = int(qblocks);
+
   hipEvent_t t1 = timer_begin(ctx, "bf_sample");
+  args.n_ranges = Gs;
+  args.qb_fast = 0;
   launch_scan(ctx, ks, dim3(unsigned(Gs), qblocks), args, kModeSample);
   launch_by_ept<SelectK>((s_rows + kThreads - 1) / kThreads, dim3(unsigned(q)), ctx->stream,
                          static_cast<const float*>(sdist), s_rows, kp, thr0);
@@ -853,12 +909,15 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   timer_end(ctx, "bf_sample", t1);
 
   hipEvent_t t2 = timer_begin(ctx, "bf_scan");
-  launch_scan(ctx, ks, dim3(unsigned(G), qblocks), args, kModeScan);
+  args.n_ranges = G;
+  args.qb_fast = large_batch ? 1 : 0;
+  launch_scan(ctx, ks, large_batch ? dim3(unsigned(G) * qblocks, 1) : dim3(unsigned(G), qblocks), args,
+              kModeScan);
   timer_end(ctx, "bf_scan", t2);
 
   hipEvent_t t3 = timer_begin(ctx, "bf_merge");
   launch_by_ept<MergeK>((m_keys + kThreads - 1) / kThreads, dim3(unsigned(q)), ctx->stream,
-                        static_cast<const uint64_t*>(part), m_keys, kp,
+                        static_cast<const uint64_t*>(part), m_keys, kp, G, stride,
                         static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   after_launch("bf_merge_kernel");
   timer_end(ctx, "bf_merge", t3);

@@ -49,7 +49,7 @@ typedef struct cvs_cagra_index cvs_cagra_index; /* device-resident graph index (
 
 /* Limits of the fused brute-force kernel (checked by cvs_bf_search*). */
 #define CVS_BF_MAX_DIM 1024
-#define CVS_BF_MAX_K 48
+#define CVS_BF_MAX_K 112
 
 /* Limits of the graph search kernel (checked by cvs_cagra_search*). */
 #define CVS_CAGRA_MAX_DIM 1024

@@ -96,7 +96,11 @@ def test_reference_golden(ctx, oracle, name):
     (1, 1, 1, 1),
     (7, 5, 3, 10),        # k > n: padded slots
     (100, 64, 130, 10),   # two query blocks
-    (1000, 96, 17, 48),   # largest k
+    (1000, 96, 17, 48),   # largest k of the LDS lists
+    (1000, 96, 17, 49),   # smallest k of the global-memory lists (kp = 128)
+    (20000, 128, 300, 100),
+    (3000, 64, 40, 112),  # largest k
+    (100, 32, 5, 112),    # k > n with global-memory lists
     (5000, 256, 33, 24),
     (2000, 1024, 5, 1),
     (3333, 1000, 9, 16),  # d not a power of two
@@ -106,6 +110,19 @@ def test_random_shapes(ctx, oracle, n, d, q, k):
     rng = np.random.default_rng(n * 31 + d)
     base = rng.standard_normal((n, d)).astype(np.float32)
     qs = rng.standard_normal((q, d)).astype(np.float32)
+    check_against_oracle(ctx, oracle, base, qs, k)
+
+
+@pytest.mark.parametrize("n,d,q,k", [
+    (30000, 64, 1500, 10),    # > 8 query blocks: range-major launch, LDS lists
+    (30000, 64, 1500, 100),   # range-major launch, global-memory lists
+    (8000, 1024, 1100, 64),
+])
+def test_large_batches(ctx, oracle, n, d, q, k):
+    rng = np.random.default_rng(q + k)
+    centers = rng.standard_normal((32, d)).astype(np.float32)
+    base = centers[rng.integers(0, 32, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
+    qs = centers[rng.integers(0, 32, q)] + 0.3 * rng.standard_normal((q, d)).astype(np.float32)
     check_against_oracle(ctx, oracle, base, qs, k)
 
 
@@ -163,7 +180,7 @@ def test_argument_errors(ctx):
     with pytest.raises(ValueError):
         ds.bf_search(np.ones((2, 4), np.float32), 0)
     with pytest.raises(ValueError):
-        ds.bf_search(np.ones((2, 4), np.float32), 49)
+        ds.bf_search(np.ones((2, 4), np.float32), 113)
     with pytest.raises(ValueError):
         ds.bf_search(np.ones((2, 5), np.float32), 3)
     with pytest.raises(ValueError):
@@ -186,6 +203,20 @@ def exact_topk_numpy(base, qs, k, extra=64):
         o = np.lexsort((c, d))[:k + 1]
         out_i[i], out_d[i] = c[o], d[o]
     return out_i, out_d
+
+
+def test_c3_full_size_large_batch(ctx, cvs):
+    """N=1,000,000, D=1024, Q=10,000, K=100 in one call: ids and distances
+    of 200 sampled queries against the exact ground truth (same gates)."""
+    n, d, q, k = 1_000_000, 1024, 10_000, 100
+    base = cvs.synth_clustered(12345, cvs.STREAM_BASE, n, d)
+    qs = cvs.synth_clustered(12345, cvs.STREAM_QUERIES, q, d)
+    nbr, dist = ctx.dataset(base).bf_search(qs, k)
+    sample = np.random.default_rng(0).choice(q, 200, replace=False)
+    gt_i, gt_d = exact_topk_numpy(base, qs[sample], k)
+    assert_parity(nbr[sample], dist[sample], gt_i.astype(np.uint32), gt_d, k)
+    recall = np.mean([len(set(nbr[s].tolist()) & set(gt_i[j, :k].tolist())) / k for j, s in enumerate(sample)])
+    assert recall >= 0.999, recall
 
 
 def test_c2_full_size_recall(ctx, cvs):
