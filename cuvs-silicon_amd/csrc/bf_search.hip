@@ -8,12 +8,15 @@
 //
 // Here the cross matrix never leaves registers.  Five launches per batch:
 //
-//  prep     queries fp32 -> fp16 32-row tiles + norms (the dataset layout).
-//  sample   the scan kernel over a strided sample of ~256*kp rows, writing
-//           every approximate query/row distance of the sample.
-//  select   per query, the kp-th smallest sampled distance T0.  At least kp
-//           dataset rows lie at or below T0, so T0 bounds the global kp-th
-//           distance and every row above it can be dropped by the scan.
+//  prep     queries fp32 -> fp16 32-row tiles + norms (the dataset layout),
+//           one wave per query.
+//  sample   the scan kernel over a strided sample of ~256*kp rows (at most
+//           16,384); each lane keeps the minimum distance of the rows it
+//           sees, so every (query, workgroup, half-wave) yields one minimum.
+//  select   per query (one wave), the kp-th smallest of those minima, T0.
+//           The kp smallest minima are kp distinct dataset rows, so at least
+//           kp rows lie at or below T0 and every row above it can be dropped
+//           by the scan.
 //  scan     one persistent workgroup per compute unit streams a contiguous
 //           range of fp16 tiles HBM -> VGPRs -> LDS (double-buffered LDS, two
 //           stages of loads in flight).  Each wave keeps the fp16 operands of
@@ -21,14 +24,20 @@
 //           dataset tile is the A operand of v_mfma_f32_32x32x16_f16 (fp32
 //           accumulate, two accumulation chains), so each lane owns one query
 //           and 16 rows of the 32x32 result.  The epilogue forms
-//           d = |q|^2 + |x|^2 - 2 q.x and appends (d, row) to the query's LDS
-//           list only if d is below the query's threshold (T0 at start).  A
-//           list that nears capacity is compacted by its wave to the kp
-//           smallest keys (ballot radix select), lowering the threshold.
-//  merge    one workgroup per query selects the kp smallest keys of all
-//           per-workgroup lists, re-ranks them with exact fp32 distances from
-//           the fp32 rows, sorts by (distance, id) and writes k results,
-//           padding with UINT32_MAX / +inf (src/cagra.cpp:240-251).
+//           d = |q|^2 + |x|^2 - 2 q.x and appends (d, row) to the query's list
+//           only if d is below the query's threshold (T0 at start).  A list
+//           that nears capacity is compacted by its wave to the kp smallest
+//           keys (ballot radix select), lowering the threshold.  Lists of
+//           kp <= 64 live in LDS, kp = 128 lists in global memory.  Each list
+//           ends with its smallest key published for the merge.
+//  merge    one workgroup per query: the kp-th smallest list minimum
+//           bounds the kp-th smallest key; each wave streams a quarter of the
+//           lists and merges every 64-key row holding a key within the bound
+//           into its running top-kp (whose kp-th key tightens the bound); the
+//           four lists are merged, the kp candidates re-ranked with exact
+//           fp32 distances from the fp32 rows, sorted by (distance, id), and
+//           k results written, padded with UINT32_MAX / +inf
+//           (src/cagra.cpp:240-251).
 //
 // The fp16 pass only *selects*; reported distances come from the fp32
 // re-rank, so distances agree with the reference's fp32 loop
@@ -106,10 +115,10 @@ struct ScanArgs {
   int n_ranges;         // dataset ranges (workgroups along N)
   int n_qblocks;        // 128-query blocks
   int qb_fast;          // 1: linear block id = range * n_qblocks + qblock
-  float* sdist;         // sample: [nq][s_rows] approximate distances
+  float* sgmin;         // sample: [nq][2 * n_ranges] minima of each lane's sampled rows
+  uint64_t* lmin;       // scan: [nq][n_ranges] smallest key of each list (sentinel if empty)
   int64_t s_units;      // sample: number of sampled units
   int64_t s_stride;     // sample: unit stride
-  int64_t s_rows;       // sample: rows per query = s_units * RPU
 };
 
 // Compacts the list of one query to its kp smallest keys and lowers the
@@ -184,7 +193,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 void bf_scan_kernel(ScanArgs a) {
   using C = Cfg<KS>;
   using L = Lists<KP, MODE>;
-  constexpr int TPS = C::TPS, SPT = C::SPT, RPU = C::RPU, NF = C::NF;
+  constexpr int TPS = C::TPS, SPT = C::SPT, NF = C::NF;
   constexpr int CAP = L::CAP;
   // Scans over 32 or 64 k-steps per tile run the software-pipelined loop.
   constexpr bool PIPE = MODE == kModeScan && KS >= 32;
@@ -290,6 +299,7 @@ void bf_scan_kernel(ScanArgs a) {
   const float qn = q_ok ? a.qnorms[my_q] : INFINITY;
   const int qw = wave * 32 + (lane & 31);  // this lane's query slot in the workgroup
   float thr = -INFINITY;
+  float smin = INFINITY;  // sample mode: minimum over this lane's rows
   if (MODE == kModeScan) {
     if (q_ok) thr = nextafterf(a.thr0[my_q], INFINITY);
     for (int i = tid; i < kQB; i += kThreads) {
@@ -359,19 +369,14 @@ void bf_scan_kernel(ScanArgs a) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) dn4[g] = *reinterpret_cast<const f32x4*>(dn + 8 * g + 4 * (lane >> 5));
     if (MODE == kModeSample) {
-      if (q_ok) {
-        const int64_t i = i0 + (j >> 1);
-        const int64_t srow0 = i * RPU + (row0 - unit_of(i) * RPU);
+      // Running minimum over this lane's sampled rows (padding rows are +inf).
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f32x4 d;
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            d[e] = qn + dn4[g][e] - 2.0f * (acc0[4 * g + e] + acc1[4 * g + e]);
-          *reinterpret_cast<f32x4*>(a.sdist + int64_t(my_q) * a.s_rows + srow0 + 8 * g +
-                                    4 * (lane >> 5)) = d;
-        }
-      }
+        for (int e = 0; e < 4; ++e)
+          smin = fminf(smin, qn + dn4[g][e] - 2.0f * (acc0[4 * g + e] + acc1[4 * g + e]));
+      (void)row0;
+      (void)j;
     } else {
       // Branch-free pass mask over the 16 rows, then the rare append.
       float dv[16];
@@ -563,195 +568,275 @@ void bf_scan_kernel(ScanArgs a) {
     commit(dv, pass, ((stage_of(0) + n_stages) / SPT - 1) * 32);
   }
 
+  if (MODE == kModeSample) {
+    // One minimum per (query, workgroup, half-wave): 2 * n_ranges per query.
+    if (q_ok) a.sgmin[int64_t(my_q) * (2 * G) + 2 * x + (lane >> 5)] = smin;
+  }
   if (MODE == kModeScan) {
     compact_wave(uint32_t(KP));
+    if constexpr (L::GL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
     for (int i = 0; i < 32; ++i) {
       const int m = wave * 32 + i;
       const int q = qbase + m;
       if (q >= a.nq) break;
       const uint32_t c = s_cnt[m];
+      uint64_t mn = kSentinel;
       if constexpr (L::GL) {
         // In place: the first kp entries of the global list, sentinel-padded.
         uint64_t* lst = list_of(m);
-        for (int e = lane; e < KP; e += 64)
-          if (uint32_t(e) >= c) lst[e] = kSentinel;
+        for (int e = lane; e < KP; e += 64) {
+          if (uint32_t(e) >= c)
+            lst[e] = kSentinel;
+          else
+            mn = lst[e] < mn ? lst[e] : mn;
+        }
       } else {
-        for (int e = lane; e < KP; e += 64)
-          a.part[(int64_t(q) * G + x) * KP + e] = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
+        for (int e = lane; e < KP; e += 64) {
+          const uint64_t key = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
+          a.part[(int64_t(q) * G + x) * KP + e] = key;
+          mn = key < mn ? key : mn;
+        }
       }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t y = shfl_xor_u64(mn, o);
+        mn = y < mn ? y : mn;
+      }
+      if (lane == 0) a.lmin[int64_t(q) * G + x] = mn;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Block-wide helpers (256 threads).
+// Queries fp32 -> fp16 tiles (the dataset's tile layout) + squared norms of
+// the fp16-rounded rows, one wave per query: lane l converts columns
+// [16*l', 16*l'+16) for l' = l, l+64, ...; the norm is a fixed-order wave
+// reduction.  Rows of the last tile beyond q are zero with norm +inf.
 // ---------------------------------------------------------------------------
-// Sum over the block; `phase` alternates the reduction buffer so that one
-// barrier per call suffices.
-__device__ __forceinline__ int block_sum(int v, int* s_red, int phase) {
+__global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restrict__ queries, int64_t q,
+                                                          int64_t d, int ksteps, int64_t q_rows,
+                                                          u32x4* __restrict__ qtiles, float* __restrict__ qnorms) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (r >= q_rows) return;
+  const bool ok = r < q;
+  const float* src = queries + (ok ? r : 0) * d;
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0;
+  const int64_t t = r >> 5;
+  float acc = 0.f;
+  for (int s = lane; s < ksteps; s += 64) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  if ((threadIdx.x & 63) == 0) s_red[phase * kWaves + (threadIdx.x >> 6)] = v;
-  __syncthreads();
-  return s_red[phase * kWaves + 0] + s_red[phase * kWaves + 1] + s_red[phase * kWaves + 2] +
-         s_red[phase * kWaves + 3];
+    for (int hpart = 0; hpart < 2; ++hpart) {
+      const int64_t c0 = int64_t(s) * kStepCols + 8 * hpart;
+      float v[8];
+      if (ok && vec && c0 + 8 <= d) {
+        const float4 x = *reinterpret_cast<const float4*>(src + c0);
+        const float4 y = *reinterpret_cast<const float4*>(src + c0 + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (ok && c0 + j < d) ? src[c0 + j] : 0.f;
+      }
+      _Float16 h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        h[j] = static_cast<_Float16>(v[j]);
+        const float hv = static_cast<float>(h[j]);
+        acc += hv * hv;
+      }
+      u32x4 packed;
+      __builtin_memcpy(&packed, h, sizeof(packed));
+      // tile t, k-step s, lane (row % 32) + 32 * hpart
+      qtiles[(t * ksteps + s) * 64 + (r & 31) + 32 * hpart] = packed;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) qnorms[r] = ok ? acc : INFINITY;
 }
 
-// kp-th smallest sampled distance per query -> initial scan threshold.
-template <int EPT>
-__global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict__ sdist,
-                                                        int64_t s_rows, int kp,
+// ---------------------------------------------------------------------------
+// Initial scan threshold per query: the kp-th smallest of the sample minima.
+// Any kp minima belong to kp distinct dataset rows, so at least kp rows lie
+// at or below it.  One wave per query (m <= 512 minima, 8 per lane), ballot
+// radix select on the order-preserving integer image.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict__ sgmin, int m, int kp, int nq,
                                                         float* __restrict__ thr0) {
-  __shared__ int s_red[2 * kWaves];
-  const int tid = threadIdx.x;
-  const float* src = sdist + int64_t(blockIdx.x) * s_rows;
-  uint32_t v[EPT];
+  const int lane = threadIdx.x & 63;
+  const int q = int(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (q >= nq) return;
+  const float* src = sgmin + int64_t(q) * m;
+  uint32_t v[8];
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const int64_t e = tid + int64_t(i) * kThreads;
-    v[i] = e < s_rows ? ord_f32(src[e]) : 0xffffffffu;
+  for (int i = 0; i < 8; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < m ? ord_f32(src[e]) : 0xffffffffu;
+  }
+  if (m < kp) {
+    if (lane == 0) thr0[q] = INFINITY;
+    return;
   }
   int need = kp;
   uint32_t pre = 0;
   for (int b = 31; b >= 0; --b) {
     int c = 0;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) c += ((v[i] ^ pre) >> b) == 0 ? 1 : 0;
-    c = block_sum(c, s_red, b & 1);
+    for (int i = 0; i < 8; ++i) c += popc(__ballot(((v[i] ^ pre) >> b) == 0));
     if (c < need) {
       need -= c;
       pre |= 1u << b;
     }
   }
-  if (tid == 0) thr0[blockIdx.x] = pre == 0xffffffffu ? INFINITY : unord_f32(pre);
+  if (lane == 0) thr0[q] = pre == 0xffffffffu ? INFINITY : unord_f32(pre);
 }
 
-// Merge + exact re-rank: one workgroup per query.
-template <int EPT>
+// ---------------------------------------------------------------------------
+// Merge + exact re-rank, one workgroup (4 waves) per query.
+//  1. The kp-th smallest list minimum bounds the kp-th smallest key (kp list
+//     minima are kp distinct keys): only keys at or below it can be among
+//     the kp smallest.  Each wave computes it (a 256-key wave sort).
+//  2. Each wave streams a quarter of the lists, 64 keys per row, all rows of
+//     a batch loaded at once; a row holding a key within the bound is sorted
+//     (wave bitonic) and merged into the wave's running sorted top-64*E,
+//     whose kp-th key then tightens the wave's bound.
+//  3. Wave 0 merges the four running lists; the kp candidates are re-ranked
+//     by the four waves with exact fp32 distances from the fp32 rows.
+//  4. Wave 0 sorts them by (distance, id) and writes k results, padded with
+//     UINT32_MAX / +inf (src/cagra.cpp:240-251).
+// ---------------------------------------------------------------------------
+template <int E>
 __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restrict__ part,
-                                                       int m_keys, int kp, int n_ranges, int stride,
-                                                       const float* __restrict__ rows, int64_t d,
+                                                       const uint64_t* __restrict__ lmin, int G, int kp,
+                                                       int stride, const float* __restrict__ rows, int64_t d,
                                                        const float* __restrict__ queries, int64_t k,
                                                        uint32_t* __restrict__ out_nbr,
                                                        float* __restrict__ out_dist) {
-  __shared__ int s_red[2 * kWaves];
-  __shared__ int s_n;
-  __shared__ uint64_t s_sel[128];
-  __shared__ float s_ex[128];
-  const int tid = threadIdx.x;
+  constexpr int kBatch = 16;
+  __shared__ uint64_t s_run[kWaves][64 * E];
+  __shared__ uint32_t s_cid[64 * E];
+  __shared__ float s_cd[64 * E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t q = blockIdx.x;
-  // Key e is entry e % kp of range e / kp's list, stride keys apart.
-  const uint64_t* src = part + q * int64_t(n_ranges) * stride;
 
-  uint32_t hi[EPT], lo[EPT];
+  // 1. Bound from the list minima (G <= 256).
+  uint64_t mins[4];
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const int e = tid + i * kThreads;
-    const uint64_t key = e < m_keys ? src[int64_t(e / kp) * stride + e % kp] : kSentinel;
-    hi[i] = uint32_t(key >> 32);
-    lo[i] = uint32_t(key);
+  for (int i = 0; i < 4; ++i) {
+    const int x = lane + 64 * i;
+    mins[i] = x < G ? lmin[q * G + x] : kSentinel;
   }
-  if (tid == 0) s_n = 0;
-
-  // kp-th smallest key: radix select on the distance word, then on the id.
-  int need = kp;
-  uint32_t pre = 0;
-  for (int b = 31; b >= 0; --b) {
-    int c = 0;
+  wave_sort_e<4>(mins);
+  uint64_t bound = kSentinel;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) c += ((hi[i] ^ pre) >> b) == 0 ? 1 : 0;
-    c = block_sum(c, s_red, b & 1);
-    if (c < need) {
-      need -= c;
-      pre |= 1u << b;
+  for (int i = 0; i < 4; ++i)
+    if (i == (kp - 1) / 64) bound = shfl_u64(mins[i], (kp - 1) % 64);
+
+  // 2. This wave's quarter of the 64-key rows.
+  uint64_t run[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) run[e] = kSentinel;
+  const uint64_t* src = part + q * int64_t(G) * stride;
+  const int total = G * kp;
+  const int n_rows = (total + 63) / 64;
+  const int r0 = (n_rows * wave) / kWaves, r1 = (n_rows * (wave + 1)) / kWaves;
+  for (int rb = r0; rb < r1; rb += kBatch) {
+    uint64_t key[kBatch];
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r) {
+      const int e = (rb + r) * 64 + lane;
+      key[r] = (rb + r < r1 && e < total) ? src[int64_t(e / kp) * stride + e % kp] : kSentinel;
     }
-  }
-  const uint32_t kth_hi = pre;
-  // Select on the id only if several keys share the kp-th distance word.
-  int eq = 0;
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) eq += hi[i] == kth_hi ? 1 : 0;
-  eq = block_sum(eq, s_red, 0);
-  uint32_t pre2 = 0xffffffffu;
-  if (eq > need) {
-    pre2 = 0;
-    for (int b = 31; b >= 0; --b) {
-      int c = 0;
+    for (int r = 0; r < kBatch; ++r) {
+      const bool pass = key[r] != kSentinel && key[r] <= bound;
+      if (__ballot(pass) == 0) continue;
+      uint64_t ck[1] = {pass ? key[r] : kSentinel};
+      wave_sort_e<1>(ck);
+      wave_merge<E>(run, ck[0]);
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) c += (hi[i] == kth_hi && ((lo[i] ^ pre2) >> b) == 0) ? 1 : 0;
-      c = block_sum(c, s_red, (b + 1) & 1);
-      if (c < need) {
-        need -= c;
-        pre2 |= 1u << b;
+      for (int e = 0; e < E; ++e) {
+        if (e == (kp - 1) / 64) {
+          const uint64_t kth = shfl_u64(run[e], (kp - 1) % 64);
+          bound = kth < bound ? kth : bound;
+        }
       }
     }
   }
-  const uint64_t kth = (uint64_t(kth_hi) << 32) | pre2;
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const uint64_t key = (uint64_t(hi[i]) << 32) | lo[i];
-    if (key <= kth && key != kSentinel) {
-      const int p = atomicAdd(&s_n, 1);
-      if (p < 128) s_sel[p] = key;
+  for (int e = 0; e < E; ++e) s_run[wave][e * 64 + lane] = run[e];
+  __syncthreads();
+
+  // 3. Merge the four running lists; re-rank the kp candidates.
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
+#pragma unroll
+      for (int e = 0; e < E; ++e) wave_merge<E>(run, s_run[w][e * 64 + lane]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int pos = e * 64 + lane;
+      s_cid[pos] = (pos < kp && run[e] != kSentinel) ? uint32_t(run[e]) : 0xffffffffu;
     }
   }
   __syncthreads();
-  const int n_sel = s_n < kp ? s_n : kp;
-
-  // Exact fp32 distances: one wave per candidate, two candidates in flight.
-  const int wave = tid >> 6, lane = tid & 63;
   const float* qv = queries + q * d;
   const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
-  for (int c0 = wave * 2; c0 < n_sel; c0 += 2 * kWaves) {
-    const int nc = c0 + 1 < n_sel ? 2 : 1;
-    float acc[2] = {0.f, 0.f};
-    for (int u = 0; u < nc; ++u) {
-      const float* xv = rows + int64_t(uint32_t(s_sel[c0 + u])) * d;
-      if (vec) {
-        for (int64_t i = int64_t(lane) * 4; i < d; i += 256) {
-          const float4 a = *reinterpret_cast<const float4*>(qv + i);
-          const float4 b = *reinterpret_cast<const float4*>(xv + i);
-          const float t0 = a.x - b.x, t1 = a.y - b.y, t2 = a.z - b.z, t3 = a.w - b.w;
+  for (int c = 4 * wave; c < kp; c += 4 * kWaves) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    uint32_t id[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) id[u] = c + u < kp ? s_cid[c + u] : 0xffffffffu;
+    if (vec) {
+      for (int64_t i = int64_t(lane) * 4; i < d; i += 256) {
+        const float4 a4 = *reinterpret_cast<const float4*>(qv + i);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (id[u] == 0xffffffffu) continue;
+          const float4 b4 = *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i);
+          const float t0 = a4.x - b4.x, t1 = a4.y - b4.y, t2 = a4.z - b4.z, t3 = a4.w - b4.w;
           acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
         }
-      } else {
-        for (int64_t i = lane; i < d; i += 64) {
-          const float t = qv[i] - xv[i];
+      }
+    } else {
+      for (int64_t i = lane; i < d; i += 64) {
+        const float a1 = qv[i];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (id[u] == 0xffffffffu) continue;
+          const float t = a1 - rows[int64_t(id[u]) * d + i];
           acc[u] += t * t;
         }
       }
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < 4; ++u) {
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) acc[u] += __shfl_xor(acc[u], o);
-    }
-    if (lane == 0) {
-      s_ex[c0] = acc[0];
-      if (nc == 2) s_ex[c0 + 1] = acc[1];
+      if (lane == 0 && c + u < kp) s_cd[c + u] = acc[u];
     }
   }
   __syncthreads();
 
-  // Rank sort by (distance, id); write k results with padding.
-  if (tid < n_sel) {
-    const float dv = s_ex[tid];
-    const uint32_t iv = uint32_t(s_sel[tid]);
-    int rank = 0;
-    for (int j = 0; j < n_sel; ++j) {
-      const float dj = s_ex[j];
-      const uint32_t ij = uint32_t(s_sel[j]);
-      rank += (dj < dv || (dj == dv && ij < iv)) ? 1 : 0;
-    }
-    if (rank < k) {
-      out_nbr[q * k + rank] = iv;
-      out_dist[q * k + rank] = dv;
-    }
+  // 4. Sort by (exact distance, id) and write k results.
+  if (wave != 0) return;
+  uint64_t fin[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int pos = e * 64 + lane;
+    const uint32_t id = pos < kp ? s_cid[pos] : 0xffffffffu;
+    fin[e] = id == 0xffffffffu ? kSentinel : (uint64_t(ord_f32(s_cd[pos])) << 32) | id;
   }
-  for (int64_t r = n_sel + tid; r < k; r += kThreads) {
-    out_nbr[q * k + r] = 0xffffffffu;
-    out_dist[q * k + r] = INFINITY;
+  wave_sort_e<E>(fin);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int64_t pos = e * 64 + lane;
+    if (pos < k) {
+      out_nbr[q * k + pos] = fin[e] == kSentinel ? 0xffffffffu : uint32_t(fin[e]);
+      out_dist[q * k + pos] = fin[e] == kSentinel ? INFINITY : unord_f32(uint32_t(fin[e] >> 32));
+    }
   }
 }
 
@@ -802,27 +887,6 @@ void launch_scan(cvs_context* ctx, int ks, dim3 grid, const ScanArgs& args, int 
   after_launch(mode == kModeScan ? "bf_scan_kernel" : "bf_sample_kernel");
 }
 
-template <template <int> class K, typename... Args>
-void launch_by_ept(int64_t ept, dim3 grid, hipStream_t s, Args... args) {
-  if (ept <= 16)
-    hipLaunchKernelGGL(K<16>::fn, grid, dim3(kThreads), 0, s, args...);
-  else if (ept <= 32)
-    hipLaunchKernelGGL(K<32>::fn, grid, dim3(kThreads), 0, s, args...);
-  else if (ept <= 64)
-    hipLaunchKernelGGL(K<64>::fn, grid, dim3(kThreads), 0, s, args...);
-  else
-    fail(CVS_ERR_RUNTIME, "list larger than the selection kernels support");
-}
-
-template <int EPT>
-struct SelectK {
-  static constexpr auto fn = bf_select_kernel<EPT>;
-};
-template <int EPT>
-struct MergeK {
-  static constexpr auto fn = bf_merge_kernel<EPT>;
-};
-
 void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q,
                       int64_t k, uint32_t* nbr, float* dist) {
   if (!ds || ds->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "dataset does not belong to context");
@@ -838,13 +902,12 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   const int rpu = 2 * kStageBlocks * 32 / ks;  // rows per unit
   const int64_t n_units = ds->n_tiles * ks / (2 * kStageBlocks);
   const int kp = choose_kp(k);
-  const int64_t q_tiles = (q + 31) / 32;
   const unsigned qblocks = unsigned((q + kQB - 1) / kQB);
   const bool global_lists = kp > 64;
   // Dataset ranges (workgroups along N): one per compute unit, at most 128
-  // with kp = 128 (the merge selects from <= 16,384 keys per query), and 32
-  // for large batches, whose 128-query blocks then run range-major so that
-  // the blocks sharing a range stream it together through L2 / MALL.
+  // with kp = 128, and 32 for large batches, whose 128-query blocks then run
+  // range-major so that the blocks sharing a range stream it together
+  // through L2 / MALL.
   const bool large_batch = qblocks > 8;
   int G = ctx->compute_units;
   if (G > 256) G = 256;
@@ -853,58 +916,65 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   if (int64_t(G) > n_units) G = int(n_units);
   const int stride = global_lists ? Lists<128, kModeScan>::CAP : kp;
 
-  // Sample: ~256*kp rows (at most 16,384) in whole units, evenly strided.
+  // Sample: ~256*kp rows (at most 16,384) in whole units, evenly strided,
+  // over Gs workgroups; 2 minima per (query, workgroup).
   int64_t s_units = std::min<int64_t>(256 * int64_t(kp), 16384) / rpu;
   if (s_units < 1) s_units = 1;
   if (s_units > n_units) s_units = n_units;
   const int64_t s_stride = n_units / s_units;
-  const int64_t s_rows = s_units * rpu;
-  int Gs = ctx->compute_units;
+  int Gs = std::min(ctx->compute_units, 256);
   if (int64_t(Gs) > s_units) Gs = int(s_units);
+  const int m_min = 2 * Gs;
 
-  // Workspaces: query tiles + norms | thresholds | sample distances; lists.
-  const size_t qtile_bytes = size_t(q_tiles) * size_t(ks) * kStepBytes;
-  const size_t qnorm_bytes = size_t(q_tiles) * 32 * sizeof(float);
-  const size_t thr_bytes = (size_t(q) * sizeof(float) + 255) / 256 * 256;
-  const size_t sdist_bytes = size_t(q) * size_t(s_rows) * sizeof(float);
-  ctx->ws_queries.reserve(qtile_bytes + qnorm_bytes + thr_bytes + sdist_bytes);
+  // Workspaces: query tiles | query norms | thresholds | sample minima |
+  // list minima; lists.
+  const int64_t q_tiles = (q + 31) / 32;
+  auto align = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t qtile_bytes = align(size_t(q_tiles) * size_t(ks) * kStepBytes);
+  const size_t qnorm_bytes = align(size_t(q_tiles) * 32 * sizeof(float));
+  const size_t thr_bytes = align(size_t(q) * sizeof(float));
+  const size_t smin_bytes = align(size_t(q) * size_t(m_min) * sizeof(float));
+  const size_t lmin_bytes = align(size_t(q) * size_t(G) * sizeof(uint64_t));
+  ctx->ws_queries.reserve(qtile_bytes + qnorm_bytes + thr_bytes + smin_bytes + lmin_bytes);
   char* wsq = ctx->ws_queries.as<char>();
-  uint16_t* qtiles = reinterpret_cast<uint16_t*>(wsq);
+  u32x4* qtiles = reinterpret_cast<u32x4*>(wsq);
   float* qnorms = reinterpret_cast<float*>(wsq + qtile_bytes);
   float* thr0 = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes);
-  float* sdist = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes);
-  const int m_keys = G * kp;
+  float* sgmin = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes);
+  uint64_t* lmin = reinterpret_cast<uint64_t*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes + smin_bytes);
   ctx->ws_partial.reserve(size_t(q) * size_t(G) * size_t(stride) * sizeof(uint64_t));
   uint64_t* part = ctx->ws_partial.as<uint64_t>();
-
-  hipEvent_t t0 = timer_begin(ctx, "bf_prep");
-  launch_to_tiles(ctx, queries, q, ds->d, ds->dp, q_tiles, qtiles, qnorms);
-  timer_end(ctx, "bf_prep", t0);
 
   ScanArgs args{};
   args.tiles = reinterpret_cast<const u32x4*>(ds->tiles);
   args.norms = reinterpret_cast<const f32x4*>(ds->norms);
   args.n_units = n_units;
-  args.qtiles = reinterpret_cast<const u32x4*>(qtiles);
+  args.qtiles = qtiles;
   args.qnorms = qnorms;
   args.nq = int(q);
   args.n_qtiles = int(q_tiles);
   args.kp = kp;
   args.thr0 = thr0;
   args.part = part;
-  args.sdist = sdist;
+  args.sgmin = sgmin;
+  args.lmin = lmin;
   args.s_units = s_units;
   args.s_stride = s_stride;
-  args.s_rows = s_rows;
-
   args.n_qblocks = int(qblocks);
+  const unsigned wave_blocks = unsigned((q + kWaves - 1) / kWaves);
+
+  hipEvent_t t0 = timer_begin(ctx, "bf_prep");
+  hipLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((q_tiles * 32 + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                     ctx->stream, queries, q, ds->d, ks, q_tiles * 32, qtiles, qnorms);
+  after_launch("query_tiles_kernel");
+  timer_end(ctx, "bf_prep", t0);
 
   hipEvent_t t1 = timer_begin(ctx, "bf_sample");
   args.n_ranges = Gs;
   args.qb_fast = 0;
   launch_scan(ctx, ks, dim3(unsigned(Gs), qblocks), args, kModeSample);
-  launch_by_ept<SelectK>((s_rows + kThreads - 1) / kThreads, dim3(unsigned(q)), ctx->stream,
-                         static_cast<const float*>(sdist), s_rows, kp, thr0);
+  hipLaunchKernelGGL(bf_select_kernel, dim3(wave_blocks), dim3(kThreads), 0, ctx->stream,
+                     static_cast<const float*>(sgmin), m_min, kp, int(q), thr0);
   after_launch("bf_select_kernel");
   timer_end(ctx, "bf_sample", t1);
 
@@ -916,9 +986,14 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   timer_end(ctx, "bf_scan", t2);
 
   hipEvent_t t3 = timer_begin(ctx, "bf_merge");
-  launch_by_ept<MergeK>((m_keys + kThreads - 1) / kThreads, dim3(unsigned(q)), ctx->stream,
-                        static_cast<const uint64_t*>(part), m_keys, kp, G, stride,
-                        static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
+  if (kp <= 64)
+    hipLaunchKernelGGL(bf_merge_kernel<1>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
+                       static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, stride,
+                       static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
+  else
+    hipLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
+                       static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, stride,
+                       static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   after_launch("bf_merge_kernel");
   timer_end(ctx, "bf_merge", t3);
 }
