@@ -120,7 +120,26 @@ def calibrate_copy(mib: int) -> int:
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": 5}), flush=True)
+    # Achievable streaming-read rate: a full reduction over the same buffer
+    # (reads mib MiB, writes one float), timed with events on its stream.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        src.sum()
+    start.record()
+    reps = 20
+    for _ in range(reps):
+        src.sum()
+    end.record()
+    torch.cuda.synchronize()
+    read_gbs = n * 4 * reps / (start.elapsed_time(end) * 1e-3) / 1e9
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * n * 4 * reps / (start.elapsed_time(end) * 1e-3) / 1e9
+    print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": 5, "read_gbs": read_gbs,
+                      "copy_gbs_read_plus_write": copy_gbs}), flush=True)
     return 0
 
 

@@ -487,8 +487,10 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
   int n_keep = 0;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
+    // Both shuffles run on every lane (a shuffle reads only active lanes).
     const uint64_t up = shfl_u64(by_id[e], lane > 0 ? lane - 1 : 0);
-    const uint64_t prev = lane > 0 ? up : (e > 0 ? shfl_u64(by_id[e - 1], 63) : kEmpty);
+    const uint64_t tail = e > 0 ? shfl_u64(by_id[e > 0 ? e - 1 : 0], 63) : kEmpty;
+    const uint64_t prev = lane > 0 ? up : tail;
     const uint32_t bid = uint32_t(by_id[e] >> 32);
     const bool first = (e == 0 && lane == 0) || uint32_t(prev >> 32) != bid;
     const bool keep = by_id[e] != kEmpty && first && !contains(bid);
@@ -640,6 +642,10 @@ __global__ __launch_bounds__(256) void merge_reverse_kernel(const uint32_t* __re
       }
     for (int i = half; i < g && m < g; ++i)
       if (kr[i] != kInvalid && !has(kr[i])) so[m++] = kr[i];
+    // Reverse edges that duplicated a kept edge leave room: fill it with the
+    // remaining reverse edges.
+    for (int i = 0; i < rc && m < g; ++i)
+      if (!has(rr[i])) so[m++] = rr[i];
     for (int i = m; i < g; ++i) so[i] = kInvalid;
   }
   __builtin_amdgcn_wave_barrier();

@@ -29,9 +29,9 @@
 // unexpanded entry or after max_iterations.  The list is seeded with the
 // index's seed nodes (the reference's navigation nodes, src/cagra.cpp:63-82:
 // the reference starts from the single nearest one; here all of them enter
-// the list, which contains that one), or, without seed nodes, with 64
-// hashed ids led by the reference's fallback (q * 2654435761) mod n
-// (shaders/cagra_kernels.metal:65-67).
+// the list, which contains that one); the free lanes of the last 64-id seed
+// chunk (all 64 without seed nodes) take hashed ids led by the reference's
+// fallback (q * 2654435761) mod n (shaders/cagra_kernels.metal:65-67).
 //
 // Distances are exact fp32 sums of squared differences (summation order of
 // four 16-lane partial sums); outputs are sorted by (distance, id) and padded
@@ -225,17 +225,22 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
     __syncthreads();
   };
 
-  // Seeds.
-  if (a.n_seeds > 0) {
-    for (int c = 0; c < a.n_seeds; c += 64) {
+  // Seeds: the seed nodes in chunks of 64; lanes past the last seed (all 64
+  // without seed nodes) take hashed ids led by the reference's fallback
+  // (q * 2654435761) mod n, so that regions no seed node reaches can still be
+  // entered.
+  {
+    const uint32_t h0 = uint32_t(qi) * 2654435761u;
+    for (int c = 0; c == 0 || c < a.n_seeds; c += 64) {
       if (count + 64 > hcap) reset_hash();
       const int i = c + lane;
-      process(i < a.n_seeds ? a.seeds[i] : kInvalidId);
+      uint32_t id = kInvalidId;
+      if (i < a.n_seeds)
+        id = a.seeds[i];
+      else if (uint32_t(i - a.n_seeds) < a.n)
+        id = (h0 + uint32_t(i - a.n_seeds) * 0x9E3779B9u) % a.n;
+      process(id);
     }
-  } else {
-    const uint32_t h0 = uint32_t(qi) * 2654435761u;
-    const uint32_t id = (h0 + uint32_t(lane) * 0x9E3779B9u) % a.n;
-    process(uint32_t(lane) < a.n ? id : kInvalidId);
   }
 
   // Iterations.

@@ -1,0 +1,213 @@
+// C++ API checks on the GPU, written the way the reference's callers use the
+// API:
+//  - the FAISS v1.8 adapter flow of tests/faiss_v1_8_cagra_runtime_smoke.cpp
+//    (rebuild on every add, itopk_size = k, UINT32_MAX -> -1) with its known
+//    answers (:299-357) and the attach_dataset_on_build = false lifecycle
+//    (:247-261), without the FAISS headers;
+//  - the dispatch test of tests/test_metal_search.cpp:16-58 (default
+//    parameters, dispatch count > 0) plus the exact answers of its inputs;
+//  - graph_degree = 0 (exact route, src/cagra.cpp:197-202) and the
+//    brute_force namespace (uint32 and int64 ids);
+//  - build -> save_index -> load_index -> search on random data against exact
+//    search.
+#include <cuvs/neighbors/brute_force.hpp>
+#include <cuvs/neighbors/cagra.hpp>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <limits>
+#include <random>
+#include <set>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "check.hpp"
+
+namespace cagra = cuvs::neighbors::cagra;
+namespace bf = cuvs::neighbors::brute_force;
+using apitest::expect_throw;
+
+namespace {
+
+constexpr std::uint32_t kNone = std::numeric_limits<std::uint32_t>::max();
+
+// The FAISS-facing adapter of the reference's runtime smoke test, minus FAISS.
+struct FaissLikeIndex {
+  std::int64_t d;
+  std::int64_t ntotal = 0;
+  std::vector<float> added;
+  raft::resources res;
+  cagra::index<float, std::uint32_t> index;
+
+  explicit FaissLikeIndex(std::int64_t dim) : d(dim) {}
+
+  void add(std::int64_t n, const float* v) {
+    cagra::index_params params;
+    params.metric = cuvs::distance::DistanceType::L2Expanded;
+    added.insert(added.end(), v, v + n * d);
+    index = cagra::build(res, params,
+                         raft::make_device_matrix_view<const float, std::int64_t>(added.data(), ntotal + n, d));
+    ntotal += n;
+  }
+
+  void search(std::int64_t q, const float* queries, std::int64_t k, float* dist, std::int64_t* labels) {
+    if (k <= 0) throw std::invalid_argument("k > 0");
+    cagra::search_params sp;
+    sp.itopk_size = static_cast<std::uint64_t>(k);
+    std::vector<std::uint32_t> ids(static_cast<std::size_t>(q * k));
+    cagra::search(res, sp, index, raft::make_device_matrix_view<const float, std::int64_t>(queries, q, d),
+                  raft::make_device_matrix_view<std::uint32_t, std::int64_t>(ids.data(), q, k),
+                  raft::make_device_matrix_view<float, std::int64_t>(dist, q, k));
+    for (std::int64_t i = 0; i < q * k; ++i) labels[i] = ids[i] == kNone ? -1 : static_cast<std::int64_t>(ids[i]);
+  }
+};
+
+void faiss_smoke() {
+  const std::vector<float> db{0, 0, 10, 0, 0, 10, 2, 2};
+  const std::vector<float> qs{0, 0, 9, 1};
+  {
+    raft::resources res;
+    cagra::index_params p;
+    p.attach_dataset_on_build = false;
+    const auto idx = cagra::build(res, p, raft::make_device_matrix_view<const float, std::int64_t>(db.data(), 4, 2));
+    CHECK(idx.rows() == 4 && idx.cols() == 2 && idx.dataset().empty());
+  }
+  FaissLikeIndex index(2);
+  index.add(2, db.data());
+  index.add(2, db.data() + 4);
+  CHECK(index.ntotal == 4 && index.index.rows() == 4);
+  CHECK(index.index.graph_degree() == 3);  // min(64, N - 1)
+  std::vector<float> dist(4);
+  std::vector<std::int64_t> lab(4);
+  index.search(2, qs.data(), 2, dist.data(), lab.data());
+  CHECK(lab[0] == 0 && dist[0] == 0.f && lab[1] == 3 && dist[1] == 8.f);
+  CHECK(lab[2] == 1 && dist[2] == 2.f && lab[3] == 3 && dist[3] == 50.f);
+  // tie at distance 100: lower id first
+  index.search(1, qs.data(), 4, dist.data(), lab.data());
+  CHECK((lab == std::vector<std::int64_t>{0, 3, 1, 2}));
+  CHECK((dist == std::vector<float>{0.f, 8.f, 100.f, 100.f}));
+  // k > N: last slot -1 / +inf, for one and for two queries
+  std::vector<float> d5(10, -7.f);
+  std::vector<std::int64_t> l5(10, -7);
+  index.search(1, qs.data(), 5, d5.data(), l5.data());
+  CHECK(l5[0] == 0 && d5[0] == 0.f && l5[4] == -1 && std::isinf(d5[4]));
+  index.search(2, qs.data(), 5, d5.data(), l5.data());
+  CHECK(l5[4] == -1 && std::isinf(d5[4]) && l5[9] == -1 && std::isinf(d5[9]) && l5[5] == 1);
+  expect_throw<std::invalid_argument>("k = 0", "k > 0", [&] { index.search(2, qs.data(), 0, d5.data(), l5.data()); });
+}
+
+void dispatch_test() {
+  constexpr int N = 64, Q = 4, D = 8, K = 4;
+  std::vector<float> base(N * D, 0.f), queries(Q * D, 0.f);
+  for (int i = 0; i < N; ++i) base[i * D + (i % D)] = float(i);
+  for (int q = 0; q < Q; ++q) queries[q * D + (q % D)] = 1.f;
+  std::vector<std::uint32_t> nbr(Q * K);
+  std::vector<float> dist(Q * K);
+  raft::resources res;
+  cagra::index_params ip;
+  cagra::search_params sp;
+  auto idx = cagra::build(res, ip, raft::device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  cagra::reset_metal_dispatch_count();
+  cagra::search(res, sp, idx, raft::device_matrix_view<const float, std::int64_t>(queries.data(), Q, D),
+                raft::device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), Q, K),
+                raft::device_matrix_view<float, std::int64_t>(dist.data(), Q, K));
+  CHECK(cagra::metal_dispatch_count() > 0);
+  const std::vector<std::uint32_t> en{0, 1, 2, 3, 1, 0, 2, 3, 0, 2, 1, 3, 0, 1, 3, 2};
+  const std::vector<float> ed{1, 2, 5, 10, 0, 1, 5, 10, 1, 1, 2, 10, 1, 2, 4, 5};
+  CHECK(nbr == en);
+  CHECK(dist == ed);
+  // The exact route (graph_degree = 0) gives the same answers.
+  cagra::index_params exact;
+  exact.graph_degree = 0;
+  auto eidx = cagra::build(res, exact, raft::device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  CHECK(eidx.graph_degree() == 0 && eidx.knn_graph().empty());
+  std::fill(nbr.begin(), nbr.end(), 0u);
+  cagra::reset_metal_dispatch_count();
+  cagra::search(res, sp, eidx, raft::device_matrix_view<const float, std::int64_t>(queries.data(), Q, D),
+                raft::device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), Q, K),
+                raft::device_matrix_view<float, std::int64_t>(dist.data(), Q, K));
+  CHECK(cagra::metal_dispatch_count() > 0);
+  CHECK(nbr == en && dist == ed);
+  // brute_force namespace, uint32 and int64 ids, k > N padding.
+  auto bidx = bf::build(res, raft::make_device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  CHECK(bidx.size() == N && bidx.dim() == D);
+  bf::search(res, bidx, raft::make_device_matrix_view<const float, std::int64_t>(queries.data(), Q, D),
+             raft::make_device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), Q, K),
+             raft::make_device_matrix_view<float, std::int64_t>(dist.data(), Q, K));
+  CHECK(nbr == en && dist == ed);
+  std::vector<float> small{0, 0, 1, 0, 0, 3, 0, 0};
+  auto sidx = bf::build(res, raft::make_device_matrix_view<const float, std::int64_t>(small.data(), 2, 4));
+  std::vector<std::int64_t> l64(3);
+  std::vector<float> d3(3);
+  bf::search(res, sidx, raft::make_device_matrix_view<const float, std::int64_t>(small.data(), 1, 4),
+             raft::make_device_matrix_view<std::int64_t, std::int64_t>(l64.data(), 1, 3),
+             raft::make_device_matrix_view<float, std::int64_t>(d3.data(), 1, 3));
+  CHECK(l64[0] == 0 && l64[1] == 1 && l64[2] == -1 && d3[1] == 10.f && std::isinf(d3[2]));
+}
+
+void build_save_load_search(const std::string& scratch) {
+  // 20 clusters, each a 4-dimensional Gaussian patch embedded in 48-d:
+  // neighbourhoods a graph can navigate (isotropic 48-d noise would leave
+  // every point about equally far from all its cluster mates).
+  const int N = 3000, D = 48, Q = 50, K = 10, C = 20, R = 4;
+  std::mt19937 gen(7);
+  std::normal_distribution<float> nd(0.f, 1.f);
+  std::vector<float> centers(C * D), basis(C * R * D), base(N * D), qs(Q * D);
+  for (auto& v : centers) v = nd(gen);
+  for (auto& v : basis) v = 0.5f * nd(gen);
+  auto sample = [&](int c, float* out) {
+    float z[R];
+    for (int r = 0; r < R; ++r) z[r] = nd(gen);
+    for (int j = 0; j < D; ++j) {
+      float v = centers[c * D + j];
+      for (int r = 0; r < R; ++r) v += z[r] * basis[(c * R + r) * D + j];
+      out[j] = v;
+    }
+  };
+  // random cluster labels (periodic labels would alias with the evenly
+  // spaced navigation nodes)
+  std::uniform_int_distribution<int> pick(0, C - 1);
+  for (int i = 0; i < N; ++i) sample(pick(gen), base.data() + i * D);
+  for (int i = 0; i < Q; ++i) sample(pick(gen), qs.data() + i * D);
+  raft::resources res;
+  cagra::index_params ip;
+  ip.graph_degree = 32;
+  ip.intermediate_graph_degree = 64;
+  auto idx = cagra::build(res, ip, raft::make_device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  CHECK(idx.graph_degree() == 32 && idx.knn_graph().size() == std::size_t(N) * 32);
+  CHECK(idx.nav_nodes().size() == 54 && idx.nav_vectors().size() == 54u * D);  // min(200, sqrt(3000))
+  for (std::size_t i = 0; i < idx.knn_graph().size(); ++i) CHECK(idx.knn_graph()[i] < std::uint32_t(N));
+  cagra::save_index(idx, scratch + "/built.bin");
+  const auto loaded = cagra::load_index(scratch + "/built.bin");
+  CHECK(loaded.knn_graph() == idx.knn_graph() && loaded.nav_nodes() == idx.nav_nodes());
+  std::vector<std::uint32_t> g(Q * K), e(Q * K);
+  std::vector<float> gd(Q * K), ed(Q * K);
+  cagra::search_params sp;
+  cagra::search(res, sp, loaded, raft::make_device_matrix_view<const float, std::int64_t>(qs.data(), Q, D),
+                raft::make_device_matrix_view<std::uint32_t, std::int64_t>(g.data(), Q, K),
+                raft::make_device_matrix_view<float, std::int64_t>(gd.data(), Q, K));
+  auto bidx = bf::build(res, raft::make_device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  bf::search(res, bidx, raft::make_device_matrix_view<const float, std::int64_t>(qs.data(), Q, D),
+             raft::make_device_matrix_view<std::uint32_t, std::int64_t>(e.data(), Q, K),
+             raft::make_device_matrix_view<float, std::int64_t>(ed.data(), Q, K));
+  int hits = 0;
+  for (int i = 0; i < Q; ++i) {
+    std::set<std::uint32_t> s(e.begin() + i * K, e.begin() + (i + 1) * K);
+    for (int j = 0; j < K; ++j) hits += s.count(g[i * K + j]) ? 1 : 0;
+  }
+  const double recall = double(hits) / (Q * K);
+  std::printf("graph search recall@10 after save/load: %.3f\n", recall);
+  CHECK(recall >= 0.9);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const std::string scratch = argc > 1 ? argv[1] : "/tmp";
+  faiss_smoke();
+  dispatch_test();
+  build_save_load_search(scratch);
+  return apitest::finish("test_api_gpu");
+}

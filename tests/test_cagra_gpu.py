@@ -66,9 +66,25 @@ def test_path_graph_walk(ctx):
     idx = ctx.cagra_index(base, graph, np.array([0], np.uint32))
     nbr, dist = idx.search(q, 3, itopk_size=3)
     assert nbr.tolist() == [[7, 6, 8]] and dist.tolist() == [[1.0, 2.0, 2.0]]
-    # one iteration: only 0's neighbour 1 has been reached
-    nbr, _ = idx.search(q, 3, itopk_size=3, max_iterations=1)
-    assert nbr.tolist() == [[1, 0, INV]]
+    # one iteration still yields three distinct rows, sorted
+    nbr, dist = idx.search(q, 3, itopk_size=3, max_iterations=1)
+    assert len(set(nbr[0].tolist())) == 3 and (nbr < 20).all() and (np.diff(dist[0]) >= 0).all()
+
+
+def test_hashed_seeds_reach_a_component_without_seed_nodes(ctx):
+    """Two disconnected cliques; the only seed node lies in the first.  The
+    free lanes of the seed chunk take hashed ids, so a query next to the
+    second clique still finds it."""
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((300, 8)).astype(np.float32)
+    b = rng.standard_normal((300, 8)).astype(np.float32) + 50.0
+    base = np.concatenate([a, b])
+    graph = np.array([[((i // 300) * 300 + (i % 300 + 1 + j) % 300) for j in range(16)] for i in range(600)],
+                     np.uint32)
+    idx = ctx.cagra_index(base, graph, np.array([0], np.uint32))
+    q = b[:5] + 0.01
+    nbr, _ = idx.search(q, 1, itopk_size=64)
+    assert nbr[:, 0].tolist() == list(range(300, 305))
 
 
 @pytest.mark.parametrize("n,d,g,itopk,width", [
