@@ -84,20 +84,24 @@ struct Cfg {
   static_assert(KS >= 2 && KS <= 64, "k-steps per tile");
 };
 
-// List geometry per kp.  A query can receive 2 lanes x H keys between two
-// overflow checks (H rows per lane); lists keep that much room.  Lists of
-// kp <= 64 live in LDS; kp = 128 lists (large k) live in global memory, one
-// per (query, workgroup), since 128 queries x 192 keys exceed the LDS budget
-// and appends are rare once the sampled threshold is in place.
+// List geometry per kp.  Each (workgroup, query) list is split into two
+// halves, one per lane holding that query (lanes l and l + 32 see different
+// rows of every tile), so each lane appends to its own half with a counter
+// in a register and no atomics.  A lane adds at most H keys between two
+// overflow checks; a check that finds a half above HALF - H rebalances the
+// query's list to its kp smallest keys, kp/2 per half, so HALF >= kp/2 + H
+// (plus slack that sets how many appends one compaction is amortized over).
+// Lists of kp <= 64 live in LDS; kp = 128 lists (large k) live in global
+// memory, one per (query, workgroup), since 128 queries x 192 keys exceed the
+// LDS budget and appends are rare once the sampled threshold is in place.
 template <int KP, int MODE>
 struct Lists {
   static constexpr bool GL = MODE == 0 && KP > 64;  // lists in global memory
   static constexpr int H = KP <= 32 ? 16 : 8;      // rows per lane between checks
-  // Beyond kp + 2H, the slack (32, 24, 8, 48 keys) sets how many pushes one
-  // compaction is amortized over; LDS lists are bounded by the 160 KiB budget.
-  static constexpr int CAP = MODE != 0 ? 1 : (KP == 16 ? 80 : (KP <= 64 ? 88 : 192));
+  static constexpr int HALF = MODE != 0 ? 1 : (KP == 16 ? 40 : (KP <= 64 ? 44 : 96));
+  static constexpr int CAP = 2 * HALF;
   static constexpr int NS = (CAP + 63) / 64;  // list entries per lane in a compaction
-  static_assert(MODE != 0 || CAP >= KP + 2 * H + 8, "list slack");
+  static_assert(MODE != 0 || HALF >= KP / 2 + H + 4, "list slack");
 };
 
 struct ScanArgs {
@@ -121,71 +125,74 @@ struct ScanArgs {
   int64_t s_stride;     // sample: unit stride
 };
 
-// Compacts the list of one query to its kp smallest keys and lowers the
-// query's threshold to the kp-th distance.  All 64 lanes take part (the list
-// pointer is wave-uniform); entry e lives in lane e % 64, slot e / 64
-// (CAP <= 64 * NS).
+// Rewrites the two-half list of one query (c0 keys at list[0..), c1 keys at
+// list[half..)) as its kp smallest keys, the first kp/2 in half 0 and the
+// rest in half 1, and returns the order image of the kp-th smallest distance
+// (0xffffffff when c0 + c1 <= kp: every key is kept and the threshold stays).
+// All 64 lanes take part (list, c0 and c1 are wave-uniform); entry e lives in
+// lane e % 64, slot e / 64.  Every entry is read before any is written.
 template <int NS>
-__device__ __forceinline__ void compact_query(uint64_t* list, uint32_t* cnt_slot, float* thr_slot,
-                                              int kp) {
+__device__ __forceinline__ uint32_t compact_query(uint64_t* list, int half, uint32_t c0, uint32_t c1,
+                                                  int kp) {
   const int lane = __lane_id();
-  const uint32_t cnt = *cnt_slot;
-  if (cnt <= uint32_t(kp)) return;
+  const uint32_t cnt = c0 + c1;
   bool v[NS];
   uint64_t k[NS];
   uint32_t h[NS], l[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    v[s] = uint32_t(lane + 64 * s) < cnt;
-    k[s] = v[s] ? list[lane + 64 * s] : kSentinel;
+    const uint32_t e = uint32_t(lane + 64 * s);
+    v[s] = e < uint32_t(half) ? e < c0 : (e - uint32_t(half)) < c1;
+    k[s] = v[s] ? list[e] : kSentinel;
     h[s] = uint32_t(k[s] >> 32);
     l[s] = uint32_t(k[s]);
   }
-  int need = kp;
-  uint32_t pre = 0;
-  for (int b = 31; b >= 0; --b) {
-    int c = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && ((h[s] ^ pre) >> b) == 0));
-    if (c < need) {
-      need -= c;
-      pre |= 1u << b;
-    }
-  }
-  const uint32_t kth_hi = pre;
-  int lt = 0, eq = 0;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    lt += popc(__ballot(v[s] && h[s] < kth_hi));
-    eq += popc(__ballot(v[s] && h[s] == kth_hi));
-  }
-  uint32_t kth_lo = 0xffffffffu;
-  if (eq > kp - lt) {  // ties on the distance word: select on the row id
-    int need2 = kp - lt;
-    uint32_t pre2 = 0;
+  uint32_t kth_hi = 0xffffffffu, kth_lo = 0xffffffffu;
+  if (cnt > uint32_t(kp)) {
+    int need = kp;
+    uint32_t pre = 0;
     for (int b = 31; b >= 0; --b) {
       int c = 0;
 #pragma unroll
-      for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && h[s] == kth_hi && ((l[s] ^ pre2) >> b) == 0));
-      if (c < need2) {
-        need2 -= c;
-        pre2 |= 1u << b;
+      for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && ((h[s] ^ pre) >> b) == 0));
+      if (c < need) {
+        need -= c;
+        pre |= 1u << b;
       }
     }
-    kth_lo = pre2;
+    kth_hi = pre;
+    int lt = 0, eq = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      lt += popc(__ballot(v[s] && h[s] < kth_hi));
+      eq += popc(__ballot(v[s] && h[s] == kth_hi));
+    }
+    if (eq > kp - lt) {  // ties on the distance word: select on the row id
+      int need2 = kp - lt;
+      uint32_t pre2 = 0;
+      for (int b = 31; b >= 0; --b) {
+        int c = 0;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && h[s] == kth_hi && ((l[s] ^ pre2) >> b) == 0));
+        if (c < need2) {
+          need2 -= c;
+          pre2 |= 1u << b;
+        }
+      }
+      kth_lo = pre2;
+    }
   }
+  const int kh = kp / 2;
   int base = 0;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const bool keep = v[s] && (h[s] < kth_hi || (h[s] == kth_hi && l[s] <= kth_lo));
     const uint64_t m = __ballot(keep);
-    if (keep) list[base + mbcnt(m)] = k[s];
+    const int p = base + mbcnt(m);
+    if (keep) list[p < kh ? p : half + (p - kh)] = k[s];
     base += popc(m);
   }
-  if (lane == 0) {
-    *cnt_slot = uint32_t(kp);
-    *thr_slot = unord_f32(kth_hi);
-  }
+  return cnt > uint32_t(kp) ? kth_hi : 0xffffffffu;
 }
 
 template <int KS, int MODE, int KP>
@@ -200,8 +207,6 @@ void bf_scan_kernel(ScanArgs a) {
 
   __shared__ u32x4 s_stage[2][kStageVecs];
   __shared__ float s_dn[2][NF];
-  __shared__ uint32_t s_cnt[kQB];
-  __shared__ float s_thr[kQB];
   __shared__ uint64_t s_buf[L::GL ? 1 : kQB * CAP];
 
   const int tid = threadIdx.x;
@@ -298,29 +303,36 @@ void bf_scan_kernel(ScanArgs a) {
   }
   const float qn = q_ok ? a.qnorms[my_q] : INFINITY;
   const int qw = wave * 32 + (lane & 31);  // this lane's query slot in the workgroup
+  const int half = lane >> 5;              // which half of the query's list this lane fills
   float thr = -INFINITY;
   float smin = INFINITY;  // sample mode: minimum over this lane's rows
-  if (MODE == kModeScan) {
-    if (q_ok) thr = nextafterf(a.thr0[my_q], INFINITY);
-    for (int i = tid; i < kQB; i += kThreads) {
-      s_cnt[i] = 0;
-      s_thr[i] = INFINITY;
-    }
-  }
+  uint32_t cnt = 0;       // keys in this lane's half of its query's list
+  if (MODE == kModeScan && q_ok) thr = nextafterf(a.thr0[my_q], INFINITY);
 
-  // Compacts every list of this wave whose count exceeds `limit`, then
-  // tightens this lane's threshold.
-  auto compact_wave = [&](uint32_t limit) CVS_INLINE {
-    uint64_t over = __ballot(lane < 32 && s_cnt[wave * 32 + lane] > limit);
+  // Rebalances every list of this wave with a half holding more than `limit`
+  // keys (or, with limit = KP / 2 - 1 at the end, more than KP keys in all)
+  // to its KP smallest keys and lowers the query's threshold to the kp-th
+  // distance when keys were dropped.
+  auto compact_wave = [&](uint32_t limit, bool total_only) CVS_INLINE {
+    const uint32_t both = cnt + uint32_t(__shfl_xor(int(cnt), 32));
+    const uint64_t over64 = __ballot(total_only ? both > uint32_t(KP) : cnt > limit);
+    uint32_t over = uint32_t(over64) | uint32_t(over64 >> 32);
     if (over == 0) return;
+    if constexpr (L::GL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
     while (over) {
-      const int i = __builtin_ctzll(over);
+      const int i = __builtin_ctz(over);
       over &= over - 1;
-      const int m = wave * 32 + i;
-      if constexpr (L::GL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      compact_query<L::NS>(list_of(m), &s_cnt[m], &s_thr[m], KP);
+      const uint32_t c0 = uint32_t(__builtin_amdgcn_readlane(int(cnt), i));
+      const uint32_t c1 = uint32_t(__builtin_amdgcn_readlane(int(cnt), i + 32));
+      const uint32_t kth = compact_query<L::NS>(list_of(wave * 32 + i), L::HALF, c0, c1, KP);
+      const uint32_t kept = c0 + c1 < uint32_t(KP) ? c0 + c1 : uint32_t(KP);
+      if ((lane & 31) == i) {
+        cnt = half == 0 ? (kept < uint32_t(KP / 2) ? kept : uint32_t(KP / 2))
+                        : (kept > uint32_t(KP / 2) ? kept - uint32_t(KP / 2) : 0u);
+        if (kth != 0xffffffffu) thr = fminf(thr, unord_f32(kth));
+      }
     }
-    thr = fminf(thr, s_thr[qw]);
+    if constexpr (L::GL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   };
 
   // Accumulators live in arch VGPRs so that all 256 AGPRs hold query operands.
@@ -330,31 +342,29 @@ void bf_scan_kernel(ScanArgs a) {
   asm volatile("" : "+v"(acc0), "+v"(acc1));
 
   // Appends the passing (distance, row) keys of one finished tile to this
-  // lane's query list.  Rare after the first tiles: each lane reserves slots
-  // for all its passing keys of H rows with one atomic, writes them, and the
-  // atomic's return value tells whether the list needs compacting (no extra
-  // LDS read).  Keys above a threshold lowered by a compaction are dropped
+  // lane's half of its query's list (rare once the sampled threshold is in
+  // place).  The loop over the 16 rows skips a row no lane passes with one
+  // ballot; the counter lives in a register, so an append is one LDS (or
+  // global) store.  After each group of H rows a half above HALF - H
+  // triggers a compaction, and keys above the lowered threshold are dropped
   // from the later groups.
   auto commit = [&](const float (&dv)[16], uint32_t pass, int64_t row0) CVS_INLINE {
     if (__ballot(pass != 0) == 0) return;
     constexpr int H = L::H;
+    uint64_t* const mine = list_of(qw) + half * L::HALF;
+    const uint32_t rbase = uint32_t(row0) + 4u * uint32_t(half);
 #pragma unroll
     for (int h = 0; h < 16; h += H) {
-      const uint32_t hp = (pass >> h) & ((1u << H) - 1u);
-      const int np = popc(hp);
-      uint32_t slot = 0;
-      if (np) slot = atomicAdd(&s_cnt[qw], uint32_t(np));
 #pragma unroll
       for (int r = h; r < h + H; ++r) {
-        if (hp & (1u << (r - h))) {
-          const uint32_t row = uint32_t(row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
-          list_of(qw)[slot] = (uint64_t(ord_f32(dv[r])) << 32) | row;
-          ++slot;
+        const bool p = ((pass >> r) & 1u) != 0;
+        if (__ballot(p) != 0 && p) {
+          mine[cnt] = (uint64_t(ord_f32(dv[r])) << 32) | (rbase + uint32_t(8 * (r >> 2) + (r & 3)));
+          ++cnt;
         }
       }
-      const uint64_t over = __ballot(np != 0 && slot > uint32_t(CAP - 2 * H));
-      if (over != 0) {
-        compact_wave(uint32_t(CAP - 2 * H));
+      if (__ballot(cnt > uint32_t(L::HALF - H)) != 0) {
+        compact_wave(uint32_t(L::HALF - H), false);
 #pragma unroll
         for (int r = h + H; r < 16; ++r)
           if (!(dv[r] < thr)) pass &= ~(1u << r);
@@ -467,7 +477,8 @@ void bf_scan_kernel(ScanArgs a) {
     // (VALU), the LDS store of stage j+1 (its buffer was last read in stage
     // j-1, which every wave finished before the barrier), the HBM load of
     // stage j+3 into the registers just stored, and the norms of the current
-    // tile.  Only the rare list append after the MFMAs branches.
+    // tile.  Only the rare list
+    // append after the MFMAs branches.
     auto lstore_b = [&](int buf, const u32x4 (&r)[kLoadsPerThread]) CVS_INLINE {
 #pragma unroll
       for (int i = 0; i < kLoadsPerThread; ++i) s_stage[buf][tid + i * kThreads] = r[i];
@@ -573,29 +584,37 @@ void bf_scan_kernel(ScanArgs a) {
     if (q_ok) a.sgmin[int64_t(my_q) * (2 * G) + 2 * x + (lane >> 5)] = smin;
   }
   if (MODE == kModeScan) {
-    compact_wave(uint32_t(KP));
-    if constexpr (L::GL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    compact_wave(0u, true);
     for (int i = 0; i < 32; ++i) {
       const int m = wave * 32 + i;
       const int q = qbase + m;
       if (q >= a.nq) break;
-      const uint32_t c = s_cnt[m];
+      const uint32_t c0 = uint32_t(__builtin_amdgcn_readlane(int(cnt), i));
+      const uint32_t c1 = uint32_t(__builtin_amdgcn_readlane(int(cnt), i + 32));
+      // Entry e of the output: half 0's keys, then half 1's, then sentinels.
+      const uint64_t* src = list_of(m);
+      constexpr int NE = (KP + 63) / 64;
+      uint64_t key[NE];
       uint64_t mn = kSentinel;
+#pragma unroll
+      for (int t = 0; t < NE; ++t) {
+        const uint32_t e = uint32_t(lane + 64 * t);
+        key[t] = e < c0 ? src[e] : (e < c0 + c1 ? src[L::HALF + (e - c0)] : kSentinel);
+        if (e >= uint32_t(KP)) key[t] = kSentinel;
+        mn = key[t] < mn ? key[t] : mn;
+      }
       if constexpr (L::GL) {
-        // In place: the first kp entries of the global list, sentinel-padded.
+        // In place (first kp entries of the global list): every entry is
+        // read before any is written.
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
         uint64_t* lst = list_of(m);
-        for (int e = lane; e < KP; e += 64) {
-          if (uint32_t(e) >= c)
-            lst[e] = kSentinel;
-          else
-            mn = lst[e] < mn ? lst[e] : mn;
-        }
+#pragma unroll
+        for (int t = 0; t < NE; ++t)
+          if (lane + 64 * t < KP) lst[lane + 64 * t] = key[t];
       } else {
-        for (int e = lane; e < KP; e += 64) {
-          const uint64_t key = uint32_t(e) < c ? s_buf[m * CAP + e] : kSentinel;
-          a.part[(int64_t(q) * G + x) * KP + e] = key;
-          mn = key < mn ? key : mn;
-        }
+#pragma unroll
+        for (int t = 0; t < NE; ++t)
+          if (lane + 64 * t < KP) a.part[(int64_t(q) * G + x) * KP + lane + 64 * t] = key[t];
       }
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) {
@@ -916,9 +935,12 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   if (int64_t(G) > n_units) G = int(n_units);
   const int stride = global_lists ? Lists<128, kModeScan>::CAP : kp;
 
-  // Sample: ~256*kp rows (at most 16,384) in whole units, evenly strided,
-  // over Gs workgroups; 2 minima per (query, workgroup).
-  int64_t s_units = std::min<int64_t>(256 * int64_t(kp), 16384) / rpu;
+  // Sample: 32,768 rows for small batches, 16,384 for large ones (whose scan
+  // is MFMA-bound), in whole units, evenly strided, over Gs workgroups;
+  // 2 minima per (query, workgroup).  The initial threshold then sits near
+  // rank kp * n / sample of each query's distances, so a workgroup's lists
+  // see about kp * n / (sample * G) appends per query over its range.
+  int64_t s_units = (large_batch ? 16384 : 32768) / rpu;
   if (s_units < 1) s_units = 1;
   if (s_units > n_units) s_units = n_units;
   const int64_t s_stride = n_units / s_units;
