@@ -87,21 +87,21 @@ struct Cfg {
 // List geometry per kp.  Each (workgroup, query) list is split into two
 // halves, one per lane holding that query (lanes l and l + 32 see different
 // rows of every tile), so each lane appends to its own half with a counter
-// in a register and no atomics.  A lane adds at most H keys between two
-// overflow checks; a check that finds a half above HALF - H rebalances the
-// query's list to its kp smallest keys, kp/2 per half, so HALF >= kp/2 + H
-// (plus slack that sets how many appends one compaction is amortized over).
-// Lists of kp <= 64 live in LDS; kp = 128 lists (large k) live in global
-// memory, one per (query, workgroup), since 128 queries x 192 keys exceed the
-// LDS budget and appends are rare once the sampled threshold is in place.
+// in a register and no atomics.  A lane adds at most one key between two
+// fill checks; a half that fills up (HALF keys) rebalances the query's list
+// to its kp smallest keys, kp/2 per half, so the slack HALF - kp/2 sets how
+// many appends one compaction is amortized over.  Lists of kp <= 64 live in
+// LDS (bounded by the 160 KiB budget next to the stage buffers); kp = 128
+// lists (large k) live in global memory, one per (query, workgroup), since
+// 128 queries x 192 keys exceed the LDS budget and appends are rare once the
+// sampled threshold is in place.
 template <int KP, int MODE>
 struct Lists {
   static constexpr bool GL = MODE == 0 && KP > 64;  // lists in global memory
-  static constexpr int H = KP <= 32 ? 16 : 8;      // rows per lane between checks
   static constexpr int HALF = MODE != 0 ? 1 : (KP == 16 ? 40 : (KP <= 64 ? 44 : 96));
   static constexpr int CAP = 2 * HALF;
   static constexpr int NS = (CAP + 63) / 64;  // list entries per lane in a compaction
-  static_assert(MODE != 0 || HALF >= KP / 2 + H + 4, "list slack");
+  static_assert(MODE != 0 || HALF >= KP / 2 + 8, "list slack");
 };
 
 struct ScanArgs {
@@ -342,32 +342,38 @@ void bf_scan_kernel(ScanArgs a) {
   asm volatile("" : "+v"(acc0), "+v"(acc1));
 
   // Appends the passing (distance, row) keys of one finished tile to this
-  // lane's half of its query's list (rare once the sampled threshold is in
-  // place).  The loop over the 16 rows skips a row no lane passes with one
-  // ballot; the counter lives in a register, so an append is one LDS (or
-  // global) store.  After each group of H rows a half above HALF - H
-  // triggers a compaction, and keys above the lowered threshold are dropped
-  // from the later groups.
-  auto commit = [&](const float (&dv)[16], uint32_t pass, int64_t row0) CVS_INLINE {
-    if (__ballot(pass != 0) == 0) return;
-    constexpr int H = L::H;
+  // lane's half of its query's list.  Appends are rare once the sampled
+  // threshold is in place (typically one or two lanes of a wave pass a row
+  // of a tile, most tiles none), so the wave first ORs the pass masks of the
+  // passing lanes (scalar reads of those lanes only), then visits just the
+  // rows some lane passes: the row index is wave-uniform, so its distance is
+  // picked from the 16-element vector by a uniform index, and each passing
+  // lane appends one key to its half (counter in a register).  A half that
+  // fills up triggers a compaction, and keys above the lowered threshold are
+  // dropped from the rows not yet visited.
+  auto commit = [&](const f32x16& dv, uint32_t pass, int64_t row0) CVS_INLINE {
+    uint64_t lanes = __ballot(pass != 0);
+    if (lanes == 0) return;
+    uint32_t rows_any = 0;
+    while (lanes) {
+      const int l = __builtin_ctzll(lanes);
+      lanes &= lanes - 1;
+      rows_any |= uint32_t(__builtin_amdgcn_readlane(int(pass), l));
+    }
     uint64_t* const mine = list_of(qw) + half * L::HALF;
     const uint32_t rbase = uint32_t(row0) + 4u * uint32_t(half);
-#pragma unroll
-    for (int h = 0; h < 16; h += H) {
-#pragma unroll
-      for (int r = h; r < h + H; ++r) {
-        const bool p = ((pass >> r) & 1u) != 0;
-        if (__ballot(p) != 0 && p) {
-          mine[cnt] = (uint64_t(ord_f32(dv[r])) << 32) | (rbase + uint32_t(8 * (r >> 2) + (r & 3)));
-          ++cnt;
-        }
+    while (rows_any) {
+      const int r = __builtin_ctz(rows_any);
+      rows_any &= rows_any - 1;
+      if ((pass >> r) & 1u) {
+        mine[cnt] = (uint64_t(ord_f32(dv[r])) << 32) | (rbase + uint32_t(8 * (r >> 2) + (r & 3)));
+        ++cnt;
       }
-      if (__ballot(cnt > uint32_t(L::HALF - H)) != 0) {
-        compact_wave(uint32_t(L::HALF - H), false);
+      if (__ballot(cnt >= uint32_t(L::HALF)) != 0) {
+        compact_wave(uint32_t(L::HALF - 1), false);
 #pragma unroll
-        for (int r = h + H; r < 16; ++r)
-          if (!(dv[r] < thr)) pass &= ~(1u << r);
+        for (int r2 = 0; r2 < 16; ++r2)
+          if (!(dv[r2] < thr)) pass &= ~(1u << r2);
       }
     }
   };
@@ -389,7 +395,7 @@ void bf_scan_kernel(ScanArgs a) {
       (void)j;
     } else {
       // Branch-free pass mask over the 16 rows, then the rare append.
-      float dv[16];
+      f32x16 dv;
       uint32_t pass = 0;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -485,7 +491,7 @@ void bf_scan_kernel(ScanArgs a) {
     };
     // Turns the dot products of a finished tile (in `dv`) into distances and
     // its pass mask.
-    auto prepare = [&](float (&dv)[16], const f32x4 (&dn)[4]) CVS_INLINE -> uint32_t {
+    auto prepare = [&](f32x16& dv, const f32x4 (&dn)[4]) CVS_INLINE -> uint32_t {
       uint32_t pass = 0;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -494,7 +500,7 @@ void bf_scan_kernel(ScanArgs a) {
       }
       return pass;
     };
-    float dv[16];
+    f32x16 dv;
     f32x4 dn[2][4];
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[r] = 0.f;
@@ -585,6 +591,29 @@ void bf_scan_kernel(ScanArgs a) {
   }
   if (MODE == kModeScan) {
     compact_wave(0u, true);
+    if constexpr (!L::GL) {
+      // LDS lists, written by all lanes at once: lane l writes entries
+      // [KP/2 * half, KP/2 * (half + 1)) of its query's output (half 0's
+      // keys, then half 1's, then sentinels), and the two lanes of a query
+      // combine their minima.
+      const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
+      const uint32_t c0 = half == 0 ? cnt : other, c1 = half == 0 ? other : cnt;
+      const int q = qbase + qw;
+      const uint64_t* src = list_of(qw);
+      uint64_t mn = kSentinel;
+      uint64_t* dst = a.part + (int64_t(q < a.nq ? q : 0) * G + x) * KP;
+#pragma unroll
+      for (int i = 0; i < KP / 2; ++i) {
+        const uint32_t e = uint32_t(half * (KP / 2) + i);
+        const uint64_t key = e < c0 ? src[e] : (e < c0 + c1 ? src[L::HALF + (e - c0)] : kSentinel);
+        mn = key < mn ? key : mn;
+        if (q < a.nq) dst[e] = key;
+      }
+      const uint64_t y = shfl_xor_u64(mn, 32);
+      mn = y < mn ? y : mn;
+      if (half == 0 && q < a.nq) a.lmin[int64_t(q) * G + x] = mn;
+      return;
+    }
     for (int i = 0; i < 32; ++i) {
       const int m = wave * 32 + i;
       const int q = qbase + m;
@@ -712,7 +741,185 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Merge + exact re-rank, one workgroup (4 waves) per query.
+// Exact re-rank and output of one query's kp candidates (ids in s_cid,
+// 0xffffffff for none), by the four waves of a workgroup: exact fp32
+// distances from the fp32 rows, 4 candidates per wave at a time, then wave
+// 0 sorts them by (distance, id) and writes k results, padded with
+// UINT32_MAX / +inf (src/cagra.cpp:240-251).  Ends the kernel for waves
+// other than 0.
+// ---------------------------------------------------------------------------
+template <int E>
+__device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s_cd, int kp, const float* rows,
+                                                 int64_t d, const float* qv, int64_t q, int64_t k,
+                                                 uint32_t* out_nbr, float* out_dist) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(qv) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
+  for (int c = 4 * wave; c < kp; c += 4 * kWaves) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    uint32_t id[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) id[u] = c + u < kp ? s_cid[c + u] : 0xffffffffu;
+    if (vec) {
+      // Four 256-column chunks per pass, all loads issued before the first
+      // is used (one HBM round trip per pass for d <= 1024).
+      for (int64_t i0 = int64_t(lane) * 4; i0 < d; i0 += 4 * 256) {
+        float4 a4[4], b4[4][4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int64_t i = i0 + c * 256;
+          a4[c] = i < d ? *reinterpret_cast<const float4*>(qv + i) : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            b4[c][u] = (i < d && id[u] != 0xffffffffu) ? *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i)
+                                                        : float4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float t0 = a4[c].x - b4[c][u].x, t1 = a4[c].y - b4[c][u].y;
+            const float t2 = a4[c].z - b4[c][u].z, t3 = a4[c].w - b4[c][u].w;
+            acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+          }
+      }
+    } else {
+      for (int64_t i = lane; i < d; i += 64) {
+        const float a1 = qv[i];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (id[u] == 0xffffffffu) continue;
+          const float t = a1 - rows[int64_t(id[u]) * d + i];
+          acc[u] += t * t;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) acc[u] += __shfl_xor(acc[u], o);
+      if (lane == 0 && c + u < kp) s_cd[c + u] = acc[u];
+    }
+  }
+  __syncthreads();
+
+  if (wave != 0) return;
+  uint64_t fin[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int pos = e * 64 + lane;
+    const uint32_t id = pos < kp ? s_cid[pos] : 0xffffffffu;
+    fin[e] = id == 0xffffffffu ? kSentinel : (uint64_t(ord_f32(s_cd[pos])) << 32) | id;
+  }
+  wave_sort_e<E>(fin);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int64_t pos = e * 64 + lane;
+    if (pos < k) {
+      out_nbr[q * k + pos] = fin[e] == kSentinel ? 0xffffffffu : uint32_t(fin[e]);
+      out_dist[q * k + pos] = fin[e] == kSentinel ? INFINITY : unord_f32(uint32_t(fin[e] >> 32));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Merge + exact re-rank for kp <= 64, one workgroup (4 waves) per query.
+//  1. The kp-th smallest list minimum bounds the kp-th smallest key (kp list
+//     minima are kp distinct keys): only keys at or below it can be among
+//     the kp smallest.  Wave 0 computes it (a 256-key wave sort) while every
+//     wave's first batch of keys is already in flight.
+//  2. A key within the bound comes from one of the kp lists whose minimum is
+//     within it, so at most kp * kp keys pass.  The four waves stream all
+//     G * kp keys and append the passing ones to an LDS buffer of that size
+//     (one atomic per wave and batch).
+//  3. Wave 0 sorts the passing keys 64 at a time and merges them into its
+//     running sorted top-64; its first kp ids are re-ranked exactly.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __restrict__ part,
+                                                              const uint64_t* __restrict__ lmin, int G, int kp,
+                                                              const float* __restrict__ rows, int64_t d,
+                                                              const float* __restrict__ queries, int64_t k,
+                                                              uint32_t* __restrict__ out_nbr,
+                                                              float* __restrict__ out_dist) {
+  constexpr int kBatch = 16;        // keys per thread and batch
+  constexpr int kMaxPass = 64 * 64; // kp * kp for kp <= 64
+  __shared__ uint64_t s_pass[kMaxPass];
+  __shared__ uint32_t s_npass;
+  __shared__ uint64_t s_bound;
+  __shared__ uint32_t s_cid[64];
+  __shared__ float s_cd[64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t q = blockIdx.x;
+  const uint64_t* src = part + q * int64_t(G) * kp;
+  const int total = G * kp;
+  if (tid == 0) s_npass = 0;
+
+  // First batch of keys, requested before the bound is known.
+  uint64_t key[kBatch];
+#pragma unroll
+  for (int r = 0; r < kBatch; ++r) {
+    const int e = r * kThreads + tid;
+    key[r] = e < total ? src[e] : kSentinel;
+  }
+  // 1. Bound from the list minima (G <= 256), by wave 0.
+  if (wave == 0) {
+    uint64_t mins[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = lane + 64 * i;
+      mins[i] = x < G ? lmin[q * G + x] : kSentinel;
+    }
+    wave_sort_e<4>(mins);
+    uint64_t bound = kSentinel;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i == (kp - 1) / 64) bound = shfl_u64(mins[i], (kp - 1) % 64);
+    if (lane == 0) s_bound = bound;
+  }
+  __syncthreads();
+  const uint64_t bound = s_bound;
+
+  // 2. Filter every key; append the passing ones.
+  for (int b0 = 0; b0 < total; b0 += kBatch * kThreads) {
+    if (b0 > 0) {
+#pragma unroll
+      for (int r = 0; r < kBatch; ++r) {
+        const int e = b0 + r * kThreads + tid;
+        key[r] = e < total ? src[e] : kSentinel;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r) {
+      const bool pass = key[r] <= bound && key[r] != kSentinel;
+      const uint64_t m = __ballot(pass);
+      if (m == 0) continue;
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&s_npass, uint32_t(popc(m)));
+      base = uint32_t(__shfl(int(base), 0));
+      const uint32_t slot = base + uint32_t(mbcnt(m));
+      if (pass && slot < uint32_t(kMaxPass)) s_pass[slot] = key[r];
+    }
+  }
+  __syncthreads();
+
+  // 3. Wave 0: top-kp of the passing keys.
+  if (wave == 0) {
+    const int n = s_npass < uint32_t(kMaxPass) ? int(s_npass) : kMaxPass;
+    uint64_t run[1] = {kSentinel};
+    for (int r0 = 0; r0 < n; r0 += 64) {
+      uint64_t ck[1] = {r0 + lane < n ? s_pass[r0 + lane] : kSentinel};
+      wave_sort_e<1>(ck);
+      wave_merge<1>(run, ck[0]);
+    }
+    s_cid[lane] = (lane < kp && run[0] != kSentinel) ? uint32_t(run[0]) : 0xffffffffu;
+  }
+  __syncthreads();
+  rerank_and_write<1>(s_cid, s_cd, kp, rows, d, queries + q * d, q, k, out_nbr, out_dist);
+}
+
+// ---------------------------------------------------------------------------
+// Merge + exact re-rank for kp = 128 (global lists), one workgroup (4 waves)
+// per query.
 //  1. The kp-th smallest list minimum bounds the kp-th smallest key (kp list
 //     minima are kp distinct keys): only keys at or below it can be among
 //     the kp smallest.  Each wave computes it (a 256-key wave sort).
@@ -800,63 +1007,7 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
     }
   }
   __syncthreads();
-  const float* qv = queries + q * d;
-  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
-  for (int c = 4 * wave; c < kp; c += 4 * kWaves) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    uint32_t id[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) id[u] = c + u < kp ? s_cid[c + u] : 0xffffffffu;
-    if (vec) {
-      for (int64_t i = int64_t(lane) * 4; i < d; i += 256) {
-        const float4 a4 = *reinterpret_cast<const float4*>(qv + i);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (id[u] == 0xffffffffu) continue;
-          const float4 b4 = *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i);
-          const float t0 = a4.x - b4.x, t1 = a4.y - b4.y, t2 = a4.z - b4.z, t3 = a4.w - b4.w;
-          acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
-        }
-      }
-    } else {
-      for (int64_t i = lane; i < d; i += 64) {
-        const float a1 = qv[i];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (id[u] == 0xffffffffu) continue;
-          const float t = a1 - rows[int64_t(id[u]) * d + i];
-          acc[u] += t * t;
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc[u] += __shfl_xor(acc[u], o);
-      if (lane == 0 && c + u < kp) s_cd[c + u] = acc[u];
-    }
-  }
-  __syncthreads();
-
-  // 4. Sort by (exact distance, id) and write k results.
-  if (wave != 0) return;
-  uint64_t fin[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int pos = e * 64 + lane;
-    const uint32_t id = pos < kp ? s_cid[pos] : 0xffffffffu;
-    fin[e] = id == 0xffffffffu ? kSentinel : (uint64_t(ord_f32(s_cd[pos])) << 32) | id;
-  }
-  wave_sort_e<E>(fin);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int64_t pos = e * 64 + lane;
-    if (pos < k) {
-      out_nbr[q * k + pos] = fin[e] == kSentinel ? 0xffffffffu : uint32_t(fin[e]);
-      out_dist[q * k + pos] = fin[e] == kSentinel ? INFINITY : unord_f32(uint32_t(fin[e] >> 32));
-    }
-  }
+  rerank_and_write<E>(s_cid, s_cd, kp, rows, d, queries + q * d, q, k, out_nbr, out_dist);
 }
 
 // ---------------------------------------------------------------------------
@@ -1009,8 +1160,8 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
 
   hipEvent_t t3 = timer_begin(ctx, "bf_merge");
   if (kp <= 64)
-    hipLaunchKernelGGL(bf_merge_kernel<1>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
-                       static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, stride,
+    hipLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
+                       static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp,
                        static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   else
     hipLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,

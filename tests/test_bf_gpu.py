@@ -102,6 +102,9 @@ def test_reference_golden(ctx, oracle, name):
     (3000, 64, 40, 112),  # largest k
     (100, 32, 5, 112),    # k > n with global-memory lists
     (5000, 256, 33, 24),
+    (4000, 300, 50, 10),    # 32 k-steps per tile (k-split scan, one stage per tile)
+    (2500, 512, 130, 100),  # 32 k-steps, two query blocks, global-memory lists
+    (6000, 384, 20, 40),
     (2000, 1024, 5, 1),
     (3333, 1000, 9, 16),  # d not a power of two
     (40000, 128, 129, 10),
