@@ -211,7 +211,7 @@ void bf_scan_kernel(ScanArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
   const int G = a.n_ranges;
   const int x = a.qb_fast ? int(blockIdx.x) / a.n_qblocks : int(blockIdx.x);
   const int qbase = (a.qb_fast ? int(blockIdx.x) % a.n_qblocks : int(blockIdx.y)) * kQB;
@@ -282,25 +282,23 @@ void bf_scan_kernel(ScanArgs a) {
   const int qt = (qbase >> 5) + wave;
   const int my_q = qbase + wave * 32 + (lane & 31);
   const bool q_ok = my_q < a.nq;
-  // Loaded 16 k-steps at a time (16 loads in flight), then pinned to AGPRs:
-  // MFMA reads B from AGPRs, which leaves the arch VGPRs for the A-fragment
-  // ring, the accumulators and the epilogue.
+  // All KS operand loads are issued at once as buffer loads (a query tile
+  // past the last one reads as zeros without a memory access), landing in
+  // AGPRs, from which MFMA reads its B operand; this leaves the arch VGPRs
+  // for the A-fragment ring, the accumulators and the epilogue.  They are
+  // pinned to AGPRs only after the last load is issued, so the prologue
+  // waits for one round trip.
   half8 qb[KS];
   const bool qt_ok = qt < a.n_qtiles;
-  const u32x4* qsrc = a.qtiles + int64_t(qt_ok ? qt : 0) * KS * 64 + lane;
+  const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4*>(a.qtiles + int64_t(qt_ok ? qt : 0) * KS * 64), 0, qt_ok ? KS * kStepBytes : 0,
+      kRsrcWord3);
 #pragma unroll
-  for (int c = 0; c < KS; c += 16) {
-    constexpr int CH = KS < 16 ? KS : 16;
-    u32x4 tmp[CH];
+  for (int i = 0; i < KS; ++i)
+    qb[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                          qrsrc, uint32_t(lane) * 16u + uint32_t(i * kStepBytes), 0, 0));
 #pragma unroll
-    for (int i = 0; i < CH; ++i) tmp[i] = qsrc[(c + i) * 64];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      half8 h = __builtin_bit_cast(half8, qt_ok ? tmp[i] : u32x4{0, 0, 0, 0});
-      asm volatile("" : "+a"(h));
-      qb[c + i] = h;
-    }
-  }
+  for (int i = 0; i < KS; ++i) asm volatile("" : "+a"(qb[i]));
   const float qn = q_ok ? a.qnorms[my_q] : INFINITY;
   const int qw = wave * 32 + (lane & 31);  // this lane's query slot in the workgroup
   const int half = lane >> 5;              // which half of the query's list this lane fills
