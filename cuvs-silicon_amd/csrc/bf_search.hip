@@ -312,7 +312,7 @@ void bf_scan_kernel(ScanArgs a) {
   // to its KP smallest keys and lowers the query's threshold to the kp-th
   // distance when keys were dropped.
   auto compact_wave = [&](uint32_t limit, bool total_only) CVS_INLINE {
-    const uint32_t both = cnt + uint32_t(__shfl_xor(int(cnt), 32));
+    const uint32_t both = cnt + xor_lanes<32>(cnt);
     const uint64_t over64 = __ballot(total_only ? both > uint32_t(KP) : cnt > limit);
     uint32_t over = uint32_t(over64) | uint32_t(over64 >> 32);
     if (over == 0) return;
@@ -594,7 +594,7 @@ void bf_scan_kernel(ScanArgs a) {
       // [KP/2 * half, KP/2 * (half + 1)) of its query's output (half 0's
       // keys, then half 1's, then sentinels), and the two lanes of a query
       // combine their minima.
-      const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
+      const uint32_t other = xor_lanes<32>(cnt);
       const uint32_t c0 = half == 0 ? cnt : other, c1 = half == 0 ? other : cnt;
       const int q = qbase + qw;
       const uint64_t* src = list_of(qw);
@@ -698,7 +698,7 @@ __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restric
     }
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  for (int o = 32; o >= 1; o >>= 1) acc += xor_lanes_f(acc, o);
   if (lane == 0) qnorms[r] = ok ? acc : INFINITY;
 }
 
@@ -795,7 +795,7 @@ __device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
 #pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc[u] += __shfl_xor(acc[u], o);
+      for (int o = 32; o >= 1; o >>= 1) acc[u] += xor_lanes_f(acc[u], o);
       if (lane == 0 && c + u < kp) s_cd[c + u] = acc[u];
     }
   }

@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void to_half_rows_kernel(const float* __restri
     acc += hv * hv;
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  for (int o = 32; o >= 1; o >>= 1) acc += xor_lanes_f(acc, o);
   if (lane == 0) norms[r] = acc;
 }
 

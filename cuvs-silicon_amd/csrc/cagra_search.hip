@@ -92,7 +92,7 @@ __device__ __forceinline__ uint64_t wave_sort(uint64_t x) {
 template <int E>
 __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
   const int lane = __lane_id();
-  const uint64_t cr = shfl_u64(c, 63 - lane);
+  const uint64_t cr = shfl_xor_u64(c, 63);  // lane 63 - lane
   top[E - 1] = top[E - 1] < cr ? top[E - 1] : cr;
 #pragma unroll
   for (int s = E / 2; s >= 1; s >>= 1) {
@@ -209,10 +209,10 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
           acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
         }
       }
-      acc += __shfl_xor(acc, 8);
-      acc += __shfl_xor(acc, 4);
-      acc += __shfl_xor(acc, 2);
-      acc += __shfl_xor(acc, 1);
+      acc += xor_lanes_f(acc, 8);
+      acc += xor_lanes_f(acc, 4);
+      acc += xor_lanes_f(acc, 2);
+      acc += xor_lanes_f(acc, 1);
       if (ok && tp == 0) s_dist[r] = acc;
     }
     __syncthreads();

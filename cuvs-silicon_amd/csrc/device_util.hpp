@@ -24,9 +24,75 @@ __device__ __forceinline__ int mbcnt(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0));
 }
 
+// Value of x held by lane (this lane ^ M) of the wave, without the LDS
+// crossbar (ds_bpermute): lane ^ 1, 2, 3 within a quad are DPP quad
+// permutes, lane ^ 15 and lane ^ 7 within a 16-lane row are the DPP row and
+// half-row mirrors (so ^ 8 = row mirror then half-row mirror, ^ 4 = half-row
+// mirror then quad permute ^ 3), and ^ 16 / ^ 32 are the gfx950 permlane
+// swaps, which exchange the odd 16-lane rows (upper 32 lanes) of one operand
+// with the even rows (lower 32 lanes) of the other: with both operands = x,
+// a lane keeps the swapped copy that came from its partner.  Composite masks
+// compose these steps.
+namespace dpp {
+constexpr int quad_xor(int v) { return (0 ^ v) | ((1 ^ v) << 2) | ((2 ^ v) << 4) | ((3 ^ v) << 6); }
+constexpr int kRowMirror = 0x140;
+constexpr int kHalfMirror = 0x141;
+}  // namespace dpp
+
+template <int M>
+__device__ __forceinline__ uint32_t xor_lanes(uint32_t x) {
+  static_assert(M > 0 && M < 64, "lane mask");
+  typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+  const int lane = __lane_id();
+  if constexpr ((M & 32) != 0) {
+    const u32x2_t r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    x = (lane & 32) ? r.x : r.y;
+  }
+  if constexpr ((M & 16) != 0) {
+    const u32x2_t r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = (lane & 16) ? r.x : r.y;
+  }
+  constexpr int L = M & 15;
+  if constexpr (L == 15) {
+    x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::kRowMirror, 0xF, 0xF, false));
+  } else if constexpr (L == 7) {
+    x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::kHalfMirror, 0xF, 0xF, false));
+  } else {
+    if constexpr ((L & 8) != 0) {
+      x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::kRowMirror, 0xF, 0xF, false));
+      x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::kHalfMirror, 0xF, 0xF, false));
+    }
+    if constexpr ((L & 4) != 0) {
+      x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::kHalfMirror, 0xF, 0xF, false));
+      x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::quad_xor(3), 0xF, 0xF, false));
+    }
+    if constexpr ((L & 3) != 0) x = uint32_t(__builtin_amdgcn_mov_dpp(int(x), dpp::quad_xor(L & 3), 0xF, 0xF, false));
+  }
+  return x;
+}
+
+// Runtime-mask form for the butterfly strides of unrolled loops (the switch
+// folds to one case); other masks use ds_bpermute.
+__device__ __forceinline__ uint32_t xor_lanes(uint32_t x, int mask) {
+  switch (mask) {
+    case 1: return xor_lanes<1>(x);
+    case 2: return xor_lanes<2>(x);
+    case 4: return xor_lanes<4>(x);
+    case 8: return xor_lanes<8>(x);
+    case 16: return xor_lanes<16>(x);
+    case 32: return xor_lanes<32>(x);
+    case 63: return xor_lanes<63>(x);
+    default: return uint32_t(__shfl_xor(int(x), mask));
+  }
+}
+
+__device__ __forceinline__ float xor_lanes_f(float x, int mask) {
+  return __uint_as_float(xor_lanes(__float_as_uint(x), mask));
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int mask) {
-  const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(x)), mask));
-  const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(x >> 32)), mask));
+  const uint32_t lo = xor_lanes(uint32_t(x), mask);
+  const uint32_t hi = xor_lanes(uint32_t(x >> 32), mask);
   return (uint64_t(hi) << 32) | lo;
 }
 
@@ -74,7 +140,7 @@ __device__ __forceinline__ void wave_sort_e(uint64_t (&v)[E]) {
 template <int E>
 __device__ __forceinline__ void wave_merge(uint64_t (&v)[E], uint64_t c) {
   const int lane = __lane_id();
-  const uint64_t cr = shfl_u64(c, 63 - lane);
+  const uint64_t cr = shfl_xor_u64(c, 63);  // lane 63 - lane
   v[E - 1] = v[E - 1] < cr ? v[E - 1] : cr;
 #pragma unroll
   for (int s = E / 2; s >= 1; s >>= 1) {
