@@ -10,9 +10,10 @@
 //
 //  prep     queries fp32 -> fp16 32-row tiles + norms (the dataset layout),
 //           one wave per query.
-//  sample   the scan kernel over a strided sample of ~256*kp rows (at most
-//           16,384); each lane keeps the minimum distance of the rows it
-//           sees, so every (query, workgroup, half-wave) yields one minimum.
+//  sample   the scan kernel over an evenly strided sample of 32,768 rows
+//           (65,536 for large batches); each lane keeps the minimum distance
+//           of the rows it sees, so every (query, workgroup, half-wave)
+//           yields one minimum.
 //  select   per query (one wave), the kp-th smallest of those minima, T0.
 //           The kp smallest minima are kp distinct dataset rows, so at least
 //           kp rows lie at or below T0 and every row above it can be dropped
@@ -25,19 +26,21 @@
 //           accumulate, two accumulation chains), so each lane owns one query
 //           and 16 rows of the 32x32 result.  The epilogue forms
 //           d = |q|^2 + |x|^2 - 2 q.x and appends (d, row) to the query's list
-//           only if d is below the query's threshold (T0 at start).  A list
-//           that nears capacity is compacted by its wave to the kp smallest
+//           only if d is below the query's threshold (T0 at start).  Each
+//           list has two halves, one per lane of its query, with the count in
+//           a register; a rare append visits only the rows some lane passes.
+//           A half that fills up is compacted by its wave to the kp smallest
 //           keys (ballot radix select), lowering the threshold.  Lists of
 //           kp <= 64 live in LDS, kp = 128 lists in global memory.  Each list
 //           ends with its smallest key published for the merge.
-//  merge    one workgroup per query: the kp-th smallest list minimum
-//           bounds the kp-th smallest key; each wave streams a quarter of the
-//           lists and merges every 64-key row holding a key within the bound
-//           into its running top-kp (whose kp-th key tightens the bound); the
-//           four lists are merged, the kp candidates re-ranked with exact
-//           fp32 distances from the fp32 rows, sorted by (distance, id), and
-//           k results written, padded with UINT32_MAX / +inf
-//           (src/cagra.cpp:240-251).
+//  merge    one workgroup per query: the kp-th smallest list minimum bounds
+//           the kp-th smallest key.  For kp <= 64 every key within it (at
+//           most kp * kp) is gathered into LDS and one wave keeps the kp
+//           smallest; for kp = 128 each wave merges the 64-key rows holding a
+//           key within the bound into its running top-kp.  The kp candidates
+//           are re-ranked with exact fp32 distances from the fp32 rows,
+//           sorted by (distance, id), and k results written, padded with
+//           UINT32_MAX / +inf (src/cagra.cpp:240-251).
 //
 // The fp16 pass only *selects*; reported distances come from the fp32
 // re-rank, so distances agree with the reference's fp32 loop
@@ -1084,12 +1087,14 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   if (int64_t(G) > n_units) G = int(n_units);
   const int stride = global_lists ? Lists<128, kModeScan>::CAP : kp;
 
-  // Sample: 32,768 rows for small batches, 16,384 for large ones (whose scan
-  // is MFMA-bound), in whole units, evenly strided, over Gs workgroups;
-  // 2 minima per (query, workgroup).  The initial threshold then sits near
-  // rank kp * n / sample of each query's distances, so a workgroup's lists
-  // see about kp * n / (sample * G) appends per query over its range.
-  int64_t s_units = (large_batch ? 16384 : 32768) / rpu;
+  // Sample: 32,768 rows for small batches, 65,536 for large ones, in whole
+  // units, evenly strided, over Gs workgroups; 2 minima per (query,
+  // workgroup).  The initial threshold then sits near rank kp * n / sample
+  // of each query's distances, so a workgroup's lists see about
+  // kp * n / (sample * G) appends per query over its range: large batches
+  // (kp = 128 and only 32 dataset ranges) need the larger sample to keep
+  // appends and list compactions off the scan's critical path.
+  int64_t s_units = (large_batch ? 65536 : 32768) / rpu;
   if (s_units < 1) s_units = 1;
   if (s_units > n_units) s_units = n_units;
   const int64_t s_stride = n_units / s_units;
