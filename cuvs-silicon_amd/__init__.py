@@ -32,7 +32,7 @@ CVS_ERR_UNSUPPORTED = 5
 BF_MAX_DIM = 1024
 BF_MAX_K = 112
 CAGRA_MAX_DIM = 1024
-CAGRA_MAX_ITOPK = 256
+CAGRA_MAX_ITOPK = 512
 CAGRA_MAX_WIDTH = 16
 
 # Every extern "C" symbol declared in include/cvs_hip.h: name -> (restype, argtypes).

@@ -63,6 +63,7 @@ struct SearchArgs {
   int dq;  // float4 per padded row (16 * dv)
   int dv;  // float4 per lane and row
   int n_seeds;
+  int seed_lanes;  // seed candidates in all: n_seeds, then hashed ids
   int k;
   int itopk;
   int width;
@@ -225,13 +226,13 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
     __syncthreads();
   };
 
-  // Seeds: the seed nodes in chunks of 64; lanes past the last seed (all 64
-  // without seed nodes) take hashed ids led by the reference's fallback
-  // (q * 2654435761) mod n, so that regions no seed node reaches can still be
-  // entered.
+  // Seeds: seed_lanes candidates in chunks of 64, first the seed nodes, then
+  // hashed ids led by the reference's fallback (q * 2654435761) mod n, so that
+  // regions no seed node reaches (clusters the graph does not link) can still
+  // be entered.
   {
     const uint32_t h0 = uint32_t(qi) * 2654435761u;
-    for (int c = 0; c == 0 || c < a.n_seeds; c += 64) {
+    for (int c = 0; c < a.seed_lanes; c += 64) {
       if (count + 64 > hcap) reset_hash();
       const int i = c + lane;
       uint32_t id = kInvalidId;
@@ -312,7 +313,7 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   if (width > CVS_CAGRA_MAX_WIDTH) fail(CVS_ERR_UNSUPPORTED, "search_width exceeds CVS_CAGRA_MAX_WIDTH");
   const int64_t per_iter = width * int64_t(idx->degree);
   if (per_iter > 2048) fail(CVS_ERR_UNSUPPORTED, "search_width * graph_degree exceeds 2048");
-  const int e_slots = itopk <= 64 ? 1 : (itopk <= 128 ? 2 : 4);
+  const int e_slots = itopk <= 64 ? 1 : (itopk <= 128 ? 2 : (itopk <= 256 ? 4 : 8));
   int64_t iters = max_iterations;
   if (iters == 0) iters = std::max<int64_t>(200, 2 * itopk / width);
   const int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
@@ -332,6 +333,9 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.dq = int(idx->dpad / 4);
   a.dv = int(idx->dpad / 64);
   a.n_seeds = int(idx->n_seeds);
+  // At least itopk candidates (all seed nodes, then hashed ids), in whole
+  // chunks of 64: a list of itopk entries starts from as many distinct rows.
+  a.seed_lanes = int((std::max<int64_t>({int64_t(idx->n_seeds), itopk, 1}) + 63) / 64 * 64);
   a.k = int(k);
   a.itopk = int(itopk);
   a.width = int(width);
@@ -343,7 +347,8 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   switch (e_slots) {
     case 1: hipLaunchKernelGGL(cagra_search_kernel<1>, grid, block, lds, ctx->stream, a); break;
     case 2: hipLaunchKernelGGL(cagra_search_kernel<2>, grid, block, lds, ctx->stream, a); break;
-    default: hipLaunchKernelGGL(cagra_search_kernel<4>, grid, block, lds, ctx->stream, a); break;
+    case 4: hipLaunchKernelGGL(cagra_search_kernel<4>, grid, block, lds, ctx->stream, a); break;
+    default: hipLaunchKernelGGL(cagra_search_kernel<8>, grid, block, lds, ctx->stream, a); break;
   }
   after_launch("cagra_search_kernel");
   timer_end(ctx, "cagra_search", t0);

@@ -53,7 +53,7 @@ typedef struct cvs_cagra_index cvs_cagra_index; /* device-resident graph index (
 
 /* Limits of the graph search kernel (checked by cvs_cagra_search*). */
 #define CVS_CAGRA_MAX_DIM 1024
-#define CVS_CAGRA_MAX_ITOPK 256
+#define CVS_CAGRA_MAX_ITOPK 512
 #define CVS_CAGRA_MAX_WIDTH 16
 
 /* ---- errors, counters ---------------------------------------------------- */
@@ -151,6 +151,9 @@ int cvs_cagra_index_destroy(cvs_cagra_index* index);
  * itopk_size = internal list length (0 -> 128, raised to k if smaller,
  * at most CVS_CAGRA_MAX_ITOPK); search_width = parents expanded per
  * iteration (0 -> 1); max_iterations (0 -> max(200, 2*itopk/width)).
+ * The list starts from max(n_seeds, itopk) candidates rounded up to 64: all
+ * seed nodes, then hashed row ids led by the reference's (q * 2654435761)
+ * mod n (shaders/cagra_kernels.metal:65-67).
  * Results sorted by (distance, id), padded with UINT32_MAX / +inf.  Host
  * pointers, blocking. */
 int cvs_cagra_search(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,

@@ -92,6 +92,7 @@ def test_hashed_seeds_reach_a_component_without_seed_nodes(ctx):
     (3000, 100, 16, 32, 1),     # d not a multiple of 64, itopk < 64
     (2500, 1000, 32, 128, 4),
     (4000, 128, 32, 256, 2),
+    (5000, 256, 32, 512, 1),    # the reference harness's itopk
 ])
 def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width):
     rng = np.random.default_rng(n + d)
@@ -110,6 +111,26 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width):
     print(f"recall@{k}: gpu {r_gpu:.4f} restated reference {r_ref:.4f}")
     assert r_gpu >= r_ref - 0.01, (r_gpu, r_ref)
     assert r_gpu > 0.8
+
+
+def test_itopk_512_on_complete_graph_is_exact(ctx, oracle):
+    """itopk 512 (8 list slots per lane) and k up to 512: on a complete graph
+    the first expansion reaches every row, so the result is the exact top-k."""
+    rng = np.random.default_rng(512)
+    n, d = 600, 16
+    base = rng.standard_normal((n, d)).astype(np.float32)
+    qs = rng.standard_normal((5, d)).astype(np.float32)
+    idx = ctx.cagra_index(base, complete_graph(n), oracle.cagra_nav_nodes(n))
+    for k, itopk in [(500, 512), (512, 0), (300, 400)]:
+        nbr, dist = idx.search(qs, k, itopk_size=itopk)
+        ref_nbr, ref_dist = oracle.bf_exact(base, qs, k)
+        check_invariants(base, qs, nbr, dist)
+        np.testing.assert_allclose(dist, ref_dist, rtol=1e-5, atol=1e-6)
+        # Ids may differ only where two distances are equal up to fp32
+        # summation order (the kernel sums in a tree, the oracle in sequence).
+        swapped = nbr != ref_nbr
+        assert swapped.mean() < 0.01, (k, int(swapped.sum()))
+        np.testing.assert_allclose(dist[swapped], ref_dist[swapped], rtol=2e-6)
 
 
 def test_invalid_graph_entries_are_ignored(ctx, oracle):
@@ -153,9 +174,9 @@ def test_argument_errors(ctx, oracle):
     with pytest.raises(ValueError):
         idx.search(q, 0)
     with pytest.raises(ValueError):
-        idx.search(q, 4, itopk_size=257)
+        idx.search(q, 4, itopk_size=513)
     with pytest.raises(ValueError):
-        idx.search(q, 300)
+        idx.search(q, 600)
     with pytest.raises(ValueError):
         idx.search(q, 4, search_width=17)
     with pytest.raises(ValueError):

@@ -7,10 +7,17 @@
 - test_api_gpu (GPU): the FAISS v1.8 adapter flow and known answers, the
   dispatch test with its exact answers, the exact route and the brute_force
   namespace, build -> save -> load -> search recall.
+- test_loaders (no GPU): fvecs/ivecs and Cohere .bin readers.
+- cohere_wiki_validation (GPU): the reference's end-to-end harness CLI on
+  synthetic Cohere-format files, exact route and graph route, with the index
+  saved by one run and loaded by the next.
 """
 import os
+import re
+import struct
 import subprocess
 
+import numpy as np
 import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -25,6 +32,7 @@ def run(name, *args):
     print(p.stdout)
     print(p.stderr)
     assert p.returncode == 0, p.stderr
+    return p.stdout
 
 
 def test_api_cpu(tmp_path):
@@ -34,3 +42,42 @@ def test_api_cpu(tmp_path):
 @pytest.mark.gpu
 def test_api_gpu(tmp_path):
     run("test_api_gpu", str(tmp_path))
+
+
+def test_loaders(tmp_path):
+    run("test_loaders", str(tmp_path))
+
+
+def write_bin(path, a):
+    """Cohere .bin: int32 rows, int32 cols, row-major payload
+    (scripts/download_cohere_wiki.py:57-71)."""
+    with open(path, "wb") as f:
+        f.write(struct.pack("<ii", *a.shape))
+        a.tofile(f)
+
+
+@pytest.mark.gpu
+def test_cohere_harness(tmp_path, cvs):
+    import oracle
+
+    n, d, q, k = 12000, 1024, 100, 10
+    base = cvs.synth_clustered(777, cvs.STREAM_BASE, n, d)
+    queries = cvs.synth_clustered(777, cvs.STREAM_QUERIES, q, d)
+    gt, _ = oracle.bf_fp64(base, queries, k, threads=8)
+    paths = [str(tmp_path / f) for f in ("base.bin", "queries.bin", "gt.bin")]
+    write_bin(paths[0], base)
+    write_bin(paths[1], queries)
+    write_bin(paths[2], gt.astype(np.int32))
+
+    def recalls(out):
+        return [float(x) for x in re.findall(r"recall@10 = ([0-9.]+)", out)]
+
+    exact = run("cohere_wiki_validation", *paths, "10", "1", "2", "0")
+    assert "PASS" in exact and recalls(exact)[0] >= 0.99
+    idx = str(tmp_path / "index.cgra")
+    graph = run("cohere_wiki_validation", *paths, "10", "1", "2", "64", idx)
+    assert "PASS" in graph and os.path.getsize(idx) > 0
+    loaded = run("cohere_wiki_validation", *paths, "10", "1", "2", "64", "", idx)
+    assert "Load time" in loaded and "PASS" in loaded
+    # The loaded index searches exactly as the one it was saved from.
+    assert recalls(loaded)[0] == recalls(graph)[0]
