@@ -1,4 +1,4 @@
-// CAGRA graph search for gfx950: one 64-lane wave per query.
+// CAGRA graph search for gfx950: one workgroup of 1-8 waves per query.
 //
 // Replaces the reference's `cagra_beam_search` kernel
 // (shaders/cagra_kernels.metal:28-199, host src/metal_context.mm:918-1111)
@@ -17,12 +17,15 @@
 //    table is cleared and the ids of the itopk list re-inserted: an id that
 //    left the list can be evaluated again, but can never re-enter it (its key
 //    is above the list's current worst), so the list never holds duplicates.
-//  - candidates: processed 64 at a time (one id per lane).  New ids pass the
-//    hash, are compacted into LDS, and their distances are computed by four
-//    16-lane teams (each lane reads 16 bytes at a stride of 256 bytes, so a
-//    row is gathered in coalesced 256-byte segments and one load instruction
-//    serves four rows).  The 64 keys are sorted with a wave bitonic sort and
-//    merged into the itopk list with a bitonic merge.
+//  - candidates: processed 64 at a time (one id per lane of the lead wave).
+//    New ids pass the hash, are compacted into LDS, and their distances are
+//    computed by the 16-lane teams of all waves (each lane reads 16 bytes at
+//    a stride of 256 bytes, so a row is gathered in coalesced 256-byte
+//    segments and one load instruction serves four rows).  The 64 keys are
+//    sorted with a wave bitonic sort and merged into the itopk list with a
+//    bitonic merge.
+//  - waves per query: 1 for large batches; up to 8 when the batch is small
+//    and each query's chain of dependent gathers is the latency (Q = 1).
 //
 // Iteration: pick the first `width` unexpanded entries of the list as
 // parents, mark them, evaluate their neighbours.  Stop when the list holds no
@@ -118,8 +121,14 @@ __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
   }
 }
 
-template <int E>
-__global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
+// One workgroup of W waves per query.  Wave 0 (the lead wave) owns the
+// itopk list, the hash inserts, the sort and the merge; all 4W 16-lane teams
+// gather candidate rows, so a chunk of 64 candidates costs ceil(64 / 4W)
+// dependent gather rounds instead of 16.  W = 1 for large batches (no
+// barriers between waves are needed), W > 1 when few queries would leave most
+// of the GPU idle and the search is latency-bound.
+template <int E, int W>
+__global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   extern __shared__ uint32_t s_mem[];
   const int H = 1 << a.hash_bits;
   const uint32_t hmask = uint32_t(H) - 1u;
@@ -128,12 +137,21 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
   uint32_t* s_ids = s_mem + H;                           // 64 fresh ids
   float* s_dist = reinterpret_cast<float*>(s_ids + 64);  // their distances
   uint32_t* s_par = s_ids + 128;                         // parents of this iteration
+  // Control words written by the lead wave and read by all after a barrier:
+  // [0, 1] fresh-id count (alternating per chunk), [2] hash fill after a
+  // reset, [3, 4] parent count (alternating per iteration).  Alternating slots
+  // keep a write for the next step from racing a slow wave's read.
+  uint32_t* s_ctl = s_par + CVS_CAGRA_MAX_WIDTH;
 
-  const int lane = threadIdx.x;
+  constexpr int kThreads = 64 * W;
+  constexpr int kTeams = 4 * W;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const bool lead = W == 1 || __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
   const int64_t qi = blockIdx.x;
-  const int team = lane >> 4, tp = lane & 15;
+  const int team = tid >> 4, tp = lane & 15;
 
-  for (int i = lane; i < H; i += 64) s_hash[i] = kInvalidId;
+  for (int i = tid; i < H; i += kThreads) s_hash[i] = kInvalidId;
 
   // Query slice of this lane: float4 columns tp + 16 j of the padded row.
   float4 qv[kMaxDv];
@@ -151,11 +169,12 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
     qv[j] = t;
   }
 
-  uint64_t top[E];
+  uint64_t top[E];  // the list (lead wave)
 #pragma unroll
   for (int e = 0; e < E; ++e) top[e] = kEmptyKey;
-  int count = 0;       // ids in the hash table (wave-uniform)
-  uint32_t evals = 0;  // distance evaluations
+  int count = 0;       // ids in the hash table (workgroup-uniform)
+  uint32_t evals = 0;  // distance evaluations (lead wave)
+  int phase = 0;       // alternates the fresh-count slot
   __syncthreads();
 
   auto hash_insert = [&](uint32_t id) -> bool {
@@ -170,29 +189,39 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
 
   auto reset_hash = [&]() {
     __syncthreads();
-    for (int i = lane; i < H; i += 64) s_hash[i] = kInvalidId;
+    for (int i = tid; i < H; i += kThreads) s_hash[i] = kInvalidId;
     __syncthreads();
-    count = 0;
+    if (lead) {
+      int c = 0;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const bool v = top[e] != kEmptyKey;
-      if (v) hash_insert(uint32_t(top[e]) >> 1);
-      count += popc(__ballot(v));
+      for (int e = 0; e < E; ++e) {
+        const bool v = top[e] != kEmptyKey;
+        if (v) hash_insert(uint32_t(top[e]) >> 1);
+        c += popc(__ballot(v));
+      }
+      if (lane == 0) s_ctl[2] = uint32_t(c);
     }
     __syncthreads();
+    count = int(s_ctl[2]);
   };
 
-  // Evaluates one id per lane (kInvalidId for none) and merges the new ones.
+  // Evaluates the candidate ids held one per lane of the lead wave
+  // (kInvalidId for none) and merges the new ones into the list.
   auto process = [&](uint32_t id) {
-    const bool fresh = id < a.n && hash_insert(id);
-    const uint64_t m = __ballot(fresh);
-    const int nf = popc(m);
+    uint32_t* const s_nf = s_ctl + phase;
+    phase ^= 1;
+    if (lead) {
+      const bool fresh = id < a.n && hash_insert(id);
+      const uint64_t m = __ballot(fresh);
+      if (fresh) s_ids[mbcnt(m)] = id;
+      if (lane == 0) *s_nf = uint32_t(popc(m));
+    }
+    __syncthreads();
+    const int nf = int(*s_nf);
     if (nf == 0) return;
-    if (fresh) s_ids[mbcnt(m)] = id;
     count += nf;
     evals += uint32_t(nf);
-    __syncthreads();
-    for (int r0 = 0; r0 < nf; r0 += 4) {
+    for (int r0 = 0; r0 < nf; r0 += kTeams) {
       const int r = r0 + team;
       const bool ok = r < nf;
       const uint32_t rid = s_ids[ok ? r : 0];
@@ -217,13 +246,18 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
       if (ok && tp == 0) s_dist[r] = acc;
     }
     __syncthreads();
-    const uint64_t key =
-        lane < nf ? (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1) : kEmptyKey;
-    merge_into<E>(top, wave_sort(key));
+    if (lead) {
+      const uint64_t key =
+          lane < nf ? (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1) : kEmptyKey;
+      merge_into<E>(top, wave_sort(key));
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-      if (e * 64 + lane >= a.itopk) top[e] = kEmptyKey;
-    __syncthreads();
+      for (int e = 0; e < E; ++e)
+        if (e * 64 + lane >= a.itopk) top[e] = kEmptyKey;
+    }
+    // With one wave, program order alone separates this chunk's LDS reads
+    // from the next chunk's writes; with more, the lead wave writes the next
+    // chunk's ids only after every wave has passed the barrier above.
+    if (W == 1) __syncthreads();
   };
 
   // Seeds: seed_lanes candidates in chunks of 64, first the seed nodes, then
@@ -236,10 +270,12 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
       if (count + 64 > hcap) reset_hash();
       const int i = c + lane;
       uint32_t id = kInvalidId;
-      if (i < a.n_seeds)
-        id = a.seeds[i];
-      else if (uint32_t(i - a.n_seeds) < a.n)
-        id = (h0 + uint32_t(i - a.n_seeds) * 0x9E3779B9u) % a.n;
+      if (lead) {
+        if (i < a.n_seeds)
+          id = a.seeds[i];
+        else if (uint32_t(i - a.n_seeds) < a.n)
+          id = (h0 + uint32_t(i - a.n_seeds) * 0x9E3779B9u) % a.n;
+      }
       process(id);
     }
   }
@@ -248,27 +284,32 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
   int it = 0;
   for (; it < a.max_iter; ++it) {
     if (count + a.width * a.g > hcap) reset_hash();
-    int np = 0;
+    uint32_t* const s_np = s_ctl + 3 + (it & 1);
+    if (lead) {
+      int np = 0;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      uint64_t m = __ballot(top[e] != kEmptyKey && (top[e] & 1ull) == 0);
-      while (m != 0 && np < a.width) {
-        const int b = __builtin_ctzll(m);
-        m &= m - 1;
-        if (lane == b) {
-          s_par[np] = uint32_t(top[e]) >> 1;
-          top[e] |= 1ull;
+      for (int e = 0; e < E; ++e) {
+        uint64_t m = __ballot(top[e] != kEmptyKey && (top[e] & 1ull) == 0);
+        while (m != 0 && np < a.width) {
+          const int b = __builtin_ctzll(m);
+          m &= m - 1;
+          if (lane == b) {
+            s_par[np] = uint32_t(top[e]) >> 1;
+            top[e] |= 1ull;
+          }
+          ++np;
         }
-        ++np;
       }
+      if (lane == 0) *s_np = uint32_t(np);
     }
-    if (np == 0) break;
     __syncthreads();
+    const int np = int(*s_np);
+    if (np == 0) break;
     const int total = np * a.g;
     for (int c = 0; c < total; c += 64) {
       const int f = c + lane;
       uint32_t id = kInvalidId;
-      if (f < total) {
+      if (lead && f < total) {
         const int p = f / a.g;
         const int j = f - p * a.g;
         id = a.graph[int64_t(s_par[p]) * a.g + j];
@@ -277,18 +318,43 @@ __global__ __launch_bounds__(64) void cagra_search_kernel(SearchArgs a) {
     }
   }
 
+  if (lead) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int pos = e * 64 + lane;
-    if (pos < a.k) {
-      const uint64_t key = top[e];
-      a.out_nbr[qi * a.k + pos] = key == kEmptyKey ? kInvalidId : uint32_t(key) >> 1;
-      a.out_dist[qi * a.k + pos] = key == kEmptyKey ? INFINITY : unord_f32(uint32_t(key >> 32));
+    for (int e = 0; e < E; ++e) {
+      const int pos = e * 64 + lane;
+      if (pos < a.k) {
+        const uint64_t key = top[e];
+        a.out_nbr[qi * a.k + pos] = key == kEmptyKey ? kInvalidId : uint32_t(key) >> 1;
+        a.out_dist[qi * a.k + pos] = key == kEmptyKey ? INFINITY : unord_f32(uint32_t(key >> 32));
+      }
+    }
+    if (a.stats && lane == 0) {
+      a.stats[2 * qi] = evals;
+      a.stats[2 * qi + 1] = uint32_t(it);
     }
   }
-  if (a.stats && lane == 0) {
-    a.stats[2 * qi] = evals;
-    a.stats[2 * qi + 1] = uint32_t(it);
+}
+
+// Waves per query: doubled while the grid stays within kWaveBudget waves (8
+// per CU), at most 8 (one query then gathers up to 32 rows per round).
+// Measured at N=100K D=1024 itopk 64 (kernel time, W = 1 / 2 / 4 / 8):
+// Q=1 0.82 / 0.51 / 0.40 / 0.34 ms, Q=100 0.91 / 0.58 / 0.47 / 0.41 ms,
+// Q=1,000 1.27 / 1.18 / 1.32 / 1.68 ms, Q=10,000 11.7 / 11.7 / 11.3 / 16.0 ms.
+constexpr int64_t kWaveBudget = 8 * 256;
+
+int waves_per_query(int64_t q) {
+  int w = 1;
+  while (w < 8 && q * w * 2 <= kWaveBudget) w *= 2;
+  return w;
+}
+
+template <int E>
+void launch_search(int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a) {
+  switch (waves) {
+    case 1: hipLaunchKernelGGL((cagra_search_kernel<E, 1>), grid, dim3(64), lds, stream, a); break;
+    case 2: hipLaunchKernelGGL((cagra_search_kernel<E, 2>), grid, dim3(128), lds, stream, a); break;
+    case 4: hipLaunchKernelGGL((cagra_search_kernel<E, 4>), grid, dim3(256), lds, stream, a); break;
+    default: hipLaunchKernelGGL((cagra_search_kernel<E, 8>), grid, dim3(512), lds, stream, a); break;
   }
 }
 
@@ -317,7 +383,7 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   int64_t iters = max_iterations;
   if (iters == 0) iters = std::max<int64_t>(200, 2 * itopk / width);
   const int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
-  const size_t lds = (size_t(1) << hash_bits) * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH) * 4;
+  const size_t lds = (size_t(1) << hash_bits) * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4;
 
   SearchArgs a{};
   a.rows = reinterpret_cast<const float4*>(idx->rows);
@@ -343,12 +409,13 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.hash_bits = hash_bits;
 
   hipEvent_t t0 = timer_begin(ctx, "cagra_search");
-  const dim3 grid(static_cast<unsigned>(q)), block(64);
+  const dim3 grid(static_cast<unsigned>(q));
+  const int waves = waves_per_query(q);
   switch (e_slots) {
-    case 1: hipLaunchKernelGGL(cagra_search_kernel<1>, grid, block, lds, ctx->stream, a); break;
-    case 2: hipLaunchKernelGGL(cagra_search_kernel<2>, grid, block, lds, ctx->stream, a); break;
-    case 4: hipLaunchKernelGGL(cagra_search_kernel<4>, grid, block, lds, ctx->stream, a); break;
-    default: hipLaunchKernelGGL(cagra_search_kernel<8>, grid, block, lds, ctx->stream, a); break;
+    case 1: launch_search<1>(waves, grid, lds, ctx->stream, a); break;
+    case 2: launch_search<2>(waves, grid, lds, ctx->stream, a); break;
+    case 4: launch_search<4>(waves, grid, lds, ctx->stream, a); break;
+    default: launch_search<8>(waves, grid, lds, ctx->stream, a); break;
   }
   after_launch("cagra_search_kernel");
   timer_end(ctx, "cagra_search", t0);
