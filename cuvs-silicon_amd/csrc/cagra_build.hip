@@ -6,7 +6,7 @@
 // (:334-395) that recomputes full 2-hop distance sets per node.  Here every
 // phase runs on the GPU and no update is lost to a race:
 //
-//  1. convert   fp32 rows -> fp16 rows (row stride dp = d rounded up to 64)
+//  1. convert   fp32 rows -> fp16 rows (row stride dp = d rounded up to 128)
 //               + fp32 squared norms of the fp16-rounded rows.
 //  2. bucket    rows are split into buckets of 256 consecutive entries of a
 //               random permutation (the reference's LCG Fisher-Yates,
@@ -62,8 +62,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint64_t kEmpty = ~0ull;
 constexpr uint32_t kInvalid = 0xffffffffu;
-constexpr int kChunkBytes = 128;  // 64 fp16 dimensions per staged chunk
-constexpr int kStageStride = 144; // bytes per staged row (128 + 16 against bank conflicts)
+// Bytes of each member row staged per step (64 fp16 dimensions); a staged
+// row is padded by 16 bytes against LDS bank conflicts.  Larger join chunks
+// (256 and 512 bytes per row per step) measured slower at N=1M D=1024: their
+// registers and LDS cost occupancy, which the join needs more.
+constexpr int kBucketChunkBytes = 128;
+constexpr int kJoinChunkBytes = 128;
+constexpr int kRowAlignDims = 128;  // fp16 row stride: d rounded up to this
 constexpr int kSample = 32;       // sampled forward/reverse new/old neighbours
 constexpr int kJoinM = 4 * kSample;
 constexpr int kBin = 128;         // update bin capacity per node
@@ -78,28 +83,35 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return uint32_t(k) >> 1
 
 // ---------------------------------------------------------------------------
 // Gram tiles of a set of fp16 rows.  The member rows s_ids[0..m) (m <= M)
-// are staged 64 dimensions at a time (M x 128 B, rows 144 B apart; rows >= m
-// are neither loaded nor used) and each wave accumulates NT 32x32 tiles:
-// tile t = rows 32*rt[t].., columns 32*ct[t]..  Loads run DEPTH chunks ahead
-// of the multiply.
+// are staged 64 dimensions at a time (M x 128 B, rows 144 B apart) and each
+// wave accumulates NT 32x32 tiles: tile t = rows 32*rt[t].., columns
+// 32*ct[t]..  Loads run DEPTH chunks ahead of the multiply.
+//
+// The gathers have no per-row branches: staging rows >= m re-read member 0's
+// row (a valid address, a cache hit; their products are never used) and the
+// prefetch past the last chunk re-reads the last chunk.  A branch around a
+// load makes the compiler wait for every outstanding load where the branch
+// rejoins, which would leave one chunk in flight whatever DEPTH is.
 // ---------------------------------------------------------------------------
-template <int M, int NT, int DEPTH>
-__device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t row_bytes, int n_chunks, int m,
+template <int M, int NT, int DEPTH, int CB>
+__device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t row_bytes, int m,
                                            const uint32_t* s_ids, char* s_stage, const int (&rt)[NT],
                                            const int (&ct)[NT], f32x16 (&acc)[NT]) {
-  constexpr int LPT = M * 8 / 256;  // 16-byte loads per thread and chunk
+  constexpr int SEG = CB / 16;        // 16-byte segments per staged row
+  constexpr int STRIDE = CB + 16;     // staged row pitch
+  constexpr int LPT = M * SEG / 256;  // 16-byte loads per thread and chunk
+  static_assert(LPT * 256 == M * SEG, "staging split");
+  const int n_chunks = int(row_bytes / CB);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const char* src[LPT];
   int dst[LPT];
-  bool live[LPT];
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
     const int idx = tid + 256 * i;
-    const int r = idx >> 3, seg = idx & 7;
-    live[i] = r < m;
-    src[i] = x16 + int64_t(s_ids[live[i] ? r : 0]) * row_bytes + seg * 16;
-    dst[i] = r * kStageStride + seg * 16;
+    const int r = idx / SEG, seg = idx % SEG;
+    src[i] = x16 + int64_t(s_ids[r < m ? r : 0]) * row_bytes + seg * 16;
+    dst[i] = r * STRIDE + seg * 16;
   }
   bool tile_live[NT];
 #pragma unroll
@@ -108,38 +120,106 @@ __device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
   }
+  const int last = n_chunks - 1;
+  // Prologue loads in chunk order (the scheduler may not interleave them), so
+  // that the loop's first use of chunk c waits only for the loads up to it.
   u32x4 reg[DEPTH][LPT];
 #pragma unroll
-  for (int c = 0; c < DEPTH; ++c)
+  for (int c = 0; c < DEPTH; ++c) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i)
-      if (live[i] && c < n_chunks)
-        reg[c][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(c) * kChunkBytes);
-  for (int c0 = 0; c0 < n_chunks; c0 += DEPTH) {
+      reg[c][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c, last)) * CB);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // One chunk: stage it, prefetch chunk c + DEPTH into the freed registers,
+  // multiply.
+  auto step = [&](int c, u32x4(&r)[LPT]) {
+    __syncthreads();
 #pragma unroll
-    for (int cc = 0; cc < DEPTH; ++cc) {
-      const int c = c0 + cc;
-      if (c >= n_chunks) break;
-      __syncthreads();
+    for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = r[i];
+    __syncthreads();
 #pragma unroll
-      for (int i = 0; i < LPT; ++i)
-        if (live[i]) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[cc][i];
-      __syncthreads();
-      if (c + DEPTH < n_chunks) {
+    for (int i = 0; i < LPT; ++i)
+      r[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + DEPTH, last)) * CB);
 #pragma unroll
-        for (int i = 0; i < LPT; ++i)
-          if (live[i]) reg[cc][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(c + DEPTH) * kChunkBytes);
+    for (int s = 0; s < CB / 32; ++s) {
+      const int koff = s * 32 + 16 * (lane >> 5);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (!tile_live[t]) continue;
+        const half8 a = *reinterpret_cast<const half8*>(s_stage + (32 * rt[t] + (lane & 31)) * STRIDE + koff);
+        const half8 b = *reinterpret_cast<const half8*>(s_stage + (32 * ct[t] + (lane & 31)) * STRIDE + koff);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
       }
+    }
+  };
+  // Whole groups of DEPTH chunks first: a loop body without early exits
+  // reaches its back edge with the loads in chunk order, so each stage waits
+  // only for its own chunk.  Then the remaining n_chunks % DEPTH chunks.
+  int c0 = 0;
+  for (; c0 + DEPTH <= n_chunks; c0 += DEPTH) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int koff = s * 32 + 16 * (lane >> 5);
+    for (int cc = 0; cc < DEPTH; ++cc) step(c0 + cc, reg[cc]);
+  }
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          if (!tile_live[t]) continue;
-          const half8 a = *reinterpret_cast<const half8*>(s_stage + (32 * rt[t] + (lane & 31)) * kStageStride + koff);
-          const half8 b = *reinterpret_cast<const half8*>(s_stage + (32 * ct[t] + (lane & 31)) * kStageStride + koff);
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
-        }
+  for (int cc = 0; cc + 1 < DEPTH; ++cc)
+    if (c0 + cc < n_chunks) step(c0 + cc, reg[cc]);
+}
+
+// Gram columns of the local join: rows s_ids[0..m), 32 < m <= 32*R (or
+// m <= 32 with R = 1), staged CB bytes per row and step.  Wave w < R computes
+// column tile w against the R row tiles into acc[0..R); waves >= R only
+// stage.  All tile guards are resolved by the template and one uniform branch
+// per chunk, so each k-step's LDS operand reads (one B tile, R A tiles) sit in
+// one basic block with its R MFMAs and can be issued ahead of them.
+template <int R, int CB>
+__device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t row_bytes, int m,
+                                          const uint32_t* s_ids, char* s_stage, int wave, f32x16 (&acc)[4]) {
+  constexpr int M = 32 * R;
+  constexpr int SEG = CB / 16;
+  constexpr int STRIDE = CB + 16;
+  constexpr int LPT = M * SEG / 256;
+  static_assert(LPT * 256 == M * SEG, "staging split");
+  const int n_chunks = int(row_bytes / CB);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const char* src[LPT];
+  int dst[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int idx = tid + 256 * i;
+    const int r = idx / SEG, seg = idx % SEG;
+    src[i] = x16 + int64_t(s_ids[r < m ? r : 0]) * row_bytes + seg * 16;
+    dst[i] = r * STRIDE + seg * 16;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
+  const bool live = wave < R;
+  const int last = n_chunks - 1;
+  const char* a_base = s_stage + (lane & 31) * STRIDE + 16 * (lane >> 5);
+  const char* b_base = a_base + 32 * wave * STRIDE;
+  u32x4 reg[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) reg[i] = *reinterpret_cast<const u32x4*>(src[i]);
+  for (int c = 0; c < n_chunks; ++c) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < LPT; ++i)
+      reg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + 1, last)) * CB);
+    if (live) {
+#pragma unroll
+      for (int s = 0; s < CB / 32; ++s) {
+        const half8 b = *reinterpret_cast<const half8*>(b_base + s * 32);
+        half8 av[R];
+#pragma unroll
+        for (int t = 0; t < R; ++t) av[t] = *reinterpret_cast<const half8*>(a_base + 32 * t * STRIDE + s * 32);
+#pragma unroll
+        for (int t = 0; t < R; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], b, acc[t], 0, 0, 0);
       }
     }
   }
@@ -171,7 +251,6 @@ struct BuildArgs {
   const char* x16;       // n x dp fp16
   const float* norms;    // n
   int64_t row_bytes;     // dp * 2
-  int n_chunks;          // dp / 64
   uint32_t n;
   int kd;                // list length (intermediate degree, <= n - 1)
   int kp;                // list stride (kd rounded up to 64)
@@ -192,11 +271,11 @@ struct BuildArgs {
 // rounds (to_bins = 1): each row's kBucketEmit nearest mates go to its
 // update bin, for the apply kernel to merge into the list.
 __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t* __restrict__ perm, int to_bins) {
-  __shared__ __attribute__((aligned(16))) char s_stage[kBucket * kStageStride];
+  __shared__ __attribute__((aligned(16))) char s_stage[kBucket * (kBucketChunkBytes + 16)];
   __shared__ float s_dist[64 * 257];  // one 64-row block of the bucket's distances
   __shared__ uint32_t s_ids[kBucket];
   __shared__ float s_norm[kBucket];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t start = int64_t(blockIdx.x) * kBucket;
   const int mb = int(std::min<int64_t>(kBucket, int64_t(a.n) - start));
   {
@@ -210,7 +289,7 @@ __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t
     const int rt[4] = {2 * rb, 2 * rb, 2 * rb + 1, 2 * rb + 1};
     const int ct[4] = {2 * wave, 2 * wave + 1, 2 * wave, 2 * wave + 1};
     f32x16 acc[4];
-    gram_tiles<kBucket, 4, 1>(a.x16, a.row_bytes, a.n_chunks, mb, s_ids, s_stage, rt, ct, acc);
+    gram_tiles<kBucket, 4, 1, kBucketChunkBytes>(a.x16, a.row_bytes, mb, s_ids, s_stage, rt, ct, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -297,14 +376,14 @@ __global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
 // partners in registers (at least one of the pair new, below the member's
 // current worst key), merges them with the partner lane's, and appends them
 // to its update bin.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void join_kernel(BuildArgs a) {
-  __shared__ __attribute__((aligned(16))) char s_stage[kJoinM * kStageStride];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void join_kernel(BuildArgs a) {
+  __shared__ __attribute__((aligned(16))) char s_stage[kJoinM * (kJoinChunkBytes + 16)];
   __shared__ uint32_t s_ids[kJoinM];
   __shared__ float s_norm[kJoinM];
   __shared__ uint64_t s_worst[kJoinM];
   __shared__ int s_m[2];  // members, new members
   __shared__ unsigned int s_emit;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t u = blockIdx.x;
   if (tid < 64) {
     // Lane-parallel member list: new forward, new reverse, old forward, old reverse.
@@ -327,18 +406,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     }
   }
   __syncthreads();
-  const int m = s_m[0], mnew = s_m[1];
+  // Wave-uniform in registers the compiler knows to be scalar, so that the
+  // tile and row guards below are scalar branches.
+  const int m = __builtin_amdgcn_readfirstlane(s_m[0]), mnew = __builtin_amdgcn_readfirstlane(s_m[1]);
   if (mnew == 0 || m < 2) return;
+  // Norm and current worst key of member tid: loaded now, stored after the
+  // Gram matrix, so that their latency overlaps the first row gathers.
+  float member_norm;
+  uint64_t member_worst;
+  {
+    const uint32_t id = s_ids[tid < m ? tid : 0];
+    member_norm = a.norms[id];
+    member_worst = a.lists[int64_t(id) * a.kp + a.kd - 1] | 1ull;
+  }
+  // Row tiles in use: most nodes hold at most 64 members once the lists
+  // settle, and stage only those rows.
+  f32x16 acc[4];
+  if (m <= 32)
+    gram_join<1, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
+  else if (m <= 64)
+    gram_join<2, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
+  else if (m <= 96)
+    gram_join<3, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
+  else
+    gram_join<4, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
   if (tid < m) {
-    const uint32_t id = s_ids[tid];
-    s_norm[tid] = a.norms[id];
-    s_worst[tid] = a.lists[int64_t(id) * a.kp + a.kd - 1] | 1ull;
+    s_norm[tid] = member_norm;
+    s_worst[tid] = member_worst;
   }
   __syncthreads();
-  const int rt[4] = {0, 1, 2, 3};
-  const int ct[4] = {wave, wave, wave, wave};
-  f32x16 acc[4];
-  gram_tiles<kJoinM, 4, 1>(a.x16, a.row_bytes, a.n_chunks, m, s_ids, s_stage, rt, ct, acc);
 
   const int col = 32 * wave + (lane & 31);
   const int half = lane >> 5;
@@ -704,7 +800,9 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   const int g = int(std::min<int64_t>(graph_degree, kd));
   const int kp = (kd + 63) / 64 * 64;
   const int e_slots = kp / 64 == 3 ? 4 : kp / 64;
-  const int64_t dp = (d + 63) / 64 * 64;
+  const int64_t dp = (d + kRowAlignDims - 1) / kRowAlignDims * kRowAlignDims;
+  static_assert(kRowAlignDims * 2 % kJoinChunkBytes == 0 && kRowAlignDims * 2 % kBucketChunkBytes == 0,
+                "row stride must hold whole chunks");
   hipStream_t st = ctx->stream;
   cvs_build_stats s{};
 
@@ -740,7 +838,6 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   a.x16 = reinterpret_cast<const char*>(x16);
   a.norms = norms;
   a.row_bytes = dp * 2;
-  a.n_chunks = int(dp / 64);
   a.n = uint32_t(n);
   a.kd = kd;
   a.kp = kp;
