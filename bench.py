@@ -380,7 +380,8 @@ def run_cagra_search(args) -> int:
     dd = cvs.DeviceArray(ctx, (q, k), np.float32)
     st = cvs.DeviceArray(ctx, (q, 2), np.uint32)
     results = []
-    for width in (1, 4):
+    for bits, width in ((16, 1), (16, 4), (32, 1), (32, 4)):
+        idx.set_traversal(bits)
         for _ in range(2):
             idx.search_async(dq, k, dn, dd, itopk_size=args.itopk, search_width=width)
         ctx.synchronize()
@@ -396,12 +397,15 @@ def run_cagra_search(args) -> int:
         ctx.set_timing(False)
         stats = st.to_host().astype(np.int64)
         nbr = dn.to_host()
-        if width == 1:
+        if width == 1 and bits == 16:
             nbr_w1 = nbr.copy()
-        # algorithmic bytes per query: distance evaluations x D*4 + expanded
-        # nodes x degree*4 (graph rows) + D*4 (the query)
+        # algorithmic bytes per query: distance evaluations x D x (2 for the
+        # fp16 traversal copy, 4 for fp32 rows) + with fp16 traversal the
+        # fp32 re-rank of the itopk list (itopk x D*4) + expanded nodes x
+        # degree*4 (graph rows) + D*4 (the query)
         expanded = stats[:, 1] * width
-        alg_bytes = float((stats[:, 0] * d * 4 + expanded * args.degree * 4 + d * 4).sum())
+        rerank = args.itopk * d * 4 if bits == 16 else 0
+        alg_bytes = float((stats[:, 0] * d * (bits // 8) + rerank + expanded * args.degree * 4 + d * 4).sum())
         # Q=1 latency: 100 distinct queries, one call each (launch to results
         # on the device, synchronised), then the kernel alone (HIP events)
         dn1 = cvs.DeviceArray(ctx, (1, k), np.uint32)
@@ -423,7 +427,7 @@ def run_cagra_search(args) -> int:
         ctx.set_timing(False)
         lat.sort()
         res = {
-            "search_width": width, "qps": q / dt, "ms_per_batch": dt * 1e3, "kernel_ms": kms,
+            "traversal_bits": bits, "search_width": width, "qps": q / dt, "ms_per_batch": dt * 1e3, "kernel_ms": kms,
             "recall_at_10": recall_at_k(nbr, gt, k), "q1_latency_ms_p50": 1e3 * lat[50],
             "q1_latency_ms_p99": 1e3 * lat[98], "q1_kernel_ms": k1ms / max(k1n, 1), "q1_recall_at_10": hits / 1000,
             "mean_distance_evaluations": float(stats[:, 0].mean()), "mean_iterations": float(stats[:, 1].mean()),
@@ -444,7 +448,7 @@ def run_cagra_search(args) -> int:
     out = {
         "metric": "CAGRA search QPS at recall@10, N=100K D=1024 degree 64 itopk 64 K=10 Q=10,000",
         "value": results[0]["qps"], "unit": "queries/s", "n_gpus": 1, "higher_is_better": True,
-        "dtype": "f32", "data": "synthetic",
+        "dtype": "f16 traversal, f32 re-rank", "data": "synthetic",
         "config": {"workload": f"CAGRA graph search, N={n} D={d} Q={q} K={k} itopk={args.itopk} "
                                f"degree={args.degree}, graph built on the GPU", "seed": args.seed},
         "widths": results,

@@ -60,6 +60,7 @@ _SIGNATURES = {
     "cvs_cagra_index_create": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_uint32, c_int,
                                        c_void_p, c_uint32, POINTER(c_void_p)]),
     "cvs_cagra_index_destroy": (c_int, [c_void_p]),
+    "cvs_cagra_index_set_traversal": (c_int, [c_void_p, c_int]),
     "cvs_cagra_search": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
                                  c_void_p, c_void_p]),
     "cvs_cagra_search_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
@@ -227,8 +228,8 @@ class Context:
     def dataset(self, rows) -> "Dataset":
         return Dataset(self, rows)
 
-    def cagra_index(self, rows, graph, seeds=None) -> "CagraIndex":
-        return CagraIndex(self, rows, graph, seeds)
+    def cagra_index(self, rows, graph, seeds=None, traversal_bits: int = 16) -> "CagraIndex":
+        return CagraIndex(self, rows, graph, seeds, traversal_bits)
 
     def cagra_build(self, rows, intermediate_degree: int = 128, graph_degree: int = 64, max_iterations: int = 20,
                     termination_threshold: float = 0.001, seed: int = DEFAULT_BUILD_SEED, out: "DeviceArray" = None):
@@ -306,7 +307,7 @@ class CagraIndex:
     """Device-resident graph index (C: cvs_cagra_index): rows, neighbour lists
     and seed (navigation) node ids."""
 
-    def __init__(self, ctx: Context, rows, graph, seeds=None):
+    def __init__(self, ctx: Context, rows, graph, seeds=None, traversal_bits: int = 16):
         self.ctx = ctx
         h = c_void_p()
         graph_dev = isinstance(graph, DeviceArray)
@@ -336,6 +337,13 @@ class CagraIndex:
                                              byref(h)))
         self.handle = h
         self.n, self.d, self.degree = int(n), int(d), int(degree)
+        self.set_traversal(traversal_bits)
+
+    def set_traversal(self, bits: int) -> None:
+        """16: candidates evaluated on the fp16 copy, final list re-ranked in
+        fp32; 32: every evaluation on the fp32 rows."""
+        _check(load().cvs_cagra_index_set_traversal(self.handle, int(bits)))
+        self.traversal_bits = int(bits)
 
     def close(self) -> None:
         if self.handle is not None:

@@ -50,10 +50,14 @@ namespace {
 
 constexpr uint32_t kInvalidId = 0xffffffffu;
 constexpr uint64_t kEmptyKey = ~0ull;
-constexpr int kMaxDv = CVS_CAGRA_MAX_DIM / 64;  // float4 per lane and row
+constexpr int kMaxDv = CVS_CAGRA_MAX_DIM / 64;   // float4 per lane and row (fp32 traversal)
+constexpr int kMaxDv8 = CVS_CAGRA_MAX_DIM / 128; // 8-column pieces per lane and row (fp16 traversal)
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
 struct SearchArgs {
   const float4* rows;     // n rows of dq float4, zero-padded
+  const uint4* rows16;    // n rows of dq8 x 8 fp16 (traversal copy), zero-padded
   const uint32_t* graph;  // n x g
   const uint32_t* seeds;  // n_seeds seed ids, or null
   const float* queries;   // q x d fp32
@@ -64,6 +68,8 @@ struct SearchArgs {
   uint32_t n;
   int g;
   int dq;  // float4 per padded row (16 * dv)
+  int dq8; // 8-column pieces per padded row (16 * dv8)
+  int dv8; // 8-column pieces per lane and row
   int dv;  // float4 per lane and row
   int n_seeds;
   int seed_lanes;  // seed candidates in all: n_seeds, then hashed ids
@@ -127,7 +133,7 @@ __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
 // dependent gather rounds instead of 16.  W = 1 for large batches (no
 // barriers between waves are needed), W > 1 when few queries would leave most
 // of the GPU idle and the search is latency-bound.
-template <int E, int W>
+template <int E, int W, bool F16>
 __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   extern __shared__ uint32_t s_mem[];
   const int H = 1 << a.hash_bits;
@@ -153,21 +159,99 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
 
   for (int i = tid; i < H; i += kThreads) s_hash[i] = kInvalidId;
 
-  // Query slice of this lane: float4 columns tp + 16 j of the padded row.
-  float4 qv[kMaxDv];
+  // Query slice of this lane.  fp32 traversal: float4 columns tp + 16 j of
+  // the padded row.  fp16 traversal (and its fp32 re-rank): 8-column pieces
+  // tp + 16 j, so that a 16-lane team reads 256 contiguous bytes of an fp16
+  // row (512 of an fp32 row) per piece.
   const float* qsrc = a.queries + qi * a.d;
+  float4 qv[F16 ? 1 : kMaxDv];
+  float qh[F16 ? kMaxDv8 : 1][8];
+  if constexpr (!F16) {
 #pragma unroll
-  for (int j = 0; j < kMaxDv; ++j) {
-    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (j < a.dv) {
-      const int64_t c = int64_t(tp + 16 * j) * 4;
-      if (c + 0 < a.d) t.x = qsrc[c + 0];
-      if (c + 1 < a.d) t.y = qsrc[c + 1];
-      if (c + 2 < a.d) t.z = qsrc[c + 2];
-      if (c + 3 < a.d) t.w = qsrc[c + 3];
+    for (int j = 0; j < kMaxDv; ++j) {
+      float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j < a.dv) {
+        const int64_t c = int64_t(tp + 16 * j) * 4;
+        if (c + 0 < a.d) t.x = qsrc[c + 0];
+        if (c + 1 < a.d) t.y = qsrc[c + 1];
+        if (c + 2 < a.d) t.z = qsrc[c + 2];
+        if (c + 3 < a.d) t.w = qsrc[c + 3];
+      }
+      qv[j] = t;
     }
-    qv[j] = t;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kMaxDv8; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int64_t c = int64_t(tp + 16 * j) * 8 + t;
+        qh[j][t] = (j < a.dv8 && c < a.d) ? qsrc[c] : 0.f;
+      }
   }
+
+  // Squared distance of row rid to the query, summed over the 16 lanes of
+  // this lane's team: from the traversal copy, or (exact) from the fp32 rows.
+  auto team_dist = [&](uint32_t rid, bool exact) -> float {
+    float acc = 0.f;
+    if constexpr (!F16) {
+      const float4* row = a.rows + int64_t(rid) * a.dq + tp;
+      float4 x[kMaxDv];
+#pragma unroll
+      for (int j = 0; j < kMaxDv; ++j)
+        if (j < a.dv) x[j] = row[16 * j];
+#pragma unroll
+      for (int j = 0; j < kMaxDv; ++j) {
+        if (j < a.dv) {
+          const float dx = qv[j].x - x[j].x, dy = qv[j].y - x[j].y;
+          const float dz = qv[j].z - x[j].z, dw = qv[j].w - x[j].w;
+          acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        }
+      }
+    } else if (!exact) {
+      const uint4* row = a.rows16 + int64_t(rid) * a.dq8 + tp;
+      uint4 x[kMaxDv8];
+#pragma unroll
+      for (int j = 0; j < kMaxDv8; ++j)
+        if (j < a.dv8) x[j] = row[16 * j];
+#pragma unroll
+      for (int j = 0; j < kMaxDv8; ++j) {
+        if (j < a.dv8) {
+          const half8_t h = __builtin_bit_cast(half8_t, x[j]);
+          float p[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const float dt = qh[j][t] - float(h[t]);
+            p[t] = dt * dt;
+          }
+          acc += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        }
+      }
+    } else {
+      const float4* row = a.rows + int64_t(rid) * a.dq + 2 * tp;
+      float4 x[2 * kMaxDv8];
+#pragma unroll
+      for (int j = 0; j < kMaxDv8; ++j) {
+        if (j < a.dv8) {
+          x[2 * j] = row[32 * j];
+          x[2 * j + 1] = row[32 * j + 1];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxDv8; ++j) {
+        if (j < a.dv8) {
+          const float4 lo = x[2 * j], hi = x[2 * j + 1];
+          const float d0 = qh[j][0] - lo.x, d1 = qh[j][1] - lo.y, d2 = qh[j][2] - lo.z, d3 = qh[j][3] - lo.w;
+          const float d4 = qh[j][4] - hi.x, d5 = qh[j][5] - hi.y, d6 = qh[j][6] - hi.z, d7 = qh[j][7] - hi.w;
+          acc += ((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3)) + ((d4 * d4 + d5 * d5) + (d6 * d6 + d7 * d7));
+        }
+      }
+    }
+    acc += xor_lanes_f(acc, 8);
+    acc += xor_lanes_f(acc, 4);
+    acc += xor_lanes_f(acc, 2);
+    acc += xor_lanes_f(acc, 1);
+    return acc;
+  };
 
   uint64_t top[E];  // the list (lead wave)
 #pragma unroll
@@ -224,25 +308,7 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
     for (int r0 = 0; r0 < nf; r0 += kTeams) {
       const int r = r0 + team;
       const bool ok = r < nf;
-      const uint32_t rid = s_ids[ok ? r : 0];
-      const float4* row = a.rows + int64_t(rid) * a.dq + tp;
-      float4 x[kMaxDv];
-#pragma unroll
-      for (int j = 0; j < kMaxDv; ++j)
-        if (j < a.dv) x[j] = row[16 * j];
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < kMaxDv; ++j) {
-        if (j < a.dv) {
-          const float dx = qv[j].x - x[j].x, dy = qv[j].y - x[j].y;
-          const float dz = qv[j].z - x[j].z, dw = qv[j].w - x[j].w;
-          acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
-        }
-      }
-      acc += xor_lanes_f(acc, 8);
-      acc += xor_lanes_f(acc, 4);
-      acc += xor_lanes_f(acc, 2);
-      acc += xor_lanes_f(acc, 1);
+      const float acc = team_dist(s_ids[ok ? r : 0], false);
       if (ok && tp == 0) s_dist[r] = acc;
     }
     __syncthreads();
@@ -318,6 +384,24 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
     }
   }
 
+  // fp16 traversal: the list's distances are recomputed exactly from the
+  // fp32 rows (all teams, 64 entries per round) and the list re-sorted, so
+  // the output is the exact top-k of the visited rows in the list.
+  if constexpr (F16) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (lead) s_ids[lane] = top[e] != kEmptyKey ? uint32_t(top[e]) >> 1 : 0u;
+      __syncthreads();
+      for (int r0 = 0; r0 < 64; r0 += kTeams) {
+        const float acc = team_dist(s_ids[r0 + team], true);
+        if (tp == 0) s_dist[r0 + team] = acc;
+      }
+      __syncthreads();
+      if (lead && top[e] != kEmptyKey) top[e] = (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1);
+    }
+    if (lead) wave_sort_e<E>(top);
+  }
+
   if (lead) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -348,14 +432,40 @@ int waves_per_query(int64_t q) {
   return w;
 }
 
-template <int E>
+template <int E, bool F16>
 void launch_search(int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a) {
   switch (waves) {
-    case 1: hipLaunchKernelGGL((cagra_search_kernel<E, 1>), grid, dim3(64), lds, stream, a); break;
-    case 2: hipLaunchKernelGGL((cagra_search_kernel<E, 2>), grid, dim3(128), lds, stream, a); break;
-    case 4: hipLaunchKernelGGL((cagra_search_kernel<E, 4>), grid, dim3(256), lds, stream, a); break;
-    default: hipLaunchKernelGGL((cagra_search_kernel<E, 8>), grid, dim3(512), lds, stream, a); break;
+    case 1: hipLaunchKernelGGL((cagra_search_kernel<E, 1, F16>), grid, dim3(64), lds, stream, a); break;
+    case 2: hipLaunchKernelGGL((cagra_search_kernel<E, 2, F16>), grid, dim3(128), lds, stream, a); break;
+    case 4: hipLaunchKernelGGL((cagra_search_kernel<E, 4, F16>), grid, dim3(256), lds, stream, a); break;
+    default: hipLaunchKernelGGL((cagra_search_kernel<E, 8, F16>), grid, dim3(512), lds, stream, a); break;
   }
+}
+
+template <int E>
+void launch_search(bool f16, int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a) {
+  if (f16)
+    launch_search<E, true>(waves, grid, lds, stream, a);
+  else
+    launch_search<E, false>(waves, grid, lds, stream, a);
+}
+
+// fp32 rows -> the fp16 traversal copy (round to nearest even), 8 values per
+// thread.
+__global__ void rows_to_half_kernel(const float4* __restrict__ src, size_t pieces, uint4* __restrict__ dst) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= pieces) return;
+  const float4 lo = src[2 * i], hi = src[2 * i + 1];
+  half8_t h;
+  h[0] = _Float16(lo.x);
+  h[1] = _Float16(lo.y);
+  h[2] = _Float16(lo.z);
+  h[3] = _Float16(lo.w);
+  h[4] = _Float16(hi.x);
+  h[5] = _Float16(hi.y);
+  h[6] = _Float16(hi.z);
+  h[7] = _Float16(hi.w);
+  dst[i] = __builtin_bit_cast(uint4, h);
 }
 
 int ceil_log2(int64_t v) {
@@ -396,8 +506,11 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.d = idx->d;
   a.n = uint32_t(idx->n);
   a.g = int(idx->degree);
+  a.rows16 = reinterpret_cast<const uint4*>(idx->rows16);
   a.dq = int(idx->dpad / 4);
   a.dv = int(idx->dpad / 64);
+  a.dq8 = int(idx->dpad / 8);
+  a.dv8 = int(idx->dpad / 128);
   a.n_seeds = int(idx->n_seeds);
   // At least itopk candidates (all seed nodes, then hashed ids), in whole
   // chunks of 64: a list of itopk entries starts from as many distinct rows.
@@ -411,11 +524,12 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   hipEvent_t t0 = timer_begin(ctx, "cagra_search");
   const dim3 grid(static_cast<unsigned>(q));
   const int waves = waves_per_query(q);
+  const bool f16 = idx->traversal_bits == 16;
   switch (e_slots) {
-    case 1: launch_search<1>(waves, grid, lds, ctx->stream, a); break;
-    case 2: launch_search<2>(waves, grid, lds, ctx->stream, a); break;
-    case 4: launch_search<4>(waves, grid, lds, ctx->stream, a); break;
-    default: launch_search<8>(waves, grid, lds, ctx->stream, a); break;
+    case 1: launch_search<1>(f16, waves, grid, lds, ctx->stream, a); break;
+    case 2: launch_search<2>(f16, waves, grid, lds, ctx->stream, a); break;
+    case 4: launch_search<4>(f16, waves, grid, lds, ctx->stream, a); break;
+    default: launch_search<8>(f16, waves, grid, lds, ctx->stream, a); break;
   }
   after_launch("cagra_search_kernel");
   timer_end(ctx, "cagra_search", t0);
@@ -448,7 +562,7 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
     ix->ctx = ctx;
     ix->n = n;
     ix->d = d;
-    ix->dpad = (d + 63) / 64 * 64;
+    ix->dpad = (d + 127) / 128 * 128;
     ix->degree = degree;
     ix->n_seeds = n_seeds;
     try {
@@ -460,6 +574,11 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
       CVS_HIP(hipMemcpy2DAsync(ix->rows, size_t(ix->dpad) * sizeof(float), rows, size_t(d) * sizeof(float),
                                size_t(d) * sizeof(float), size_t(n),
                                rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream));
+      CVS_HIP(hipMalloc(&ix->rows16, size_t(n) * size_t(ix->dpad) * 2));
+      hipLaunchKernelGGL(rows_to_half_kernel, dim3(unsigned((size_t(n) * size_t(ix->dpad) / 8 + 255) / 256)), dim3(256),
+                         0, ctx->stream, reinterpret_cast<const float4*>(ix->rows), size_t(n) * size_t(ix->dpad) / 8,
+                         reinterpret_cast<uint4*>(ix->rows16));
+      after_launch("rows_to_half_kernel");
       CVS_HIP(hipMemcpyAsync(ix->graph, graph, size_t(n) * degree * sizeof(uint32_t),
                              graph_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream));
       if (n_seeds)
@@ -468,6 +587,7 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
       CVS_HIP(hipStreamSynchronize(ctx->stream));
     } catch (...) {
       if (ix->rows) (void)hipFree(ix->rows);
+      if (ix->rows16) (void)hipFree(ix->rows16);
       if (ix->graph) (void)hipFree(ix->graph);
       if (ix->seeds) (void)hipFree(ix->seeds);
       delete ix;
@@ -483,9 +603,18 @@ int cvs_cagra_index_destroy(cvs_cagra_index* index) {
     bind(index->ctx);
     (void)hipStreamSynchronize(index->ctx->stream);
     (void)hipFree(index->rows);
+    (void)hipFree(index->rows16);
     (void)hipFree(index->graph);
     if (index->seeds) (void)hipFree(index->seeds);
     delete index;
+  });
+}
+
+int cvs_cagra_index_set_traversal(cvs_cagra_index* index, int bits) {
+  return guarded([&] {
+    if (!index) fail(CVS_ERR_INVALID_ARGUMENT, "null index");
+    if (bits != 16 && bits != 32) fail(CVS_ERR_INVALID_ARGUMENT, "traversal precision must be 16 or 32 bits");
+    index->traversal_bits = bits;
   });
 }
 

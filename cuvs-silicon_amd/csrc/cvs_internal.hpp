@@ -102,10 +102,12 @@ struct cvs_cagra_index {
   cvs_context* ctx = nullptr;
   int64_t n = 0;
   int64_t d = 0;
-  int64_t dpad = 0;        // row stride in floats (d rounded up to 64)
+  int64_t dpad = 0;        // row stride in elements (d rounded up to 128)
   uint32_t degree = 0;
   uint32_t n_seeds = 0;
+  int traversal_bits = 16;   // 16: traverse rows16, re-rank the list from rows; 32: rows only
   float* rows = nullptr;     // n x dpad fp32, zero-padded
+  void* rows16 = nullptr;    // n x dpad fp16 copy of rows, zero-padded
   uint32_t* graph = nullptr; // n x degree
   uint32_t* seeds = nullptr; // n_seeds ids
 };

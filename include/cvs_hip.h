@@ -144,6 +144,15 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
                            cvs_cagra_index** out_index);
 int cvs_cagra_index_destroy(cvs_cagra_index* index);
 
+/* Precision of the graph traversal: 16 (the default) evaluates candidates on
+ * an fp16 copy of the rows made at index creation, then recomputes the
+ * distances of the final itopk list from the fp32 rows and re-sorts it, so
+ * that output distances are exact fp32; 32 evaluates every candidate on the
+ * fp32 rows, as the reference's beam search does
+ * (shaders/cagra_kernels.metal:117-132).  No counterpart in the reference:
+ * the fp16 copy halves the bytes each distance evaluation reads. */
+int cvs_cagra_index_set_traversal(cvs_cagra_index* index, int bits);
+
 /* Approximate k-NN by graph search.  Replaces MetalContext::search_cagra
  * (metal_context.hpp:57-73; src/metal_context.mm:918-1111) and the host
  * entry-point selection (src/cagra.cpp:128-178).  Parameters keep the

@@ -87,14 +87,16 @@ def test_hashed_seeds_reach_a_component_without_seed_nodes(ctx):
     assert nbr[:, 0].tolist() == list(range(300, 305))
 
 
-@pytest.mark.parametrize("n,d,g,itopk,width", [
-    (3000, 64, 32, 64, 1),
-    (3000, 100, 16, 32, 1),     # d not a multiple of 64, itopk < 64
-    (2500, 1000, 32, 128, 4),
-    (4000, 128, 32, 256, 2),
-    (5000, 256, 32, 512, 1),    # the reference harness's itopk
+@pytest.mark.parametrize("n,d,g,itopk,width,bits", [
+    (3000, 64, 32, 64, 1, 16),
+    (3000, 64, 32, 64, 1, 32),
+    (3000, 100, 16, 32, 1, 16),     # d not a multiple of 64, itopk < 64
+    (2500, 1000, 32, 128, 4, 16),
+    (2500, 1000, 32, 128, 4, 32),
+    (4000, 128, 32, 256, 2, 16),
+    (5000, 256, 32, 512, 1, 16),    # the reference harness's itopk
 ])
-def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width):
+def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width, bits):
     rng = np.random.default_rng(n + d)
     centers = rng.standard_normal((16, d)).astype(np.float32)
     base = centers[rng.integers(0, 16, n)] + 0.5 * rng.standard_normal((n, d)).astype(np.float32)
@@ -104,7 +106,7 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width):
     k = 10
     gt, _ = oracle.bf_exact(base, qs, k, threads=16)
     ref_nbr, _ = oracle.cagra_reference_search(base, graph, nav, qs, k, itopk_size=itopk, threads=16)
-    idx = ctx.cagra_index(base, graph, nav)
+    idx = ctx.cagra_index(base, graph, nav, traversal_bits=bits)
     nbr, dist = idx.search(qs, k, itopk_size=itopk, search_width=width)
     check_invariants(base, qs, nbr, dist)
     r_gpu, r_ref = recall(nbr, gt, k), recall(ref_nbr, gt, k)
@@ -113,15 +115,20 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width):
     assert r_gpu > 0.8
 
 
-def test_itopk_512_on_complete_graph_is_exact(ctx, oracle):
+@pytest.mark.parametrize("bits", [32, 16])
+def test_itopk_512_on_complete_graph_is_exact(ctx, oracle, bits):
     """itopk 512 (8 list slots per lane) and k up to 512: on a complete graph
-    the first expansion reaches every row, so the result is the exact top-k."""
+    the first expansion reaches every row, so the result is the exact top-k.
+    With fp16 traversal the list holds the itopk best by fp16 distance and is
+    re-ranked in fp32, so the exact top-k comes out when k leaves a margin
+    below itopk (rows near rank itopk may swap across it)."""
     rng = np.random.default_rng(512)
     n, d = 600, 16
     base = rng.standard_normal((n, d)).astype(np.float32)
     qs = rng.standard_normal((5, d)).astype(np.float32)
-    idx = ctx.cagra_index(base, complete_graph(n), oracle.cagra_nav_nodes(n))
-    for k, itopk in [(500, 512), (512, 0), (300, 400)]:
+    idx = ctx.cagra_index(base, complete_graph(n), oracle.cagra_nav_nodes(n), traversal_bits=bits)
+    cases = [(500, 512), (512, 0), (300, 400)] if bits == 32 else [(300, 512), (100, 400), (10, 64)]
+    for k, itopk in cases:
         nbr, dist = idx.search(qs, k, itopk_size=itopk)
         ref_nbr, ref_dist = oracle.bf_exact(base, qs, k)
         check_invariants(base, qs, nbr, dist)
@@ -185,6 +192,8 @@ def test_argument_errors(ctx, oracle):
         ctx.cagra_index(np.ones((10, 1025), np.float32), g)
     with pytest.raises(ValueError):
         ctx.cagra_index(base, g, np.array([10], np.uint32))
+    with pytest.raises(ValueError):
+        idx.set_traversal(8)
 
 
 @pytest.mark.parametrize("n,d,q", [(60_000, 128, 500), (100_000, 1024, 1000)])
@@ -195,7 +204,7 @@ def test_recall_on_reference_built_graph(ctx, cvs, oracle, n, d, q):
     benchmark distribution (64 centres, sigma 0.3, L2-normalised), degree
     64, itopk 64.  GPU search recall@10 (search_width 1 and 4) must be at
     least the restated reference search's; the second case is the full
-    N=100,000 D=1024 configuration."""
+    N=100,000 D=1024 configuration.  Both traversal precisions."""
     base = cvs.synth_clustered(12345, cvs.STREAM_BASE, n, d)
     qs = cvs.synth_clustered(12345, cvs.STREAM_QUERIES, q, d)
     graph = oracle.cagra_build_reference(base, 64, threads=16)
@@ -204,10 +213,12 @@ def test_recall_on_reference_built_graph(ctx, cvs, oracle, n, d, q):
     ref, _ = oracle.cagra_reference_search(base, graph, nav, qs, 10, itopk_size=64, threads=16)
     r_ref = recall(ref, gt, 10)
     idx = ctx.cagra_index(base, graph, nav)
-    for width in (1, 4):
-        nbr, dist = idx.search(qs, 10, itopk_size=64, search_width=width)
-        check_invariants(base, qs, nbr, dist)
-        r_gpu = recall(nbr, gt, 10)
-        print(f"N={n} D={d} reference-built graph, width {width}: recall@10 gpu {r_gpu:.4f} "
-              f"restated reference {r_ref:.4f}")
-        assert r_gpu >= r_ref - 0.01
+    for bits in (16, 32):
+        idx.set_traversal(bits)
+        for width in (1, 4):
+            nbr, dist = idx.search(qs, 10, itopk_size=64, search_width=width)
+            check_invariants(base, qs, nbr, dist)
+            r_gpu = recall(nbr, gt, 10)
+            print(f"N={n} D={d} reference-built graph, {bits}-bit traversal, width {width}: recall@10 gpu "
+                  f"{r_gpu:.4f} restated reference {r_ref:.4f}")
+            assert r_gpu >= r_ref - 0.01
