@@ -61,6 +61,7 @@ _SIGNATURES = {
                                        c_void_p, c_uint32, POINTER(c_void_p)]),
     "cvs_cagra_index_destroy": (c_int, [c_void_p]),
     "cvs_cagra_index_set_traversal": (c_int, [c_void_p, c_int]),
+    "cvs_cagra_index_edge_distances": (c_int, [c_void_p, c_void_p, c_void_p, c_int]),
     "cvs_cagra_search": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
                                  c_void_p, c_void_p]),
     "cvs_cagra_search_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
@@ -338,6 +339,20 @@ class CagraIndex:
         self.handle = h
         self.n, self.d, self.degree = int(n), int(d), int(degree)
         self.set_traversal(traversal_bits)
+
+    def edge_distances(self, out: "DeviceArray" = None):
+        """Exact squared L2 length of every graph edge, (n, degree) float32
+        (+inf where the entry is not a row id); into `out` (a device array)
+        when given, else returned as a host array."""
+        if out is not None:
+            if out.shape != (self.n, self.degree) or out.dtype != np.float32:
+                raise ValueError(f"out must be a float32 device array of shape {(self.n, self.degree)}")
+            _check(load().cvs_cagra_index_edge_distances(self.ctx.handle, self.handle, out.ptr, 1))
+            return out
+        host = np.empty((self.n, self.degree), np.float32)
+        _check(load().cvs_cagra_index_edge_distances(self.ctx.handle, self.handle,
+                                                     host.ctypes.data_as(c_void_p), 0))
+        return host
 
     def set_traversal(self, bits: int) -> None:
         """16: candidates evaluated on the fp16 copy, final list re-ranked in

@@ -468,6 +468,47 @@ __global__ void rows_to_half_kernel(const float4* __restrict__ src, size_t piece
   dst[i] = __builtin_bit_cast(uint4, h);
 }
 
+// Exact squared L2 length of every graph edge (the reference's
+// recompute_graph_distances, shaders/cagra_kernels.metal:658-681).  One
+// workgroup per node: the node's row stays in registers (float4 columns
+// tp + 16 j per lane of each 16-lane team) and the 16 teams gather the
+// neighbour rows, 256 contiguous bytes per load instruction and team.
+// Entries that are not row ids (UINT32_MAX, or >= n) get +inf.
+__global__ __launch_bounds__(256) void edge_distances_kernel(const float4* __restrict__ rows, int dq, int dv,
+                                                             const uint32_t* __restrict__ graph, int g, uint32_t n,
+                                                             float* __restrict__ out) {
+  const int64_t node = blockIdx.x;
+  const int tid = threadIdx.x, team = tid >> 4, tp = tid & 15;
+  float4 xv[kMaxDv];
+  const float4* self = rows + node * dq + tp;
+#pragma unroll
+  for (int j = 0; j < kMaxDv; ++j)
+    if (j < dv) xv[j] = self[16 * j];
+  for (int e = team; e < g; e += 16) {
+    const uint32_t nb = graph[node * g + e];
+    const bool valid = nb < n;
+    const float4* row = rows + int64_t(valid ? nb : uint32_t(node)) * dq + tp;
+    float4 x[kMaxDv];
+#pragma unroll
+    for (int j = 0; j < kMaxDv; ++j)
+      if (j < dv) x[j] = row[16 * j];
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxDv; ++j) {
+      if (j < dv) {
+        const float dx = xv[j].x - x[j].x, dy = xv[j].y - x[j].y;
+        const float dz = xv[j].z - x[j].z, dw = xv[j].w - x[j].w;
+        acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+    }
+    acc += xor_lanes_f(acc, 8);
+    acc += xor_lanes_f(acc, 4);
+    acc += xor_lanes_f(acc, 2);
+    acc += xor_lanes_f(acc, 1);
+    if (tp == 0) out[node * g + e] = valid ? acc : INFINITY;
+  }
+}
+
 int ceil_log2(int64_t v) {
   int b = 0;
   while ((int64_t(1) << b) < v) ++b;
@@ -607,6 +648,31 @@ int cvs_cagra_index_destroy(cvs_cagra_index* index) {
     (void)hipFree(index->graph);
     if (index->seeds) (void)hipFree(index->seeds);
     delete index;
+  });
+}
+
+int cvs_cagra_index_edge_distances(cvs_context* ctx, const cvs_cagra_index* index, float* out_distances,
+                                   int out_on_device) {
+  return guarded([&] {
+    bind(ctx);
+    if (!index || index->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
+    if (!out_distances) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
+    const size_t count = size_t(index->n) * index->degree;
+    float* dst = out_distances;
+    if (!out_on_device) {
+      ctx->ws_io.reserve(count * sizeof(float));
+      dst = ctx->ws_io.as<float>();
+    }
+    hipEvent_t t0 = timer_begin(ctx, "cagra_edge_distances");
+    hipLaunchKernelGGL(edge_distances_kernel, dim3(unsigned(index->n)), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<const float4*>(index->rows), int(index->dpad / 4), int(index->dpad / 64),
+                       static_cast<const uint32_t*>(index->graph), int(index->degree), uint32_t(index->n), dst);
+    after_launch("edge_distances_kernel");
+    timer_end(ctx, "cagra_edge_distances", t0);
+    if (!out_on_device) {
+      CVS_HIP(hipMemcpyAsync(out_distances, dst, count * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+      CVS_HIP(hipStreamSynchronize(ctx->stream));
+    }
   });
 }
 

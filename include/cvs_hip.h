@@ -153,6 +153,15 @@ int cvs_cagra_index_destroy(cvs_cagra_index* index);
  * the fp16 copy halves the bytes each distance evaluation reads. */
 int cvs_cagra_index_set_traversal(cvs_cagra_index* index, int bits);
 
+/* Exact squared L2 length of every edge of the index's graph: out[i*degree
+ * + j] = |row i - row graph[i][j]|^2 in fp32, +inf where the entry is not a
+ * row id (UINT32_MAX, or >= n).  Replaces the reference's
+ * recompute_graph_distances pass (shaders/cagra_kernels.metal:658-681, host
+ * src/metal_context.mm:683-709).  out_on_device = 0: n x degree host floats,
+ * blocking; 1: a device buffer, enqueued on the context stream. */
+int cvs_cagra_index_edge_distances(cvs_context* ctx, const cvs_cagra_index* index, float* out_distances,
+                                   int out_on_device);
+
 /* Approximate k-NN by graph search.  Replaces MetalContext::search_cagra
  * (metal_context.hpp:57-73; src/metal_context.mm:918-1111) and the host
  * entry-point selection (src/cagra.cpp:128-178).  Parameters keep the

@@ -60,6 +60,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_cagra_build_ref.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
         L.oracle_knn_graph.restype = None
         L.oracle_knn_graph.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
+        L.oracle_edge_distances.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int]
         _lib = L
     return _lib
 
@@ -191,6 +192,18 @@ def cagra_reference_search(base, graph, nav_ids, queries, k: int, itopk_size: in
     entry = cagra_entry_points(queries, nav_ids, base[nav_ids]) if len(nav_ids) else None
     beam, iters = cagra_search_policy(itopk_size, max_iterations, len(queries))
     return cagra_search(base, graph, queries, k, beam, iters, entry, threads)
+
+
+def edge_distances(rows, graph, threads: int = 1) -> np.ndarray:
+    """The reference's recompute_graph_distances restated
+    (shaders/cagra_kernels.metal:658-681)."""
+    rows = np.ascontiguousarray(rows, np.float32)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    n, d = rows.shape
+    g = graph.shape[1]
+    out = np.empty((n, g), np.float32)
+    lib().oracle_edge_distances(_p(rows), n, d, _p(graph), int(g), _p(out), int(threads))
+    return out
 
 
 def knn_graph(base, g: int, threads: int = 1) -> np.ndarray:

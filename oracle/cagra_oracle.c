@@ -232,3 +232,35 @@ void oracle_knn_graph(const float* base, int64_t n, int64_t d, uint32_t g, uint3
     free(bi);
   }
 }
+
+/* recompute_graph_distances (reference shaders/cagra_kernels.metal:658-681):
+ * per edge, the squared L2 distance of the node's row to its neighbour's,
+ * accumulated over float4 groups (dist += dot(delta, delta), the four
+ * products summed left to right) over the first 4*floor(d/4) columns only, as
+ * the reference's D >> 2 loop does; UINT32_MAX entries get +inf.  Ids >= n
+ * (out of range for the reference, which would read past the dataset) also
+ * get +inf here. */
+void oracle_edge_distances(const float* rows, int64_t n, int64_t d, const uint32_t* graph, uint32_t g,
+                           float* out, int threads) {
+  const int64_t d4 = d / 4;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (int64_t i = 0; i < n; ++i) {
+    const float* a = rows + i * d;
+    for (uint32_t e = 0; e < g; ++e) {
+      const uint32_t nb = graph[i * (int64_t)g + e];
+      if (nb == INVALID_ID || (int64_t)nb >= n) {
+        out[i * (int64_t)g + e] = INFINITY;
+        continue;
+      }
+      const float* b = rows + (int64_t)nb * d;
+      float dist = 0.f;
+      for (int64_t c = 0; c < d4; ++c) {
+        const float dx = a[4 * c] - b[4 * c], dy = a[4 * c + 1] - b[4 * c + 1];
+        const float dz = a[4 * c + 2] - b[4 * c + 2], dw = a[4 * c + 3] - b[4 * c + 3];
+        const float dot = ((dx * dx + dy * dy) + dz * dz) + dw * dw;
+        dist += dot;
+      }
+      out[i * (int64_t)g + e] = dist;
+    }
+  }
+}

@@ -39,6 +39,14 @@ void oracle_bf_fp64(const float* base, int64_t n, int64_t d, const float* querie
 
 /* ---- CAGRA search (oracle/cagra_oracle.c) ------------------------------- */
 
+/* recompute_graph_distances (reference shaders/cagra_kernels.metal:658-681):
+ * squared L2 length of every graph edge over float4 groups of the first
+ * 4*floor(d/4) columns; +inf for UINT32_MAX (and, here, ids >= n).  Pinned:
+ * numpy fp64 on random graphs (multiple-of-4 d), the truncation to 4*floor(d/4)
+ * columns on a d = 6 case, and the +inf entries. */
+void oracle_edge_distances(const float* rows, int64_t n, int64_t d, const uint32_t* graph, uint32_t g,
+                           float* out, int threads);
+
 /* Navigation nodes of a built index (src/cagra.cpp:65-72): returns
  * n_nav = min(200, floor(sqrt(n))) and, if out_ids is non-null, writes
  * out_ids[i] = (uint32)(i * (n / n_nav)).  Pinned: closed form at n = 1, 10,

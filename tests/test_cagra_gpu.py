@@ -222,3 +222,28 @@ def test_recall_on_reference_built_graph(ctx, cvs, oracle, n, d, q):
             print(f"N={n} D={d} reference-built graph, {bits}-bit traversal, width {width}: recall@10 gpu "
                   f"{r_gpu:.4f} restated reference {r_ref:.4f}")
             assert r_gpu >= r_ref - 0.01
+
+
+@pytest.mark.parametrize("n,d,g", [(2000, 128, 32), (1500, 100, 16), (700, 1024, 64)])
+def test_edge_distances_match_oracle(ctx, cvs, oracle, n, d, g):
+    """cvs_cagra_index_edge_distances against the restated
+    recompute_graph_distances (1e-5 relative; the oracle sums float4 groups in
+    sequence, the kernel in a tree) and numpy fp64, with +inf entries; host
+    and device output."""
+    rng = np.random.default_rng(n + g)
+    base = rng.standard_normal((n, d)).astype(np.float32)
+    graph = rng.integers(0, n, (n, g)).astype(np.uint32)
+    graph[1, :3] = INV
+    graph[n - 1, g - 1] = n + 3
+    idx = ctx.cagra_index(base, graph)
+    got = idx.edge_distances()
+    ok = graph < n
+    if d % 4 == 0:
+        np.testing.assert_allclose(got[ok], oracle.edge_distances(base, graph, threads=8)[ok], rtol=1e-5, atol=1e-5)
+    exact = ((base.astype(np.float64)[:, None, :] - base.astype(np.float64)[np.where(ok, graph, 0)]) ** 2).sum(-1)
+    np.testing.assert_allclose(got[ok], exact[ok], rtol=1e-5, atol=1e-5)
+    assert np.isinf(got[~ok]).all()
+    dev = cvs.DeviceArray(ctx, (n, g), np.float32)
+    idx.edge_distances(out=dev)
+    ctx.synchronize()
+    np.testing.assert_array_equal(dev.to_host(), got)

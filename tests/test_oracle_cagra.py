@@ -210,3 +210,25 @@ def test_knn_graph_matches_brute_force(oracle):
         assert g[i].tolist() == expect
     tiny = oracle.knn_graph(FAISS_DB, 5)
     assert (tiny[:, 3:] == INV).all() and (tiny[:, :3] != INV).all()
+
+
+def test_edge_distances_pinned(oracle):
+    """recompute_graph_distances restated: numpy fp64 distances on a random
+    graph with d a multiple of 4; the reference's D >> 2 loop reads only the
+    first 4*floor(d/4) columns (d = 6: columns 4 and 5 are ignored); +inf for
+    UINT32_MAX and out-of-range ids."""
+    rng = np.random.default_rng(658)
+    n, d, g = 300, 64, 12
+    rows = rng.standard_normal((n, d)).astype(np.float32)
+    graph = rng.integers(0, n, (n, g)).astype(np.uint32)
+    graph[3, 5] = 0xFFFFFFFF
+    graph[7, 0] = n + 5
+    got = oracle.edge_distances(rows, graph, threads=4)
+    ok = graph < n
+    ref = ((rows.astype(np.float64)[:, None, :] - rows.astype(np.float64)[np.where(ok, graph, 0)]) ** 2).sum(-1)
+    np.testing.assert_allclose(got[ok], ref[ok], rtol=2e-6, atol=1e-6)
+    assert np.isinf(got[~ok]).all() and (~ok).sum() == 2
+    # d = 6: the last two columns do not count
+    small = np.array([[0, 0, 0, 0, 5, 5], [1, 2, 2, 0, -7, 9]], np.float32)
+    out = oracle.edge_distances(small, np.array([[1], [0]], np.uint32))
+    assert out.tolist() == [[9.0], [9.0]]
