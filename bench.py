@@ -436,6 +436,29 @@ def run_cagra_search(args) -> int:
         }
         log(json.dumps(res))
         results.append(res)
+    # Q=1 latency of multi-team search (teams x per-team list, fp16 traversal)
+    idx.set_traversal(16)
+    teams_lat = []
+    for teams, per_team in ((8, 32), (16, 32), (8, 64)):
+        lat, hits = [], 0
+        for i, dq1 in enumerate(single):
+            ctx.synchronize()
+            t1 = time.perf_counter()
+            idx.search_teams_async(dq1, k, dn1, dd1, teams, itopk_size=per_team)
+            ctx.synchronize()
+            lat.append(time.perf_counter() - t1)
+            hits += len(set(dn1.to_host()[0].tolist()) & set(gt[i].tolist()))
+        ctx.set_timing(True)
+        for dq1 in single:
+            idx.search_teams_async(dq1, k, dn1, dd1, teams, itopk_size=per_team)
+        ctx.synchronize()
+        tms, tn = ctx.kernel_time("cagra_search")
+        ctx.set_timing(False)
+        lat.sort()
+        teams_lat.append({"teams": teams, "itopk_per_team": per_team, "q1_latency_ms_p50": 1e3 * lat[50],
+                          "q1_latency_ms_p99": 1e3 * lat[98], "q1_kernel_ms": tms / max(tn, 1),
+                          "q1_recall_at_10": hits / 1000})
+        log(json.dumps(teams_lat[-1]))
     # restated reference search on the same graph, all host cores, sampled queries
     sample = min(q, args.cpu_sample * 50)
     threads = os.cpu_count() or 1
@@ -452,6 +475,7 @@ def run_cagra_search(args) -> int:
         "config": {"workload": f"CAGRA graph search, N={n} D={d} Q={q} K={k} itopk={args.itopk} "
                                f"degree={args.degree}, graph built on the GPU", "seed": args.seed},
         "widths": results,
+        "q1_teams": teams_lat,
         "build": bst,
         "reference_search_same_graph": {"recall_at_10": ref_recall, "queries": sample,
                                         "gpu_recall_at_10_same_queries": gpu_recall_sample},

@@ -62,6 +62,10 @@ _SIGNATURES = {
     "cvs_cagra_index_destroy": (c_int, [c_void_p]),
     "cvs_cagra_index_set_traversal": (c_int, [c_void_p, c_int]),
     "cvs_cagra_index_edge_distances": (c_int, [c_void_p, c_void_p, c_void_p, c_int]),
+    "cvs_cagra_search_teams": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
+                                       c_uint32, c_void_p, c_void_p]),
+    "cvs_cagra_search_teams_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32,
+                                             c_uint32, c_uint32, c_void_p, c_void_p]),
     "cvs_cagra_search": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
                                  c_void_p, c_void_p]),
     "cvs_cagra_search_async": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
@@ -383,6 +387,27 @@ class CagraIndex:
                                        int(itopk_size), int(search_width), int(max_iterations),
                                        nbr.ctypes.data_as(c_void_p), dist.ctypes.data_as(c_void_p)))
         return nbr, dist
+
+    def search_teams(self, queries, k: int, teams: int, itopk_size: int = 32, search_width: int = 1,
+                     max_iterations: int = 0):
+        """Multi-team graph search of host queries (C: cvs_cagra_search_teams):
+        `teams` searches per query with `itopk_size`-entry lists, merged."""
+        queries = _f32(queries)
+        if queries.ndim != 2 or queries.shape[1] != self.d:
+            raise ValueError("queries must be (q, d)")
+        q = queries.shape[0]
+        nbr = np.empty((q, k), dtype=np.uint32)
+        dist = np.empty((q, k), dtype=np.float32)
+        _check(load().cvs_cagra_search_teams(self.ctx.handle, self.handle, queries.ctypes.data_as(c_void_p), q, int(k),
+                                             int(itopk_size), int(search_width), int(max_iterations), int(teams),
+                                             nbr.ctypes.data_as(c_void_p), dist.ctypes.data_as(c_void_p)))
+        return nbr, dist
+
+    def search_teams_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray, teams: int,
+                           itopk_size: int = 32, search_width: int = 1, max_iterations: int = 0) -> None:
+        _check(load().cvs_cagra_search_teams_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0], int(k),
+                                                   int(itopk_size), int(search_width), int(max_iterations),
+                                                   int(teams), nbr.ptr, dist.ptr))
 
     def search_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray, itopk_size: int = 64,
                      search_width: int = 1, max_iterations: int = 0, stats: DeviceArray | None = None) -> None:

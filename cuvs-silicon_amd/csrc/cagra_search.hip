@@ -78,6 +78,8 @@ struct SearchArgs {
   int width;
   int max_iter;
   int hash_bits;
+  int teams;            // workgroups per query (block b = query b / teams, team b % teams)
+  uint64_t* team_keys;  // teams > 1: (q * teams) x itopk list keys, merged afterwards
 };
 
 // Ascending bitonic sort of one 64-bit key per lane.
@@ -154,7 +156,8 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const bool lead = W == 1 || __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
-  const int64_t qi = blockIdx.x;
+  const int64_t qi = blockIdx.x / a.teams;
+  const int tm = int(blockIdx.x - qi * a.teams);
   const int team = tid >> 4, tp = lane & 15;
 
   for (int i = tid; i < H; i += kThreads) s_hash[i] = kInvalidId;
@@ -329,12 +332,15 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   // Seeds: seed_lanes candidates in chunks of 64, first the seed nodes, then
   // hashed ids led by the reference's fallback (q * 2654435761) mod n, so that
   // regions no seed node reaches (clusters the graph does not link) can still
-  // be entered.
+  // be entered.  With several teams per query, team t takes the candidates
+  // t, t + teams, t + 2 teams, ... of that sequence (the reference's teams
+  // start from entry points rotated by n / teams,
+  // shaders/cagra_kernels.metal:243-250).
   {
     const uint32_t h0 = uint32_t(qi) * 2654435761u;
     for (int c = 0; c < a.seed_lanes; c += 64) {
       if (count + 64 > hcap) reset_hash();
-      const int i = c + lane;
+      const int i = (c + lane) * a.teams + tm;
       uint32_t id = kInvalidId;
       if (lead) {
         if (i < a.n_seeds)
@@ -402,7 +408,13 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
     if (lead) wave_sort_e<E>(top);
   }
 
-  if (lead) {
+  if (lead && a.team_keys) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int pos = e * 64 + lane;
+      if (pos < a.itopk) a.team_keys[int64_t(blockIdx.x) * a.itopk + pos] = top[e];
+    }
+  } else if (lead) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int pos = e * 64 + lane;
@@ -448,6 +460,52 @@ void launch_search(bool f16, int waves, dim3 grid, size_t lds, hipStream_t strea
     launch_search<E, true>(waves, grid, lds, stream, a);
   else
     launch_search<E, false>(waves, grid, lds, stream, a);
+}
+
+// Merge of the teams' lists of one query (one wave per query): the teams x
+// itopk keys are sorted, an id found by several teams is kept once (every
+// team computes the same fp32 distance for it, so copies are adjacent once
+// the expanded bit is ignored), and the k smallest are written, padded with
+// UINT32_MAX / +inf.  The reference merges its teams' beams on the host with
+// the same dedupe (src/metal_context.mm:1003-1035).
+template <int E2>
+__global__ __launch_bounds__(64) void team_merge_kernel(const uint64_t* __restrict__ keys, int total, int k,
+                                                        uint32_t* __restrict__ out_nbr, float* __restrict__ out_dist) {
+  const int64_t qi = blockIdx.x;
+  const int lane = threadIdx.x;
+  uint64_t v[E2];
+#pragma unroll
+  for (int e = 0; e < E2; ++e) {
+    const int pos = e * 64 + lane;
+    v[e] = pos < total ? (keys[qi * total + pos] | 1ull) : kEmptyKey;
+  }
+  wave_sort_e<E2>(v);
+  int base = 0;
+  uint32_t carry_lo = 0, carry_hi = 0;  // key at the previous slot's lane 63
+#pragma unroll
+  for (int e = 0; e < E2; ++e) {
+    const uint32_t lo = uint32_t(v[e]), hi = uint32_t(v[e] >> 32);
+    uint32_t plo = uint32_t(__shfl_up(int(lo), 1)), phi = uint32_t(__shfl_up(int(hi), 1));
+    if (lane == 0) {
+      plo = carry_lo;
+      phi = carry_hi;
+    }
+    const uint64_t prev = (uint64_t(phi) << 32) | plo;
+    const bool uniq = v[e] != kEmptyKey && ((e == 0 && lane == 0) || v[e] != prev);
+    const uint64_t m = __ballot(uniq);
+    const int rank = base + mbcnt(m);
+    if (uniq && rank < k) {
+      out_nbr[qi * k + rank] = uint32_t(v[e]) >> 1;
+      out_dist[qi * k + rank] = unord_f32(uint32_t(v[e] >> 32));
+    }
+    base += popc(m);
+    carry_lo = uint32_t(__builtin_amdgcn_readlane(int(lo), 63));
+    carry_hi = uint32_t(__builtin_amdgcn_readlane(int(hi), 63));
+  }
+  for (int r = base + lane; r < k; r += 64) {
+    out_nbr[qi * k + r] = kInvalidId;
+    out_dist[qi * k + r] = INFINITY;
+  }
 }
 
 // fp32 rows -> the fp16 traversal copy (round to nearest even), 8 values per
@@ -517,7 +575,7 @@ int ceil_log2(int64_t v) {
 
 void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const float* queries,
                          int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
-                         uint32_t max_iterations, uint32_t* nbr, float* dist, uint32_t* stats) {
+                         uint32_t max_iterations, uint32_t* nbr, float* dist, uint32_t* stats, int teams = 1) {
   if (!idx || idx->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
   if (!queries || !nbr || !dist) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
   if (q <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count must be positive");
@@ -526,6 +584,10 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   const int64_t itopk = std::max<int64_t>(itopk_size ? itopk_size : 128, k);
   if (itopk > CVS_CAGRA_MAX_ITOPK)
     fail(CVS_ERR_UNSUPPORTED, "itopk_size (or k) exceeds CVS_CAGRA_MAX_ITOPK");
+  if (teams < 1 || teams > CVS_CAGRA_MAX_TEAMS) fail(CVS_ERR_INVALID_ARGUMENT, "teams must be in [1, CVS_CAGRA_MAX_TEAMS]");
+  if (teams > 1 && int64_t(teams) * itopk > CVS_CAGRA_MAX_ITOPK)
+    fail(CVS_ERR_UNSUPPORTED, "teams * itopk_size exceeds CVS_CAGRA_MAX_ITOPK");
+  if (q * teams > int64_t(INT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "too many queries in one call");
   const int64_t width = search_width ? search_width : 1;
   if (width > CVS_CAGRA_MAX_WIDTH) fail(CVS_ERR_UNSUPPORTED, "search_width exceeds CVS_CAGRA_MAX_WIDTH");
   const int64_t per_iter = width * int64_t(idx->degree);
@@ -553,18 +615,26 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.dq8 = int(idx->dpad / 8);
   a.dv8 = int(idx->dpad / 128);
   a.n_seeds = int(idx->n_seeds);
-  // At least itopk candidates (all seed nodes, then hashed ids), in whole
-  // chunks of 64: a list of itopk entries starts from as many distinct rows.
-  a.seed_lanes = int((std::max<int64_t>({int64_t(idx->n_seeds), itopk, 1}) + 63) / 64 * 64);
+  // At least itopk candidates (all seed nodes, then hashed ids; each team its
+  // share of the seed nodes), in whole chunks of 64: a list of itopk entries
+  // starts from as many distinct rows.
+  const int64_t team_seeds = (int64_t(idx->n_seeds) + teams - 1) / teams;
+  a.seed_lanes = int((std::max<int64_t>({team_seeds, itopk, 1}) + 63) / 64 * 64);
   a.k = int(k);
   a.itopk = int(itopk);
   a.width = int(width);
   a.max_iter = int(std::min<int64_t>(iters, INT32_MAX));
   a.hash_bits = hash_bits;
+  a.teams = teams;
+  if (teams > 1) {
+    ctx->ws_teams.reserve(size_t(q) * size_t(teams) * size_t(itopk) * sizeof(uint64_t));
+    a.team_keys = ctx->ws_teams.as<uint64_t>();
+    a.stats = nullptr;
+  }
 
   hipEvent_t t0 = timer_begin(ctx, "cagra_search");
-  const dim3 grid(static_cast<unsigned>(q));
-  const int waves = waves_per_query(q);
+  const dim3 grid(static_cast<unsigned>(q * teams));
+  const int waves = waves_per_query(q * teams);
   const bool f16 = idx->traversal_bits == 16;
   switch (e_slots) {
     case 1: launch_search<1>(f16, waves, grid, lds, ctx->stream, a); break;
@@ -573,6 +643,19 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
     default: launch_search<8>(f16, waves, grid, lds, ctx->stream, a); break;
   }
   after_launch("cagra_search_kernel");
+  if (teams > 1) {
+    const int total = int(teams * itopk);
+    const uint64_t* keys = a.team_keys;
+    if (total <= 64)
+      hipLaunchKernelGGL(team_merge_kernel<1>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+    else if (total <= 128)
+      hipLaunchKernelGGL(team_merge_kernel<2>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+    else if (total <= 256)
+      hipLaunchKernelGGL(team_merge_kernel<4>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+    else
+      hipLaunchKernelGGL(team_merge_kernel<8>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+    after_launch("team_merge_kernel");
+  }
   timer_end(ctx, "cagra_search", t0);
 }
 
@@ -692,6 +775,41 @@ int cvs_cagra_search_async(cvs_context* ctx, const cvs_cagra_index* index, const
     bind(ctx);
     cagra_search_device(ctx, index, queries_dev, q, k, itopk_size, search_width, max_iterations,
                         out_neighbors_dev, out_distances_dev, out_stats_dev);
+  });
+}
+
+int cvs_cagra_search_teams_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                                 int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                                 uint32_t max_iterations, uint32_t teams, uint32_t* out_neighbors_dev,
+                                 float* out_distances_dev) {
+  return guarded([&] {
+    bind(ctx);
+    cagra_search_device(ctx, index, queries_dev, q, k, itopk_size, search_width, max_iterations,
+                        out_neighbors_dev, out_distances_dev, nullptr, int(std::min<uint32_t>(teams, 1u << 20)));
+  });
+}
+
+int cvs_cagra_search_teams(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
+                           int64_t k, uint32_t itopk_size, uint32_t search_width, uint32_t max_iterations,
+                           uint32_t teams, uint32_t* out_neighbors, float* out_distances) {
+  return guarded([&] {
+    bind(ctx);
+    if (!index || !queries || !out_neighbors || !out_distances) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
+    if (index->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
+    if (q <= 0 || k <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count and k must be positive");
+    const size_t qbytes = size_t(q) * size_t(index->d) * sizeof(float);
+    const size_t obytes = size_t(q) * size_t(k) * sizeof(float);
+    ctx->ws_io.reserve(qbytes + 2 * obytes + 256);
+    char* base = ctx->ws_io.as<char>();
+    float* dq = reinterpret_cast<float*>(base);
+    uint32_t* dn = reinterpret_cast<uint32_t*>(base + (qbytes + 127) / 128 * 128);
+    float* dd = reinterpret_cast<float*>(reinterpret_cast<char*>(dn) + (obytes + 127) / 128 * 128);
+    CVS_HIP(hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, ctx->stream));
+    cagra_search_device(ctx, index, dq, q, k, itopk_size, search_width, max_iterations, dn, dd, nullptr,
+                        int(std::min<uint32_t>(teams, 1u << 20)));
+    CVS_HIP(hipMemcpyAsync(out_neighbors, dn, obytes, hipMemcpyDeviceToHost, ctx->stream));
+    CVS_HIP(hipMemcpyAsync(out_distances, dd, obytes, hipMemcpyDeviceToHost, ctx->stream));
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
   });
 }
 

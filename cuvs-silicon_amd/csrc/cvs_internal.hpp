@@ -85,6 +85,7 @@ struct cvs_context {
   cvs::DeviceBuffer ws_queries;   // fp16 query tiles + query norms
   cvs::DeviceBuffer ws_partial;   // per-workgroup candidate lists
   cvs::DeviceBuffer ws_io;        // staging of host queries / results
+  cvs::DeviceBuffer ws_teams;     // per-team lists of multi-team graph search
 };
 
 struct cvs_dataset {

@@ -179,6 +179,23 @@ void search<float, std::uint32_t, std::int64_t>(
     auto clamp32 = [](std::uint64_t v) {
       return static_cast<std::uint32_t>(std::min<std::uint64_t>(v, 0xffffffffu));
     };
+    if (params.algo == search_algo::MULTI_CTA) {
+      // Teams of workgroups per query with 32-entry lists (k if larger), as
+      // many teams as cuVS's multi-CTA mode uses CTAs: max(search_width,
+      // ceil(itopk_size / 32)), at least 2, within CVS_CAGRA_MAX_TEAMS and
+      // CVS_CAGRA_MAX_ITOPK entries in all.  The reference's own multi-team
+      // kernel (shaders/cagra_kernels.metal:200-327) is compiled but disabled.
+      const std::uint64_t itopk = params.itopk_size ? params.itopk_size : 128;
+      const std::uint64_t per_team = std::max<std::uint64_t>(32, static_cast<std::uint64_t>(k));
+      std::uint64_t teams = std::max<std::uint64_t>({2, params.search_width, (itopk + 31) / 32});
+      teams = std::min<std::uint64_t>({teams, CVS_CAGRA_MAX_TEAMS, std::max<std::uint64_t>(1, CVS_CAGRA_MAX_ITOPK / per_team)});
+      counted([&] {
+        return cvs_cagra_search_teams(ctx, dev.graph_index->ix, queries.data_handle(), q, k, clamp32(per_team), 1,
+                                      clamp32(params.max_iterations), clamp32(teams), neighbors.data_handle(),
+                                      distances.data_handle());
+      });
+      return;
+    }
     counted([&] {
       return cvs_cagra_search(ctx, dev.graph_index->ix, queries.data_handle(), q, k,
                               clamp32(params.itopk_size), clamp32(params.search_width),

@@ -55,6 +55,7 @@ typedef struct cvs_cagra_index cvs_cagra_index; /* device-resident graph index (
 #define CVS_CAGRA_MAX_DIM 1024
 #define CVS_CAGRA_MAX_ITOPK 512
 #define CVS_CAGRA_MAX_WIDTH 16
+#define CVS_CAGRA_MAX_TEAMS 64
 
 /* ---- errors, counters ---------------------------------------------------- */
 
@@ -177,6 +178,23 @@ int cvs_cagra_index_edge_distances(cvs_context* ctx, const cvs_cagra_index* inde
 int cvs_cagra_search(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
                      int64_t k, uint32_t itopk_size, uint32_t search_width, uint32_t max_iterations,
                      uint32_t* out_neighbors, float* out_distances);
+
+/* Multi-team graph search, the reference's cagra_beam_search_multi_cta
+ * (shaders/cagra_kernels.metal:200-327, host merge src/metal_context.mm:
+ * 1003-1035): `teams` independent searches per query (1 to
+ * CVS_CAGRA_MAX_TEAMS), each with its own itopk list (itopk_size as above,
+ * teams * itopk at most CVS_CAGRA_MAX_ITOPK) and its own share of the start
+ * candidates (team t takes candidates t, t + teams, ...); the teams' lists are
+ * merged on the GPU, an id found by several teams counted once.  Smaller
+ * per-team lists need fewer iterations, so a small batch (Q = 1) answers
+ * sooner.  Host pointers, blocking; the _async form takes device pointers. */
+int cvs_cagra_search_teams(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
+                           int64_t k, uint32_t itopk_size, uint32_t search_width, uint32_t max_iterations,
+                           uint32_t teams, uint32_t* out_neighbors, float* out_distances);
+int cvs_cagra_search_teams_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                                 int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                                 uint32_t max_iterations, uint32_t teams, uint32_t* out_neighbors_dev,
+                                 float* out_distances_dev);
 
 /* Same, with device pointers; enqueued on the context stream.
  * `out_stats_dev` (q x 2 uint32, may be null) receives per query the number

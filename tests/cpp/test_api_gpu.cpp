@@ -200,6 +200,31 @@ void build_save_load_search(const std::string& scratch) {
   const double recall = double(hits) / (Q * K);
   std::printf("graph search recall@10 after save/load: %.3f\n", recall);
   CHECK(recall >= 0.9);
+
+  // search_algo::MULTI_CTA: teams of workgroups per query, merged; each row
+  // sorted by distance with unique ids, distances those of the exact search
+  // for the same ids, recall close to the single search's.
+  cagra::search_params mp;
+  mp.algo = cagra::search_algo::MULTI_CTA;
+  mp.itopk_size = 128;  // 4 teams of 32
+  std::vector<std::uint32_t> m(Q * K);
+  std::vector<float> md(Q * K);
+  cagra::search(res, mp, loaded, raft::make_device_matrix_view<const float, std::int64_t>(qs.data(), Q, D),
+                raft::make_device_matrix_view<std::uint32_t, std::int64_t>(m.data(), Q, K),
+                raft::make_device_matrix_view<float, std::int64_t>(md.data(), Q, K));
+  int mhits = 0;
+  for (int i = 0; i < Q; ++i) {
+    std::set<std::uint32_t> s(e.begin() + i * K, e.begin() + (i + 1) * K);
+    std::set<std::uint32_t> row(m.begin() + i * K, m.begin() + (i + 1) * K);
+    CHECK(row.size() == std::size_t(K));
+    for (int j = 0; j < K; ++j) {
+      mhits += s.count(m[i * K + j]) ? 1 : 0;
+      if (j > 0) CHECK(md[i * K + j - 1] <= md[i * K + j]);
+    }
+  }
+  const double mrecall = double(mhits) / (Q * K);
+  std::printf("multi-team (MULTI_CTA) recall@10: %.3f\n", mrecall);
+  CHECK(mrecall >= recall - 0.05);
 }
 
 }  // namespace

@@ -247,3 +247,54 @@ def test_edge_distances_match_oracle(ctx, cvs, oracle, n, d, g):
     idx.edge_distances(out=dev)
     ctx.synchronize()
     np.testing.assert_array_equal(dev.to_host(), got)
+
+
+@pytest.mark.parametrize("bits", [16, 32])
+def test_teams_complete_graph_known_answers(ctx, oracle, bits):
+    """Multi-team search (cvs_cagra_search_teams): on a complete graph every
+    team reaches every row in its first expansion, so the merged result is
+    the exact top-k once per id, whichever team found it (the FAISS smoke
+    answers, reference tests/faiss_v1_8_cagra_runtime_smoke.cpp:299-357,
+    including the tie at distance 100 and the k > n padding)."""
+    db = np.array([[0, 0], [10, 0], [0, 10], [2, 2]], np.float32)
+    qs = np.array([[0, 0], [9, 1]], np.float32)
+    idx = ctx.cagra_index(db, complete_graph(4), oracle.cagra_nav_nodes(4), traversal_bits=bits)
+    for teams in (2, 3, 8):
+        nbr, dist = idx.search_teams(qs, 5, teams, itopk_size=8)
+        assert nbr[:, :4].tolist() == [[0, 3, 1, 2], [1, 3, 0, 2]], teams
+        assert dist[:, :4].tolist() == [[0.0, 8.0, 100.0, 100.0], [2.0, 50.0, 82.0, 162.0]]
+        assert nbr[:, 4].tolist() == [INV, INV] and np.isinf(dist[:, 4]).all()
+
+
+@pytest.mark.parametrize("teams,itopk,bits", [(4, 32, 16), (8, 16, 16), (4, 32, 32), (16, 32, 16)])
+def test_teams_recall_and_invariants(ctx, oracle, teams, itopk, bits):
+    """Multi-team search on a kNN graph: rows sorted by (distance, id), ids
+    unique (a row found by several teams is kept once), exact distances, and
+    recall@10 at least the single search's with a list of the same total
+    length capped at 64, minus 0.02."""
+    rng = np.random.default_rng(teams * 100 + itopk)
+    n, d, g, k = 4000, 96, 32, 10
+    centers = rng.standard_normal((16, d)).astype(np.float32)
+    base = centers[rng.integers(0, 16, n)] + 0.5 * rng.standard_normal((n, d)).astype(np.float32)
+    qs = centers[rng.integers(0, 16, 200)] + 0.5 * rng.standard_normal((200, d)).astype(np.float32)
+    graph = oracle.knn_graph(base, g, threads=16)
+    idx = ctx.cagra_index(base, graph, oracle.cagra_nav_nodes(n), traversal_bits=bits)
+    gt, _ = oracle.bf_exact(base, qs, k, threads=16)
+    nbr, dist = idx.search_teams(qs, k, teams, itopk_size=itopk)
+    check_invariants(base, qs, nbr, dist)
+    single, _ = idx.search(qs, k, itopk_size=min(64, teams * itopk))
+    r_teams, r_single = recall(nbr, gt, k), recall(single, gt, k)
+    print(f"{teams} teams x itopk {itopk}: recall@10 {r_teams:.4f}, single search {r_single:.4f}")
+    assert r_teams >= r_single - 0.02
+
+
+def test_teams_argument_errors(ctx, oracle):
+    base = np.ones((10, 4), np.float32)
+    idx = ctx.cagra_index(base, complete_graph(10))
+    q = np.ones((2, 4), np.float32)
+    with pytest.raises(ValueError):
+        idx.search_teams(q, 4, 0)
+    with pytest.raises(ValueError):
+        idx.search_teams(q, 4, 65)
+    with pytest.raises(ValueError):
+        idx.search_teams(q, 4, 4, itopk_size=256)   # 4 x 256 > 512
