@@ -239,6 +239,32 @@ int cvs_cagra_build(cvs_context* ctx, const float* rows, int64_t n, int64_t d, i
                     float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
                     cvs_build_stats* stats);
 
+/* Phase timings and counters of one cvs_cagra_build_reference call. */
+typedef struct cvs_ref_build_stats {
+  uint32_t graph_degree;          /* output degree (<= n - 1) */
+  uint32_t clusters;              /* k-means centres (0 on the exact path) */
+  uint32_t kmeans_iterations;     /* Lloyd iterations run (<= 20) */
+  uint32_t descent_iterations;    /* 2-hop nn-descent iterations run (<= 5) */
+  uint32_t descent_changed_nodes; /* nodes whose list changed in the last iteration */
+  double seconds_kmeans;
+  double seconds_seed;            /* exact or per-cluster seeding + random bucketing */
+  double seconds_descent;
+  double seconds_total;
+} cvs_ref_build_stats;
+
+/* The reference's own graph build for n <= 200,000, on the GPU: for
+ * n <= 50,000 the exact degree-G kNN graph (src/metal_context.mm:324-349);
+ * above, IVF k-means seeding with per-cluster exact neighbours over the own
+ * and 3 nearest clusters (:351-435, :576-611, :712-792), one random bucketing
+ * round (:795-851) and at most 5 nn-descent iterations over 2-hop neighbours
+ * (:853-911), G = min(graph_degree, n - 1) <= 64.  Lists never repeat an id
+ * (the reference's may).  For graph-quality comparison with cvs_cagra_build;
+ * n > 200,000 (the reference's PQ seeding) is CVS_ERR_UNSUPPORTED.  Output
+ * as cvs_cagra_build. */
+int cvs_cagra_build_reference(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                              uint32_t graph_degree, uint32_t* out_graph, int graph_on_device,
+                              cvs_ref_build_stats* stats);
+
 #ifdef __cplusplus
 }
 #endif

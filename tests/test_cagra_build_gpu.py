@@ -131,3 +131,43 @@ def test_c5_full_size_build(ctx, cvs, oracle):
     r = recall(nbr, gt, 10)
     print(f"N=1M build: {st['seconds_total']:.2f} s, {st['iterations']} iterations, recall@10 {r:.4f}")
     assert r >= 0.6, r
+
+
+def neighbour_recall(graph, exact, k):
+    """Share of each row's exact k nearest neighbours present in its list."""
+    return float(np.mean([len(set(graph[i].tolist()) & set(exact[i, :k].tolist())) / k for i in range(len(graph))]))
+
+
+@pytest.mark.parametrize("n,d,g", [(3000, 64, 32), (60_000, 128, 64)])
+def test_reference_build_matches_oracle(ctx, cvs, oracle, n, d, g):
+    """cvs_cagra_build_reference (the reference's build, src/metal_context.mm:
+    289-914, on the GPU) against the oracle's restatement of it on the same
+    data: the same graph invariants (no repeated ids, which the reference
+    itself allows), neighbour quality within 0.02 of the restated graph's,
+    and the restated reference search on each graph within 0.02 recall.
+    n = 3000: the exact path (exact kNN graph: all but ties equal); n = 60,000:
+    k-means + per-cluster seeding, bucketing and nn-descent."""
+    base = cvs.synth_clustered(4242, cvs.STREAM_BASE, n, d)
+    qs = cvs.synth_clustered(4242, cvs.STREAM_QUERIES, 300, d)
+    graph, st = ctx.cagra_build_reference(base, g)
+    check_graph(graph, n, g)
+    ref = oracle.cagra_build_reference(base, g, threads=16)
+    sample = np.random.default_rng(1).choice(n, 500, replace=False)
+    gt_rows, _ = oracle.bf_exact(base, base[sample], 11, threads=16)
+    exact = np.stack([r[r != s][:10] for r, s in zip(gt_rows, sample)])
+    q_gpu = neighbour_recall(graph[sample], exact, 10)
+    q_ref = neighbour_recall(ref[sample], exact, 10)
+    nav = oracle.cagra_nav_nodes(n)
+    gt, _ = oracle.bf_exact(base, qs, 10, threads=16)
+    s_gpu, _ = oracle.cagra_reference_search(base, graph, nav, qs, 10, itopk_size=64, threads=16)
+    s_ref, _ = oracle.cagra_reference_search(base, ref, nav, qs, 10, itopk_size=64, threads=16)
+    r_gpu, r_ref = recall(s_gpu, gt, 10), recall(s_ref, gt, 10)
+    print(f"n={n}: stats {st}; neighbour recall@10 gpu {q_gpu:.4f} oracle {q_ref:.4f}; "
+          f"search recall gpu graph {r_gpu:.4f} oracle graph {r_ref:.4f}")
+    if n <= 50_000:
+        assert st["clusters"] == 0 and q_gpu >= 0.999
+    else:
+        assert st["clusters"] == int(np.sqrt(n)) and 1 <= st["kmeans_iterations"] <= 20
+        assert 1 <= st["descent_iterations"] <= 5
+    assert q_gpu >= q_ref - 0.02
+    assert r_gpu >= r_ref - 0.02
