@@ -486,10 +486,8 @@ void build_reference(cvs_context* ctx, const float* rows_in, int64_t n, int64_t 
   float* rows = mem.alloc<float>(size_t(n) * dp);
   float* rnorm = mem.alloc<float>(size_t(n));
   uint64_t* keys = mem.alloc<uint64_t>(size_t(n) * g);
-  CVS_HIP(hipMemsetAsync(rows, 0, size_t(n) * dp * sizeof(float), s));
-  CVS_HIP(hipMemcpy2DAsync(rows, size_t(dp) * sizeof(float), rows_in, size_t(d) * sizeof(float),
-                           size_t(d) * sizeof(float), size_t(n),
-                           rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
+  if (dp != d) CVS_HIP(hipMemsetAsync(rows, 0, size_t(n) * dp * sizeof(float), s));
+  upload_rows(ctx, rows, dp, rows_in, n, d, rows_on_device);
   hipLaunchKernelGGL(row_norms_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, s, rows, n, dp, rnorm);
   after_launch("row_norms_kernel");
   CVS_HIP(hipMemsetAsync(keys, 0xff, size_t(n) * g * sizeof(uint64_t), s));

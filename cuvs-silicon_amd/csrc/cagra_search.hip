@@ -695,9 +695,7 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
       CVS_HIP(hipMalloc(&ix->graph, size_t(n) * degree * sizeof(uint32_t)));
       if (n_seeds) CVS_HIP(hipMalloc(&ix->seeds, size_t(n_seeds) * sizeof(uint32_t)));
       if (ix->dpad != d) CVS_HIP(hipMemsetAsync(ix->rows, 0, row_bytes, ctx->stream));
-      CVS_HIP(hipMemcpy2DAsync(ix->rows, size_t(ix->dpad) * sizeof(float), rows, size_t(d) * sizeof(float),
-                               size_t(d) * sizeof(float), size_t(n),
-                               rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream));
+      upload_rows(ctx, ix->rows, ix->dpad, rows, n, d, rows_on_device);
       CVS_HIP(hipMalloc(&ix->rows16, size_t(n) * size_t(ix->dpad) * 2));
       hipLaunchKernelGGL(rows_to_half_kernel, dim3(unsigned((size_t(n) * size_t(ix->dpad) / 8 + 255) / 256)), dim3(256),
                          0, ctx->stream, reinterpret_cast<const float4*>(ix->rows), size_t(n) * size_t(ix->dpad) / 8,

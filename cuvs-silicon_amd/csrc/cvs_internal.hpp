@@ -118,6 +118,14 @@ namespace cvs {
 // Makes the context's device current for the calling thread.
 void bind(cvs_context* ctx);
 
+// Copies n rows of d floats (contiguous, host or device memory) into dst
+// with a row pitch of `pitch` floats (pitch >= d; the pad columns are left as
+// they are), enqueued on the context stream.  A host source moves in one
+// contiguous transfer (staged through a device buffer when pitch != d):
+// row-by-row transfers from pageable host memory are slow.
+void upload_rows(cvs_context* ctx, float* dst, int64_t pitch, const float* src, int64_t n, int64_t d,
+                 int src_on_device);
+
 // Event bracketing for the timing facility.
 hipEvent_t timer_begin(cvs_context* ctx, const char* kernel);
 void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin);

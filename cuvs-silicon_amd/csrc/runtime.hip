@@ -40,6 +40,36 @@ void bind(cvs_context* ctx) {
   CVS_HIP(hipSetDevice(ctx->device));
 }
 
+void upload_rows(cvs_context* ctx, float* dst, int64_t pitch, const float* src, int64_t n, int64_t d,
+                 int src_on_device) {
+  const size_t row = size_t(d) * sizeof(float);
+  if (pitch == d) {
+    CVS_HIP(hipMemcpyAsync(dst, src, row * size_t(n), src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           ctx->stream));
+    return;
+  }
+  const float* dsrc = src;
+  void* staging = nullptr;
+  if (!src_on_device) {
+    CVS_HIP(hipMalloc(&staging, row * size_t(n)));
+    const hipError_t e = hipMemcpyAsync(staging, src, row * size_t(n), hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+      (void)hipFree(staging);
+      check_hip(e, "hipMemcpyAsync");
+    }
+    dsrc = static_cast<const float*>(staging);
+  }
+  const hipError_t e = hipMemcpy2DAsync(dst, size_t(pitch) * sizeof(float), dsrc, row, row, size_t(n),
+                                        hipMemcpyDeviceToDevice, ctx->stream);
+  if (staging) {
+    // The staging buffer is released once the copy out of it has finished.
+    const hipError_t es = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(staging);
+    check_hip(es, "hipStreamSynchronize");
+  }
+  check_hip(e, "hipMemcpy2DAsync");
+}
+
 hipEvent_t timer_begin(cvs_context* ctx, const char* kernel) {
   if (!ctx->timing) return nullptr;
   KernelTimer& t = ctx->timers[kernel];
