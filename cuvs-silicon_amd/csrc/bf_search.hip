@@ -210,6 +210,7 @@ void bf_scan_kernel(ScanArgs a) {
 
   __shared__ u32x4 s_stage[2][kStageVecs];
   __shared__ float s_dn[2][NF];
+  __shared__ float s_dnp[PIPE ? 4 : 1][32];  // pipelined scan: norms of tiles t & 3
   __shared__ uint64_t s_buf[L::GL ? 1 : kQB * CAP];
 
   const int tid = threadIdx.x;
@@ -478,13 +479,16 @@ void bf_scan_kernel(ScanArgs a) {
     }
   } else {
     // ---- software-pipelined scan (32 or 64 k-steps per tile) ----
-    // Stage j sits in LDS buffer j&1 and register set j&1 (ra / rb).  Per
-    // stage, after one barrier, a single scheduling region interleaves with
-    // the stage's 32 MFMAs: the previous tile's distance/threshold test
-    // (VALU), the LDS store of stage j+1 (its buffer was last read in stage
-    // j-1, which every wave finished before the barrier), the HBM load of
-    // stage j+3 into the registers just stored, and the norms of the current
-    // tile.  Only the rare list
+    // Stage j sits in LDS buffer j&1 and, until it is stored there, in
+    // register set j&1 (ra / rb).  Per stage, after one barrier, a single scheduling region
+    // interleaves with the stage's 32 MFMAs: the previous tile's
+    // distance/threshold test (VALU), the LDS store of stage j+1 (its buffer
+    // was last read in stage j-1, which every wave finished before the
+    // barrier) and the HBM load of stage j+3 into the registers just stored.
+    // A tile's norms travel with its last stage: loaded with that stage's
+    // register set (one float per lane, row lane%32), stored to LDS slot
+    // (tile & 3) together with the stage, and read by the epilogue in the
+    // next tile's first stage, two barriers later.  Only the rare list
     // append after the MFMAs branches.
     auto lstore_b = [&](int buf, const u32x4 (&r)[kLoadsPerThread]) CVS_INLINE {
 #pragma unroll
@@ -501,8 +505,17 @@ void bf_scan_kernel(ScanArgs a) {
       }
       return pass;
     };
+    // Norms of this workgroup's tiles (local tile t at byte 128 t); loads
+    // past the last tile return zeros without a memory access.
+    const __amdgpu_buffer_rsrc_t nrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(reinterpret_cast<const float*>(a.norms) + (stage_of(0) / SPT) * 32), 0,
+        int(uint32_t(n_stages / SPT) * 128u), kRsrcWord3);
+    auto nload = [&](int s) CVS_INLINE -> float {
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           nrsrc, uint32_t(s / SPT) * 128u + uint32_t(lane & 31) * 4u, 0, 0));
+    };
+    auto dn_slot = [&](int t) CVS_INLINE -> float* { return s_dnp[t & 3]; };
     f32x16 dv;
-    f32x4 dn[2][4];
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[r] = 0.f;
 
@@ -510,20 +523,19 @@ void bf_scan_kernel(ScanArgs a) {
     // interleave is fixed: slot i issues MFMA i, the LDS read of block i+8
     // (8-deep A ring, two accumulation chains), and one piece of the side
     // work.  Slot 0 of a tile's first stage first sums the previous tile's
-    // two chains; slots 8-11 of its last stage load this tile's norms ahead
-    // of the stage loads (so waiting for them never waits for newer loads);
-    // slots 12-19 store stage j+1 to LDS and reuse each register for stage
-    // j+3; slots 16-31 of a first stage turn the previous tile's dot
-    // products into distances and pass bits.
-    auto pstep = [&](auto par_c, u32x4 (&r)[kLoadsPerThread], int j) CVS_INLINE {
+    // two chains and slots 8-11 read that tile's norms from LDS; slots 12-19
+    // store stage j+1 to LDS and reuse each register for stage j+3; slot 20
+    // stores a tile's norms, slot 21 loads them; slots 16-31 of a first stage
+    // turn the previous tile's dot products into distances and pass bits.
+    auto pstep = [&](auto par_c, u32x4 (&r)[kLoadsPerThread], float& rn, int j) CVS_INLINE {
       constexpr int PAR = decltype(par_c)::value;
-      constexpr bool FIRST = SPT == 1 || PAR == 0;  // first stage of its tile
-      constexpr bool LAST = SPT == 1 || PAR == 1;   // last stage of its tile
+      constexpr bool FIRST = SPT == 1 || PAR == 0;    // first stage of its tile
+      constexpr bool STORE_N = SPT == 1 || PAR == 0;  // stage j+1 (stored here) ends a tile
+      constexpr bool LOAD_N = SPT == 1 || PAR == 0;   // stage j+3 (loaded here) ends a tile
       constexpr int KOFF = (PAR * kStageBlocks) % KS;
-      constexpr int DN_USE = SPT == 1 ? (PAR ^ 1) : 0;  // norms of the previous tile
-      constexpr int DN_LOAD = SPT == 1 ? PAR : 0;       // norms of this tile
       constexpr int PF = 8;
       const int64_t tile = (stage_of(0) + j) / SPT;
+      const int tl = j / SPT;  // tile of stage j, counted in this workgroup
       const u32x4* sb = s_stage[PAR] + lane;
       const uint32_t off = uint32_t(j + 3) * kStageBytes + uint32_t(tid) * 16;
       __syncthreads();
@@ -535,6 +547,7 @@ void bf_scan_kernel(ScanArgs a) {
 #pragma unroll
       for (int p = 0; p < PF; ++p) ring[p] = __builtin_bit_cast(half8, sb[p * 64]);
       uint32_t pass = 0;
+      f32x4 dn4[4];
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < kStageBlocks; ++i) {
@@ -545,10 +558,11 @@ void bf_scan_kernel(ScanArgs a) {
           acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + i], (FIRST && i < 2) ? zero : acc1, 0, 0, 0);
         else
           acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[KOFF + i], (FIRST && i < 2) ? zero : acc0, 0, 0, 0);
-        if constexpr (LAST) {
+        if constexpr (FIRST) {
           if (i >= 8 && i < 12) {
             const int g = i - 8;
-            dn[DN_LOAD][g] = a.norms[tile * 8 + 2 * g + (lane >> 5)];
+            // Slot of tile tl-1 (for the first tile: never written, masked below).
+            dn4[g] = *reinterpret_cast<const f32x4*>(dn_slot(tl + 3) + 8 * g + 4 * (lane >> 5));
           }
         }
         if (i >= 12 && i < 12 + kLoadsPerThread) {
@@ -557,10 +571,16 @@ void bf_scan_kernel(ScanArgs a) {
           r[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                rsrc, off + uint32_t(e * kThreads * 16), 0, kAuxNT));
         }
+        if constexpr (STORE_N) {
+          if (i == 20) dn_slot((j + 1) / SPT)[lane & 31] = rn;
+        }
+        if constexpr (LOAD_N) {
+          if (i == 21) rn = nload(j + 3);
+        }
         if constexpr (FIRST) {
           if (i >= 16) {
             const int q = i - 16;
-            dv[q] = qn + dn[DN_USE][q >> 2][q & 3] - 2.0f * dv[q];
+            dv[q] = qn + dn4[q >> 2][q & 3] - 2.0f * dv[q];
             pass |= (dv[q] < thr ? 1u : 0u) << q;
           }
         }
@@ -572,17 +592,26 @@ void bf_scan_kernel(ScanArgs a) {
         commit(dv, pass, (tile - 1) * 32);
       }
     };
+    // Register sets: stage s in set s & 1; ra and rb hold stages 0 and 1.
+    float na = 0.f, nb = nload(1);
+    if constexpr (SPT == 1) na = nload(0);
     lstore_b(0, ra);
+    if constexpr (SPT == 1) dn_slot(0)[lane & 31] = na;
     gload_b(ra, 2);
+    if constexpr (SPT == 1) na = nload(2);
     for (int j = 0; j < n_stages; j += 2) {
-      pstep(std::integral_constant<int, 0>{}, rb, j);
-      pstep(std::integral_constant<int, 1>{}, ra, j + 1);
+      pstep(std::integral_constant<int, 0>{}, rb, nb, j);
+      pstep(std::integral_constant<int, 1>{}, ra, na, j + 1);
     }
-    // Last tile.
-    constexpr int DN_LAST = SPT == 1 ? 1 : 0;
+    // Last tile (its norms were stored with its last stage, before the
+    // final barrier).
+    f32x4 dn_last[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      dn_last[g] = *reinterpret_cast<const f32x4*>(dn_slot(n_stages / SPT - 1) + 8 * g + 4 * (lane >> 5));
 #pragma unroll
     for (int q = 0; q < 16; ++q) dv[q] = acc0[q] + acc1[q];
-    const uint32_t pass = prepare(dv, dn[DN_LAST]);
+    const uint32_t pass = prepare(dv, dn_last);
     commit(dv, pass, ((stage_of(0) + n_stages) / SPT - 1) * 32);
   }
 
