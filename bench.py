@@ -549,6 +549,25 @@ def run_cagra_build(args) -> int:
                            "achieved_gbs": e_bytes / (ems * 1e-3) / 1e9 if ems else None,
                            "hbm_frac": e_bytes / (ems * 1e-3) / 1e9 / HBM_PEAK_GBS if ems else None},
     }
+    # The reference's own build algorithm at this size, on the GPU, for
+    # comparison (above 200,000 rows: IVF k-means, product-quantised
+    # per-cluster seeding re-scored exactly, one bucketing round, no
+    # nn-descent; src/metal_context.mm:289-914, src/cagra.cpp:59).  The
+    # reference's own run of it at N=1M took 2714 s for recall 0.72 at itopk
+    # 512 (docs/multi-cta-ivf-pq-lessons.md:5).
+    if n > 200_000 and d == 1024 and not args.no_recall:
+        log("building with the reference's algorithm")
+        t = time.perf_counter()
+        rgraph, rst = ctx.cagra_build_reference(base, args.degree)
+        rwall = time.perf_counter() - t
+        log(json.dumps(rst))
+        ridx = ctx.cagra_index(drows, rgraph, nav)
+        rec = {}
+        for it in (args.itopk, 512):
+            rn, _ = ridx.search(qs, k, itopk_size=it)
+            on, _ = idx.search(qs, k, itopk_size=it)
+            rec[f"itopk {it}"] = {"reference_algorithm_graph": recall_at_k(rn, gt, k), "this_build": recall_at_k(on, gt, k)}
+        out["reference_algorithm"] = {"seconds": rwall, "stats": rst, "recall_at_10": rec, "queries": q}
     print(json.dumps(out), flush=True)
     return 0
 

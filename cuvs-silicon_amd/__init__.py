@@ -63,6 +63,8 @@ _SIGNATURES = {
     "cvs_cagra_index_set_traversal": (c_int, [c_void_p, c_int]),
     "cvs_cagra_build_reference": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_void_p, c_int,
                                           c_void_p]),
+    "cvs_cagra_build_reference_ex": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_int64, c_int64,
+                                             c_void_p, c_int, c_void_p]),
     "cvs_cagra_index_edge_distances": (c_int, [c_void_p, c_void_p, c_void_p, c_int]),
     "cvs_cagra_search_teams": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32, c_uint32, c_uint32,
                                        c_uint32, c_void_p, c_void_p]),
@@ -78,7 +80,7 @@ class RefBuildStats(ctypes.Structure):
     _fields_ = [("graph_degree", c_uint32), ("clusters", c_uint32), ("kmeans_iterations", c_uint32),
                 ("descent_iterations", c_uint32), ("descent_changed_nodes", c_uint32),
                 ("seconds_kmeans", c_double), ("seconds_seed", c_double), ("seconds_descent", c_double),
-                ("seconds_total", c_double)]
+                ("seconds_total", c_double), ("pq_iterations", c_uint32), ("seconds_pq", c_double)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -248,17 +250,25 @@ class Context:
     def cagra_index(self, rows, graph, seeds=None, traversal_bits: int = 16) -> "CagraIndex":
         return CagraIndex(self, rows, graph, seeds, traversal_bits)
 
-    def cagra_build_reference(self, rows, graph_degree: int = 64):
+    def cagra_build_reference(self, rows, graph_degree: int = 64, exact_limit: int = None, pq_limit: int = None):
         """The reference's own build algorithm on the GPU (exact seeding for
         n <= 50,000; IVF k-means + per-cluster seeding, random bucketing and
-        2-hop nn-descent up to 200,000).  Returns (graph, stats)."""
+        2-hop nn-descent up to 200,000; product-quantised seeding above).
+        exact_limit / pq_limit replace those two sizes (tests).  Returns
+        (graph, stats)."""
         st = RefBuildStats()
         rows = _f32(rows)
         n, d = rows.shape
         g = max(min(int(graph_degree), n - 1), 1)
         host = np.empty((n, g), np.uint32)
-        _check(load().cvs_cagra_build_reference(self.handle, rows.ctypes.data_as(c_void_p), n, d, 0, int(graph_degree),
-                                                host.ctypes.data_as(c_void_p), 0, byref(st)))
+        if exact_limit is None and pq_limit is None:
+            _check(load().cvs_cagra_build_reference(self.handle, rows.ctypes.data_as(c_void_p), n, d, 0,
+                                                    int(graph_degree), host.ctypes.data_as(c_void_p), 0, byref(st)))
+        else:
+            _check(load().cvs_cagra_build_reference_ex(
+                self.handle, rows.ctypes.data_as(c_void_p), n, d, 0, int(graph_degree),
+                50000 if exact_limit is None else int(exact_limit), 200000 if pq_limit is None else int(pq_limit),
+                host.ctypes.data_as(c_void_p), 0, byref(st)))
         return host, st.as_dict()
 
     def cagra_build(self, rows, intermediate_degree: int = 128, graph_degree: int = 64, max_iterations: int = 20,

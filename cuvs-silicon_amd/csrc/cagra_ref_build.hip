@@ -1,7 +1,7 @@
 // The reference's own CAGRA graph build on gfx950 (cvs_cagra_build_reference).
 //
-// Restates MetalContext::build_knn_graph for N <= 200,000
-// (src/metal_context.mm:289-914, called from src/cagra.cpp:47-59), so that a
+// Restates MetalContext::build_knn_graph (src/metal_context.mm:289-914,
+// called from src/cagra.cpp:47-59), so that a
 // graph of the reference's algorithm can be built on the GPU and compared with
 // this library's own build (cagra_build.hip):
 //
@@ -29,6 +29,20 @@
 //                         nn-descent (:853-911): 5 iterations over the
 //                         2-hop neighbours (lists as at the start of the
 //                         iteration), stopping early when no list changes.
+//   N > 200,000           the same k-means and candidate lists, but the
+//                         seeding ranks candidates by product-quantisation
+//                         distance (:437-568, :614-681): 8 subspaces of 128
+//                         dimensions, 256 centres each (k-means, at most 10
+//                         iterations), distance = the sum over subspaces of
+//                         the squared distance of the two rows' centres,
+//                         computed here as the squared distance of the rows
+//                         rebuilt from their codes; the kept entries then get
+//                         exact distances (:683-709); random bucketing as
+//                         above; no nn-descent (src/cagra.cpp:59).
+//
+// cvs_cagra_build_reference_ex takes the two size limits (50,000 and
+// 200,000 in the reference) as arguments, so that the phases of a size
+// class can also run at other sizes (tests).
 //
 // Differences, all deliberate: lists never hold an id twice (the reference's
 // insert_neighbor does not check); an nn-descent iteration expands the
@@ -69,6 +83,14 @@ __global__ __launch_bounds__(256) void row_norms_kernel(const float* __restrict_
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) acc += xor_lanes_f(acc, o);
   if (lane == 0) out[r] = acc;
+}
+
+// Squared distance from two squared norms and a dot product, in one fixed
+// rounding order (no contraction), so that every kernel whose keys meet in
+// one list gives the same pair the same key and the lists' duplicate check
+// (equal adjacent keys) sees it.
+__device__ __forceinline__ float pair_dist(float na, float dot, float nb) {
+  return __fadd_rn(__fsub_rn(na, __fmul_rn(2.f, dot)), nb);
 }
 
 // The fp32 dot products of a 64-row x 64-column tile: row i of A =
@@ -305,7 +327,7 @@ __global__ __launch_bounds__(256) void group_topk_kernel(const float* __restrict
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * tr + i, c = 4 * tc + j;
         if (r < it.n_own && c < nb)
-          s_dist[r][c] = rnorm[s_aid[r]] - 2.f * acc[i][j] + rnorm[s_bid[c]];
+          s_dist[r][c] = pair_dist(rnorm[s_aid[r]], acc[i][j], rnorm[s_bid[c]]);
       }
     __syncthreads();
     for (int r = wave; r < it.n_own; r += 4) {
@@ -434,6 +456,58 @@ __global__ __launch_bounds__(256) void two_hop_kernel(const float4* __restrict__
   }
 }
 
+// Product quantisation of the reference's N > 200,000 path
+// (src/metal_context.mm:437-568): 8 subspaces of 128 dimensions, 256 centres
+// each.  Rows rebuilt from their codes: dimensions 128 m .. 128 m + 127 of
+// row i are centre codes[m][i] of subspace m, so the squared distance of two
+// rebuilt rows is the reference's symmetric table sum
+// sum_m |c_m(a) - c_m(b)|^2 (:552-566).  One workgroup per row.
+constexpr int kPqM = 8, kPqDim = 128, kPqK = 256;
+
+__global__ __launch_bounds__(256) void pq_decode_kernel(const uint32_t* __restrict__ codes,
+                                                        const float* __restrict__ ctr, int64_t n,
+                                                        float* __restrict__ out) {
+  const int64_t i = blockIdx.x;
+  const int t = threadIdx.x;  // float4 of the row
+  const int m = t >> 5;       // 32 float4 per subspace
+  const uint32_t c = codes[int64_t(m) * n + i];
+  const float4 v = reinterpret_cast<const float4*>(ctr + (int64_t(m) * kPqK + c) * kPqDim)[t & 31];
+  reinterpret_cast<float4*>(out + i * (kPqM * kPqDim))[t] = v;
+}
+
+// Exact squared L2 of every list entry (the reference's
+// recompute_graph_distances after PQ seeding, src/metal_context.mm:683-709),
+// then the list re-sorted by (distance, id).  One wave per row, lane e on
+// entry e: the same arithmetic as group_topk_kernel (dimension-order fused
+// multiply-adds, pair_dist), so a later bucketing merge that meets an entry
+// again computes the same key and drops the copy.
+__global__ __launch_bounds__(64) void rescore_keys_kernel(const float* __restrict__ rows,
+                                                          const float* __restrict__ rnorm, int dp, int g,
+                                                          uint64_t* __restrict__ keys) {
+  const int64_t node = blockIdx.x;
+  const int lane = threadIdx.x;
+  uint64_t* lst = keys + node * g;
+  const uint64_t key = lane < g ? lst[lane] : kNoKey;
+  uint64_t nk = kNoKey;
+  if (key != kNoKey) {
+    const uint32_t j = uint32_t(key) >> 1;
+    const float4* a = reinterpret_cast<const float4*>(rows + node * dp);
+    const float4* b = reinterpret_cast<const float4*>(rows + int64_t(j) * dp);
+    float acc = 0.f;
+    for (int c = 0; c < dp / 4; ++c) {
+      const float4 x = a[c], y = b[c];
+      acc = __builtin_fmaf(x.x, y.x, acc);
+      acc = __builtin_fmaf(x.y, y.y, acc);
+      acc = __builtin_fmaf(x.z, y.z, acc);
+      acc = __builtin_fmaf(x.w, y.w, acc);
+    }
+    nk = (uint64_t(ord_f32(pair_dist(rnorm[node], acc, rnorm[j]))) << 32) | uint32_t(key);
+  }
+  uint64_t v[1] = {nk};
+  wave_sort_e<1>(v);
+  if (lane < g) lst[lane] = v[0];
+}
+
 // keys -> ids (kNoId for empty slots).
 __global__ void keys_to_ids_kernel(const uint64_t* __restrict__ keys, size_t count, uint32_t* __restrict__ ids) {
   const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -466,12 +540,18 @@ struct Mem {
 };
 
 void build_reference(cvs_context* ctx, const float* rows_in, int64_t n, int64_t d, int rows_on_device,
-                     uint32_t graph_degree, uint32_t* out_graph, int graph_on_device, cvs_ref_build_stats* stats) {
+                     uint32_t graph_degree, int64_t exact_limit, int64_t pq_limit, uint32_t* out_graph,
+                     int graph_on_device, cvs_ref_build_stats* stats) {
   const auto t_start = std::chrono::steady_clock::now();
   if (!rows_in || !out_graph) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
   if (n <= 0 || d <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "dataset must be non-empty");
-  if (n > 200000) fail(CVS_ERR_UNSUPPORTED, "the reference's build for N > 200,000 (PQ seeding) is not provided");
   if (d > 1024) fail(CVS_ERR_UNSUPPORTED, "dimension exceeds 1024");
+  if (exact_limit < 0 || pq_limit < 0) fail(CVS_ERR_INVALID_ARGUMENT, "size limits must be non-negative");
+  // Product-quantised seeding above pq_limit (the reference's N > 200,000
+  // path) reads 8 subspaces of 128 dimensions of every row.
+  const bool pq = n > exact_limit && n > pq_limit;
+  if (pq && d != kPqM * kPqDim)
+    fail(CVS_ERR_UNSUPPORTED, "product-quantised seeding (N above the PQ limit) needs d = 1024");
   const int g = int(std::min<int64_t>(graph_degree, n - 1));
   if (g > kMaxG) fail(CVS_ERR_UNSUPPORTED, "graph_degree exceeds 64 for the reference build");
   cvs_ref_build_stats st{};
@@ -492,7 +572,7 @@ void build_reference(cvs_context* ctx, const float* rows_in, int64_t n, int64_t 
   after_launch("row_norms_kernel");
   CVS_HIP(hipMemsetAsync(keys, 0xff, size_t(n) * g * sizeof(uint64_t), s));
 
-  if (n <= 50000) {
+  if (n <= exact_limit) {
     // Exact seeding: the exact (g+1)-NN of every row by the fused brute-force
     // search, its own row dropped.
     const auto t_seed = std::chrono::steady_clock::now();
@@ -605,8 +685,86 @@ void build_reference(cvs_context* ctx, const float* rows_in, int64_t n, int64_t 
   }
   st.seconds_kmeans = seconds_since(t_km);
 
-  // Per-cluster exact seeding: groups of up to 64 own rows against the
-  // cluster's candidate list.
+  // Product quantisation (N above the PQ limit, src/metal_context.mm:449-568):
+  // per subspace m, k-means with 256 centres seeded by evenly strided rows,
+  // at most 10 Lloyd iterations (stopping when no row changes centre), then
+  // one more assignment pass as the codes; the rows rebuilt from their codes
+  // then stand in for the rows in the per-cluster seeding, whose distances
+  // are then the reference's symmetric PQ table sums.
+  float* seed_rows = rows;
+  float* seed_norm = rnorm;
+  if (pq) {
+    const auto t_pq = std::chrono::steady_clock::now();
+    float* sub = mem.alloc<float>(size_t(n) * kPqDim);
+    float* snorm = mem.alloc<float>(size_t(n));
+    float* pq_ctr = mem.alloc<float>(size_t(kPqM) * kPqK * kPqDim);
+    float* pcnorm = mem.alloc<float>(size_t(kPqK));
+    uint32_t* codes = mem.alloc<uint32_t>(size_t(kPqM) * n);
+    uint32_t* pinit_d = mem.alloc<uint32_t>(size_t(kPqK));
+    uint32_t* pmembers_d = mem.alloc<uint32_t>(size_t(n));
+    int64_t* pstarts_d = mem.alloc<int64_t>(size_t(kPqK) + 1);
+    std::vector<uint32_t> pinit(static_cast<size_t>(kPqK));
+    const double pstride = double(n) / double(kPqK);
+    for (int c = 0; c < kPqK; ++c)
+      pinit[size_t(c)] = uint32_t(std::min<int64_t>(int64_t(double(c) * pstride + pstride * 0.5), n - 1));
+    CVS_HIP(hipMemcpyAsync(pinit_d, pinit.data(), size_t(kPqK) * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    std::vector<uint32_t> passign(static_cast<size_t>(n)), pfresh(static_cast<size_t>(n));
+    std::vector<uint32_t> pmembers(static_cast<size_t>(n));
+    std::vector<int64_t> pstarts(static_cast<size_t>(kPqK) + 1);
+    auto assign_step = [&](float* ctr, uint32_t* out) {
+      hipLaunchKernelGGL(row_norms_kernel, dim3(unsigned((kPqK + 3) / 4)), dim3(256), 0, s, ctr, int64_t(kPqK),
+                         kPqDim, pcnorm);
+      after_launch("row_norms_kernel");
+      hipLaunchKernelGGL(nearest_centre_kernel, dim3(unsigned((n + kTile - 1) / kTile)), dim3(256), 0, s, sub, snorm,
+                         n, ctr, pcnorm, kPqK, kPqDim, out, static_cast<float*>(nullptr));
+      after_launch("nearest_centre_kernel");
+    };
+    for (int m = 0; m < kPqM; ++m) {
+      float* ctr = pq_ctr + size_t(m) * kPqK * kPqDim;
+      uint32_t* code_m = codes + size_t(m) * n;
+      CVS_HIP(hipMemcpy2DAsync(sub, kPqDim * sizeof(float), rows + m * kPqDim, size_t(dp) * sizeof(float),
+                               kPqDim * sizeof(float), size_t(n), hipMemcpyDeviceToDevice, s));
+      hipLaunchKernelGGL(row_norms_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, s, sub, n, kPqDim, snorm);
+      after_launch("row_norms_kernel");
+      hipLaunchKernelGGL(gather_rows_kernel, dim3(unsigned(kPqK)), dim3(256), 0, s, sub, kPqDim, pinit_d, kPqK, ctr);
+      after_launch("gather_rows_kernel");
+      for (int iter = 0; iter < 10; ++iter) {
+        assign_step(ctr, code_m);
+        CVS_HIP(hipMemcpyAsync(pfresh.data(), code_m, size_t(n) * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        CVS_HIP(hipStreamSynchronize(s));
+        ++st.pq_iterations;
+        const bool changed = iter == 0 || pfresh != passign;
+        passign.swap(pfresh);
+        if (!changed) break;
+        // Centre sums in row order (src/metal_context.mm:507-517).
+        std::fill(pstarts.begin(), pstarts.end(), 0);
+        for (int64_t i = 0; i < n; ++i) pstarts[size_t(passign[size_t(i)]) + 1]++;
+        for (int c = 0; c < kPqK; ++c) pstarts[size_t(c) + 1] += pstarts[size_t(c)];
+        std::vector<int64_t> fill(pstarts.begin(), pstarts.end() - 1);
+        for (int64_t i = 0; i < n; ++i) pmembers[size_t(fill[passign[size_t(i)]]++)] = uint32_t(i);
+        CVS_HIP(hipMemcpyAsync(pmembers_d, pmembers.data(), size_t(n) * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+        CVS_HIP(hipMemcpyAsync(pstarts_d, pstarts.data(), (size_t(kPqK) + 1) * sizeof(int64_t),
+                               hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(centre_sum_kernel, dim3(unsigned(kPqK)), dim3(256), 0, s, sub, kPqDim, pmembers_d,
+                           pstarts_d, ctr);
+        after_launch("centre_sum_kernel");
+      }
+      assign_step(ctr, code_m);  // the codes (:519-548)
+    }
+    seed_rows = mem.alloc<float>(size_t(n) * dp);
+    seed_norm = mem.alloc<float>(size_t(n));
+    hipLaunchKernelGGL(pq_decode_kernel, dim3(unsigned(n)), dim3(256), 0, s, static_cast<const uint32_t*>(codes),
+                       static_cast<const float*>(pq_ctr), n, seed_rows);
+    after_launch("pq_decode_kernel");
+    hipLaunchKernelGGL(row_norms_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, s, seed_rows, n, dp, seed_norm);
+    after_launch("row_norms_kernel");
+    CVS_HIP(hipStreamSynchronize(s));
+    st.seconds_pq = seconds_since(t_pq);
+  }
+
+  // Per-cluster seeding: groups of up to 64 own rows against the cluster's
+  // candidate list; exact distances, or PQ distances (rebuilt rows) then
+  // exact distances of the kept entries (src/metal_context.mm:683-709).
   const auto t_seed = std::chrono::steady_clock::now();
   {
     const int64_t max_own = (n / K) * 4 + 64;
@@ -633,9 +791,14 @@ void build_reference(cvs_context* ctx, const float* rows_in, int64_t n, int64_t 
     CVS_HIP(hipMemcpyAsync(cand_d, cand.data(), cand.size() * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     CVS_HIP(hipMemcpyAsync(items_d, items.data(), items.size() * sizeof(GroupItem), hipMemcpyHostToDevice, s));
     if (!items.empty()) {
-      hipLaunchKernelGGL(group_topk_kernel, dim3(unsigned(items.size())), dim3(256), 0, s, rows, rnorm, dp,
+      hipLaunchKernelGGL(group_topk_kernel, dim3(unsigned(items.size())), dim3(256), 0, s, seed_rows, seed_norm, dp,
                          static_cast<const uint32_t*>(cand_d), static_cast<const GroupItem*>(items_d), g, 0, keys);
       after_launch("group_topk_kernel");
+    }
+    if (pq) {
+      hipLaunchKernelGGL(rescore_keys_kernel, dim3(unsigned(n)), dim3(64), 0, s, static_cast<const float*>(rows),
+                         static_cast<const float*>(rnorm), dp, g, keys);
+      after_launch("rescore_keys_kernel");
     }
     CVS_HIP(hipStreamSynchronize(s));
   }
@@ -666,13 +829,15 @@ void build_reference(cvs_context* ctx, const float* rows_in, int64_t n, int64_t 
   }
   st.seconds_seed = seconds_since(t_seed);
 
-  // nn-descent over 2-hop neighbours, at most 5 iterations.
+  // nn-descent over 2-hop neighbours: at most 5 iterations, none on the PQ
+  // path (src/cagra.cpp:59).
   const auto t_nd = std::chrono::steady_clock::now();
   {
     uint64_t* other = mem.alloc<uint64_t>(size_t(n) * g);
     unsigned int* changed_d = mem.alloc<unsigned int>(1);
     uint64_t* cur = keys;
-    for (int iter = 0; iter < 5; ++iter) {
+    const int nd_iters = pq ? 0 : 5;
+    for (int iter = 0; iter < nd_iters; ++iter) {
       CVS_HIP(hipMemsetAsync(changed_d, 0, sizeof(unsigned int), s));
       hipLaunchKernelGGL(two_hop_kernel, dim3(unsigned(n)), dim3(256), 0, s, reinterpret_cast<const float4*>(rows),
                          dp / 4, dp / 64, uint32_t(n), g, static_cast<const uint64_t*>(cur), other, changed_d);
@@ -709,6 +874,17 @@ extern "C" int cvs_cagra_build_reference(cvs_context* ctx, const float* rows, in
                                          int graph_on_device, cvs_ref_build_stats* stats) {
   return guarded([&] {
     bind(ctx);
-    build_reference(ctx, rows, n, d, rows_on_device, graph_degree, out_graph, graph_on_device, stats);
+    build_reference(ctx, rows, n, d, rows_on_device, graph_degree, 50000, 200000, out_graph, graph_on_device, stats);
+  });
+}
+
+extern "C" int cvs_cagra_build_reference_ex(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
+                                            int rows_on_device, uint32_t graph_degree, int64_t exact_limit,
+                                            int64_t pq_limit, uint32_t* out_graph, int graph_on_device,
+                                            cvs_ref_build_stats* stats) {
+  return guarded([&] {
+    bind(ctx);
+    build_reference(ctx, rows, n, d, rows_on_device, graph_degree, exact_limit, pq_limit, out_graph,
+                    graph_on_device, stats);
   });
 }

@@ -250,20 +250,37 @@ typedef struct cvs_ref_build_stats {
   double seconds_seed;            /* exact or per-cluster seeding + random bucketing */
   double seconds_descent;
   double seconds_total;
+  uint32_t pq_iterations;         /* product-quantisation k-means iterations, all subspaces (PQ path) */
+  double seconds_pq;              /* product-quantisation training and encoding (PQ path) */
 } cvs_ref_build_stats;
 
-/* The reference's own graph build for n <= 200,000, on the GPU: for
- * n <= 50,000 the exact degree-G kNN graph (src/metal_context.mm:324-349);
- * above, IVF k-means seeding with per-cluster exact neighbours over the own
- * and 3 nearest clusters (:351-435, :576-611, :712-792), one random bucketing
- * round (:795-851) and at most 5 nn-descent iterations over 2-hop neighbours
- * (:853-911), G = min(graph_degree, n - 1) <= 64.  Lists never repeat an id
- * (the reference's may).  For graph-quality comparison with cvs_cagra_build;
- * n > 200,000 (the reference's PQ seeding) is CVS_ERR_UNSUPPORTED.  Output
- * as cvs_cagra_build. */
+/* The reference's own graph build on the GPU: for n <= 50,000 the exact
+ * degree-G kNN graph (src/metal_context.mm:324-349); above, IVF k-means
+ * seeding with per-cluster neighbours over the own and 3 nearest clusters
+ * (:351-435, :576-611, :712-792), one random bucketing round (:795-851) and
+ * at most 5 nn-descent iterations over 2-hop neighbours (:853-911); for
+ * n > 200,000 the per-cluster neighbours are ranked by product-quantisation
+ * distance (8 x 128-dimension subspaces, 256 centres; :437-568, :614-681)
+ * and re-scored exactly (:683-709), with no nn-descent (src/cagra.cpp:59);
+ * this needs d = 1024.  G = min(graph_degree, n - 1) <= 64.  Lists never
+ * repeat an id (the reference's may).  For graph-quality comparison with
+ * cvs_cagra_build.  Output as cvs_cagra_build.  Replaces
+ * MetalContext::build_knn_graph (metal_context.hpp:47-55) as called by
+ * cagra::build (src/cagra.cpp:47-62). */
 int cvs_cagra_build_reference(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
                               uint32_t graph_degree, uint32_t* out_graph, int graph_on_device,
                               cvs_ref_build_stats* stats);
+
+/* cvs_cagra_build_reference with the size limits of its phases as
+ * arguments: exact seeding for n <= exact_limit, product-quantised seeding
+ * for n > max(exact_limit, pq_limit), IVF seeding with exact distances
+ * between them (the reference's limits: 50,000 and 200,000,
+ * src/metal_context.mm:297, :438; src/cagra.cpp:59).  Lets tests run the
+ * reference's large-N phases at small n; cvs_cagra_build_reference is this
+ * call with the reference's limits. */
+int cvs_cagra_build_reference_ex(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                                 uint32_t graph_degree, int64_t exact_limit, int64_t pq_limit, uint32_t* out_graph,
+                                 int graph_on_device, cvs_ref_build_stats* stats);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,11 @@ def lib() -> ctypes.CDLL:
                                           c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_void_p, c_int]
         L.oracle_cagra_build_ref.restype = c_int
         L.oracle_cagra_build_ref.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
+        L.oracle_cagra_build_ref_ex.restype = c_int
+        L.oracle_cagra_build_ref_ex.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int, c_int64,
+                                                c_int64]
+        L.oracle_pq_train.restype = None
+        L.oracle_pq_train.argtypes = [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]
         L.oracle_knn_graph.restype = None
         L.oracle_knn_graph.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
         L.oracle_edge_distances.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int]
@@ -215,16 +220,32 @@ def knn_graph(base, g: int, threads: int = 1) -> np.ndarray:
     return out
 
 
-def cagra_build_reference(base, graph_degree: int = 64, threads: int = 1) -> np.ndarray:
-    """The reference's graph build restated (src/metal_context.mm:289-914,
-    n <= 200,000): returns n x min(graph_degree, n - 1) uint32 ids."""
+def cagra_build_reference(base, graph_degree: int = 64, threads: int = 1, exact_limit: int = 50000,
+                          pq_limit: int = 200000) -> np.ndarray:
+    """The reference's graph build restated (src/metal_context.mm:289-914):
+    returns n x min(graph_degree, n - 1) uint32 ids.  exact_limit / pq_limit
+    are the size limits of its phases (the reference's: 50,000 and 200,000)."""
     base = np.ascontiguousarray(base, np.float32)
     n, d = base.shape
     g = min(int(graph_degree), n - 1)
     out = np.empty((n, max(g, 0)), np.uint32)
-    rc = lib().oracle_cagra_build_ref(_p(base), n, d, int(graph_degree), _p(out), int(threads))
+    rc = lib().oracle_cagra_build_ref_ex(_p(base), n, d, int(graph_degree), _p(out), int(threads), int(exact_limit),
+                                         int(pq_limit))
     if rc == 2:
-        raise ValueError("the reference's N > 200,000 build path is not restated")
+        raise ValueError("product-quantised seeding needs d >= 1024")
     if rc != 0:
         raise ValueError("invalid arguments")
     return out
+
+
+def pq_train(base, threads: int = 1):
+    """Product quantisation of the build's PQ path (src/metal_context.mm:
+    437-568): returns (codes n x 8 uint8, lut 8 x 256 x 256 float32)."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    if d < 1024:
+        raise ValueError("product quantisation reads 8 x 128 dimensions")
+    codes = np.empty((n, 8), np.uint8)
+    lut = np.empty((8, 256, 256), np.float32)
+    lib().oracle_pq_train(_p(base), n, d, int(threads), _p(codes), _p(lut))
+    return codes, lut

@@ -1,8 +1,9 @@
 /*
  * CPU restatement of the reference's CAGRA graph build (TEST INFRASTRUCTURE
  * ONLY; see oracle.h): cagra::build (src/cagra.cpp:47-59) ->
- * MetalContext::build_knn_graph (src/metal_context.mm:289-914) for
- * N <= 200,000.  Compiled with -ffp-contract=off.
+ * MetalContext::build_knn_graph (src/metal_context.mm:289-914), all three
+ * size classes (exact seeding, IVF seeding with exact distances, IVF seeding
+ * with product-quantisation distances).  Compiled with -ffp-contract=off.
  *
  * Where the reference's arithmetic order is unspecified (cblas_sgemm cross
  * products, Metal's float4 dot), a fixed order is chosen and stated.  The
@@ -102,14 +103,98 @@ static void select_smallest(uint32_t* idx, int64_t m, int64_t take, const float*
   }
 }
 
+/* Product quantisation of the rows (src/metal_context.mm:437-568): for each
+ * of 8 subspaces of 128 dimensions, k-means with 256 centres from evenly
+ * strided rows, at most 10 iterations (stop when no row changes centre),
+ * then one more assignment pass as the codes; and the symmetric table
+ * lut[m][a][b] = sum over the subspace of (c_a - c_b)^2 in dimension order
+ * (:552-566). */
+void oracle_pq_train(const float* data, int64_t n, int64_t d, int nt, uint8_t* codes, float* lut) {
+  enum { M = 8, DS = 128, KC = 256 };
+  float* ctr = (float*)malloc(sizeof(float) * KC * DS);
+  float* cn = (float*)malloc(sizeof(float) * KC);
+  float* vn = (float*)malloc(sizeof(float) * (size_t)n);
+  int32_t* asg = (int32_t*)calloc((size_t)n, sizeof(int32_t));
+  int64_t* counts = (int64_t*)malloc(sizeof(int64_t) * KC);
+  for (int m = 0; m < M; ++m) {
+    const int64_t off = (int64_t)m * DS;
+    const double stride = (double)n / KC;
+    for (int c = 0; c < KC; ++c) {
+      int64_t ix = (int64_t)((double)c * stride + stride * 0.5);
+      if (ix > n - 1) ix = n - 1;
+      memcpy(ctr + c * DS, data + ix * d + off, sizeof(float) * DS);
+    }
+    for (int64_t i = 0; i < n; ++i) vn[i] = sq_norm(data + i * d + off, DS);
+    for (int iter = 0; iter <= 10; ++iter) {
+      /* iterations 0..9 are Lloyd steps; pass 10 (or the pass after the
+       * loop stopped) is the encoding E-step with the final centres */
+      for (int c = 0; c < KC; ++c) cn[c] = sq_norm(ctr + c * DS, DS);
+      int changed = iter == 0;
+#pragma omp parallel for schedule(static) num_threads(nt) reduction(| : changed)
+      for (int64_t i = 0; i < n; ++i) {
+        float best = INFINITY;
+        int32_t bc = 0;
+        for (int c = 0; c < KC; ++c) {
+          const float dd = vn[i] - 2.f * dot_blk(data + i * d + off, ctr + c * DS, DS) + cn[c];
+          if (dd < best) {
+            best = dd;
+            bc = c;
+          }
+        }
+        if (asg[i] != bc) {
+          changed = 1;
+          asg[i] = bc;
+        }
+        codes[i * M + m] = (uint8_t)bc;
+      }
+      if (iter == 10 || !changed) break;
+      memset(ctr, 0, sizeof(float) * KC * DS);
+      memset(counts, 0, sizeof(int64_t) * KC);
+      for (int64_t i = 0; i < n; ++i) {
+        counts[asg[i]]++;
+        float* c = ctr + asg[i] * DS;
+        const float* x = data + i * d + off;
+        for (int j = 0; j < DS; ++j) c[j] += x[j];
+      }
+      for (int c = 0; c < KC; ++c)
+        if (counts[c] > 0) {
+          const float inv = 1.0f / (float)counts[c];
+          for (int j = 0; j < DS; ++j) ctr[c * DS + j] *= inv;
+        }
+    }
+    for (int a = 0; a < KC; ++a)
+      for (int b = a; b < KC; ++b) {
+        float s2 = 0.f;
+        for (int j = 0; j < DS; ++j) {
+          const float df = ctr[a * DS + j] - ctr[b * DS + j];
+          s2 += df * df;
+        }
+        lut[((int64_t)m * KC + a) * KC + b] = s2;
+        lut[((int64_t)m * KC + b) * KC + a] = s2;
+      }
+  }
+  free(ctr);
+  free(cn);
+  free(vn);
+  free(asg);
+  free(counts);
+}
+
 int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
                            uint32_t* out_graph, int threads) {
-  if (!data || !out_graph || n <= 0 || d <= 0) return 1;
-  if (n > 200000) return 2; /* the N > 200,000 PQ path is not restated */
+  return oracle_cagra_build_ref_ex(data, n, d, graph_degree, out_graph, threads, 50000, 200000);
+}
+
+int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
+                              uint32_t* out_graph, int threads, int64_t exact_limit, int64_t pq_limit) {
+  if (!data || !out_graph || n <= 0 || d <= 0 || exact_limit < 0 || pq_limit < 0) return 1;
+  /* N > pq_limit: product-quantised seeding over 8 x 128 dimensions */
+  const int pq = n > exact_limit && n > pq_limit;
+  if (pq && d < 1024) return 2;
   const int nt = threads > 0 ? threads : 1;
   /* src/cagra.cpp:47-59 */
   const uint32_t g = graph_degree < (uint32_t)(n - 1) ? graph_degree : (uint32_t)(n - 1);
-  const uint32_t nd_iters = n <= 50000 ? 20u : (n <= 200000 ? 5u : 0u);
+  const uint32_t nd_iters = n <= exact_limit ? 20u : (n <= pq_limit ? 5u : 0u);
   if (g == 0) return 0;
 
   uint32_t* graph = out_graph;
@@ -121,7 +206,7 @@ int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t gra
   }
   for (int64_t i = 0; i < n; ++i) norms[i] = sq_norm(data + i * d, d);
 
-  if (n <= 50000) {
+  if (n <= exact_limit) {
     /* Exact all-pairs seeding (:324-349), one row at a time. */
 #pragma omp parallel num_threads(nt)
     {
@@ -221,7 +306,15 @@ int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t gra
       free(key);
       free(kidx);
     }
-    /* Exact per-cluster seeding (:712-792). */
+    /* Per-cluster seeding: exact distances (:712-792), or PQ table sums
+     * (:614-681) followed by exact distances of every kept entry (:683-709). */
+    uint8_t* codes = NULL;
+    float* lut = NULL;
+    if (pq) {
+      codes = (uint8_t*)malloc((size_t)n * 8);
+      lut = (float*)malloc(sizeof(float) * 8 * 256 * 256);
+      oracle_pq_train(data, n, d, nt, codes, lut);
+    }
     const int64_t max_own = (n / K) * 4 + 64;
 #pragma omp parallel num_threads(nt)
     {
@@ -246,9 +339,17 @@ int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t gra
           const uint32_t vi = own[i];
           const float ni = norms[vi];
           for (int64_t p = 0; p < m; ++p) {
-            key[p] = probe[p] == vi ? INFINITY
-                                    : ni - 2.f * dot_blk(data + (int64_t)vi * d, data + (int64_t)probe[p] * d, d) +
-                                          norms[probe[p]];
+            if (probe[p] == vi) {
+              key[p] = INFINITY;
+            } else if (pq) {
+              const uint8_t* ca = codes + (int64_t)vi * 8;
+              const uint8_t* cb = codes + (int64_t)probe[p] * 8;
+              float s2 = 0.f;
+              for (int sm = 0; sm < 8; ++sm) s2 += lut[((int64_t)sm * 256 + ca[sm]) * 256 + cb[sm]];
+              key[p] = s2;
+            } else {
+              key[p] = ni - 2.f * dot_blk(data + (int64_t)vi * d, data + (int64_t)probe[p] * d, d) + norms[probe[p]];
+            }
             midx[p] = (uint32_t)p;
           }
           select_smallest(midx, m, take, key);
@@ -262,6 +363,19 @@ int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t gra
       free(probe);
       free(key);
       free(midx);
+    }
+    if (pq) {
+      /* Exact squared L2 of every entry (recompute_graph_distances,
+       * shaders/cagra_kernels.metal:658-681: float4 partial sums over
+       * 4 floor(d / 4) dimensions; entries that are not row ids get +inf). */
+#pragma omp parallel for schedule(static) num_threads(nt)
+      for (int64_t i = 0; i < n; ++i)
+        for (uint32_t e = 0; e < g; ++e) {
+          const uint32_t nb = graph[i * g + e];
+          gdist[i * g + e] = nb < (uint32_t)n ? l2_f4(data + i * d, data + (int64_t)nb * d, d) : INFINITY;
+        }
+      free(codes);
+      free(lut);
     }
     free(cent);
     free(assign);

@@ -101,14 +101,31 @@ void oracle_knn_graph(const float* base, int64_t n, int64_t d, uint32_t g, uint3
  * iterations.  Writes n x G ids (UINT32_MAX for missing).  Cross products use
  * a fixed 8-way summation where the reference calls cblas_sgemm; nn-descent
  * reads other nodes' lists as of the start of each iteration (one legal
- * schedule of the reference's racy kernel).  Returns 0, 1 on bad arguments,
- * 2 for n > 200,000 (the PQ path is not restated).  Pinned: equals the exact
+ * schedule of the reference's racy kernel).  For n > 200,000 the per-cluster
+ * seeding ranks candidates by product-quantisation table sums
+ * (src/metal_context.mm:437-568, :614-681; 8 subspaces of 128 dimensions,
+ * 256 centres) and re-scores the kept entries exactly (:683-709), with no
+ * nn-descent.  Returns 0, 1 on bad arguments, 2 when the PQ path meets
+ * d < 1024.  Pinned: equals the exact
  * kNN graph on integer data through the exact-seeding path; on the IVF path,
  * rows are full, in range, free of self edges and hold most exact neighbours
  * (tests/test_oracle_build.py).  Bit-exact graphs are parity unpinned (the
  * reference's own result depends on a GPU race and on BLAS order). */
 int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
                            uint32_t* out_graph, int threads);
+
+/* oracle_cagra_build_ref with the size limits as arguments (exact seeding
+ * for n <= exact_limit, PQ seeding for n > max(exact_limit, pq_limit); the
+ * reference's limits are 50,000 and 200,000), so that tests can run the
+ * large-N phases at small n.  The PQ seeding is pinned by its equivalence
+ * with exact per-cluster seeding over the rows rebuilt from their codes
+ * (tests/test_oracle_build.py). */
+int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
+                              uint32_t* out_graph, int threads, int64_t exact_limit, int64_t pq_limit);
+
+/* The product-quantisation training of the build's PQ path, exposed for its
+ * pinning tests: codes n x 8 (uint8), lut 8 x 256 x 256. */
+void oracle_pq_train(const float* data, int64_t n, int64_t d, int threads, uint8_t* codes, float* lut);
 
 #ifdef __cplusplus
 }

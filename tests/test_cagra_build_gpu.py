@@ -171,3 +171,38 @@ def test_reference_build_matches_oracle(ctx, cvs, oracle, n, d, g):
         assert 1 <= st["descent_iterations"] <= 5
     assert q_gpu >= q_ref - 0.02
     assert r_gpu >= r_ref - 0.02
+
+
+@pytest.mark.gpu
+def test_reference_pq_build_matches_oracle(ctx, cvs, oracle):
+    """The reference's N > 200,000 build (product-quantised per-cluster
+    seeding, src/metal_context.mm:437-709; no nn-descent, src/cagra.cpp:59),
+    run at n = 6,000 through the size-limit arguments, against the oracle's
+    restatement.  The GPU ranks candidates by the squared distance of the rows
+    rebuilt from their codes, the oracle by summing the symmetric PQ table
+    (two formulations of the same distance), so graphs agree up to fp32 ties:
+    neighbour recall and the restated reference search recall within 0.03."""
+    n, d, g = 6000, 1024, 32
+    base = cvs.synth_clustered(77, cvs.STREAM_BASE, n, d)
+    qs = cvs.synth_clustered(77, cvs.STREAM_QUERIES, 300, d)
+    print(f"reference PQ build n={n} d={d} g={g} on the GPU", flush=True)
+    graph, st = ctx.cagra_build_reference(base, g, exact_limit=0, pq_limit=0)
+    check_graph(graph, n, g)
+    ref = oracle.cagra_build_reference(base, g, threads=16, exact_limit=0, pq_limit=0)
+    sample = np.random.default_rng(2).choice(n, 500, replace=False)
+    gt_rows, _ = oracle.bf_exact(base, base[sample], 11, threads=16)
+    exact = np.stack([r[r != s][:10] for r, s in zip(gt_rows, sample)])
+    q_gpu = neighbour_recall(graph[sample], exact, 10)
+    q_ref = neighbour_recall(ref[sample], exact, 10)
+    nav = oracle.cagra_nav_nodes(n)
+    gt, _ = oracle.bf_exact(base, qs, 10, threads=16)
+    s_gpu, _ = oracle.cagra_reference_search(base, graph, nav, qs, 10, itopk_size=64, threads=16)
+    s_ref, _ = oracle.cagra_reference_search(base, ref, nav, qs, 10, itopk_size=64, threads=16)
+    r_gpu, r_ref = recall(s_gpu, gt, 10), recall(s_ref, gt, 10)
+    print(f"stats {st}; neighbour recall@10 gpu {q_gpu:.4f} oracle {q_ref:.4f}; "
+          f"search recall gpu graph {r_gpu:.4f} oracle graph {r_ref:.4f}")
+    assert st["descent_iterations"] == 0 and 8 <= st["pq_iterations"] <= 80
+    assert q_gpu >= q_ref - 0.03
+    assert r_gpu >= r_ref - 0.03
+    with pytest.raises(ValueError):  # CVS_ERR_UNSUPPORTED: the PQ path needs d = 1024
+        ctx.cagra_build_reference(base[:, :512], g, exact_limit=0, pq_limit=0)

@@ -8,7 +8,13 @@ oracle/cagra_build_oracle.c; reference src/metal_context.mm:289-914).
 - IVF path (50,000 < n <= 200,000): rows full, ids in range, no self edges
   (the reference allows repeated ids from its bucketing merge, so repeats are
   only counted), and most exact neighbours present.
-- n > 200,000 is refused (the PQ path is not restated).
+- PQ path (n > 200,000; run here at small n through the size-limit
+  arguments): the product quantisation (:437-568) is pinned in closed form
+  on data whose 128-dimension slices are drawn from 256 dyadic prototypes
+  per subspace laid out so that the evenly strided initial centres are
+  exactly the prototypes: k-means converges at once, every code is known,
+  and every table entry is an exact fp32 sum.  The PQ seeding graph is in
+  range and free of self edges; d < 1024 is refused.
 """
 import numpy as np
 import pytest
@@ -64,6 +70,58 @@ def test_ivf_path_quality(oracle):
     assert share > 0.9
 
 
-def test_refuses_pq_path(oracle):
+def test_pq_path_needs_d1024(oracle):
+    """The PQ path reads 8 subspaces of 128 dimensions of every row."""
     with pytest.raises(ValueError):
         oracle.cagra_build_reference(np.zeros((200_001, 1), np.float32), 8)
+    with pytest.raises(ValueError):
+        oracle.cagra_build_reference(np.zeros((100, 512), np.float32), 8, exact_limit=0, pq_limit=0)
+
+
+def prototype_rows(seed=3):
+    """2048 rows of d = 1024.  Subspace m of row i = 8 c + j holds prototype
+    (c + m j) mod 256 of that subspace (256 random multiples of 1/16 in
+    [-2, 2]), so each prototype fills exactly 8 rows of each subspace and the
+    evenly strided rows 8 c + 4 that seed the centres hold prototypes
+    (c + 4 m) mod 256: all 256, once each."""
+    rng = np.random.default_rng(seed)
+    protos = rng.integers(-32, 33, size=(8, 256, 128)).astype(np.float32) / 16.0
+    i = np.arange(2048)
+    c, j = i // 8, i % 8
+    base = np.empty((2048, 1024), np.float32)
+    for m in range(8):
+        base[:, 128 * m:128 * (m + 1)] = protos[m][(c + m * j) % 256]
+    return base, protos
+
+
+def test_pq_train_closed_form(oracle):
+    """Centres start as the prototypes (centre c = prototype (c + 4 m) mod
+    256), every row sits at distance 0 from its own, and each centre's mean
+    of 8 identical dyadic slices is that slice exactly, so k-means stops after
+    one step: code of row 8 c + j in subspace m = (c + m (j - 4)) mod 256, and
+    lut[m][a][b] = |P_m[(a + 4m) % 256] - P_m[(b + 4m) % 256]|^2 exactly."""
+    base, protos = prototype_rows()
+    codes, lut = oracle.pq_train(base, threads=4)
+    i = np.arange(2048)
+    c, j = i // 8, i % 8
+    for m in range(8):
+        assert (codes[:, m] == (c + m * (j - 4)) % 256).all(), m
+        p = protos[m][(np.arange(256) + 4 * m) % 256].astype(np.float64)
+        want = ((p[:, None, :] - p[None, :, :]) ** 2).sum(-1)
+        assert np.array_equal(lut[m].astype(np.float64), want), m
+
+
+def test_pq_path_graph(oracle, cvs):
+    """The PQ seeding (k-means clusters, candidates of the own and 3 nearest
+    clusters ranked by table sums, exact distances of the kept entries,
+    bucketing, no nn-descent) on clustered data: full rows of in-range ids,
+    no self edges, and neighbours well above chance."""
+    n, g = 3000, 16
+    base = cvs.synth_clustered(11, cvs.STREAM_BASE, n, 1024)
+    gr = oracle.cagra_build_reference(base, g, threads=8, exact_limit=0, pq_limit=0)
+    assert gr.shape == (n, g) and (gr < n).all()
+    assert not (gr == np.arange(n, dtype=np.uint32)[:, None]).any()
+    exact = oracle.knn_graph(base, 10, threads=8)
+    share = np.mean([len(set(exact[i].tolist()) & set(gr[i].tolist())) / 10 for i in range(0, n, 7)])
+    print(f"PQ path: share of exact 10-NN {share:.3f}")
+    assert share > 0.3
