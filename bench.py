@@ -106,6 +106,36 @@ def read_traffic(name: str):
     return None
 
 
+def calibrate_mfma() -> int:
+    """The matrix-core rate this device sustains on a plain fp16 GEMM from
+    the vendor library (torch.matmul -> hipBLASLt), fp32 accumulate, at the
+    brute-force scan's inner dimension (M = 10,240 queries, N = 65,536 rows,
+    K = 1,024) and at a square 8,192 shape.  A reference point next to the
+    fused scan's fraction of the nominal 2.5 PFLOP/s (clocks drop under
+    sustained matrix load)."""
+    import torch
+
+    out = {}
+    for name, (m, n_, k) in {"scan_shape": (10240, 65536, 1024), "square_8192": (8192, 8192, 8192)}.items():
+        a = torch.randn(m, k, device="cuda:0", dtype=torch.float16)
+        b = torch.randn(n_, k, device="cuda:0", dtype=torch.float16).t().contiguous()
+        for _ in range(3):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        start.record()
+        for _ in range(reps):
+            torch.matmul(a, b)
+        end.record()
+        torch.cuda.synchronize()
+        tflops = 2.0 * m * n_ * k * reps / (start.elapsed_time(end) * 1e-3) / 1e12
+        out[name] = {"m": m, "n": n_, "k": k, "tflops": tflops, "frac_of_nominal": tflops / MFMA_F16_PEAK_TFLOPS}
+        del a, b
+    print(json.dumps({"calibrate_mfma_fp16_gemm": out}), flush=True)
+    return 0
+
+
 def calibrate_copy(mib: int) -> int:
     """Copies `mib` MiB device-to-device with torch's copy_, which the HIP
     runtime serves with its blit kernel `__amd_rocclr_copyBuffer` (reads mib
@@ -156,6 +186,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=12, help="queries timed on the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--calibrate-mfma", action="store_true",
+                    help="time a plain fp16 GEMM from the vendor library (matrix-core reference point)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (PMC byte-counter calibration)")
     ap.add_argument("--workload", choices=["bf", "bf-large", "cagra-search", "cagra-build"], default="bf",
@@ -168,6 +200,8 @@ def main() -> int:
 
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.calibrate_mfma:
+        return calibrate_mfma()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
               "how the search would shard over several GPUs is described in the design notes, "
