@@ -200,17 +200,21 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
   const int last = n_chunks - 1;
   const char* a_base = s_stage + (lane & 31) * STRIDE + 16 * (lane >> 5);
   const char* b_base = a_base + 32 * wave * STRIDE;
-  u32x4 reg[LPT];
+  // Two register sets: chunk c + 2 is gathered while chunk c is multiplied,
+  // so each gather has two chunks of work to arrive in.
+  u32x4 reg0[LPT], reg1[LPT];
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) reg[i] = *reinterpret_cast<const u32x4*>(src[i]);
-  for (int c = 0; c < n_chunks; ++c) {
+  for (int i = 0; i < LPT; ++i) reg0[i] = *reinterpret_cast<const u32x4*>(src[i]);
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) reg1[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(1, last)) * CB);
+  auto step = [&](u32x4 (&reg)[LPT], int c) __attribute__((always_inline)) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[i];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < LPT; ++i)
-      reg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + 1, last)) * CB);
+      reg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + 2, last)) * CB);
     if (live) {
 #pragma unroll
       for (int s = 0; s < CB / 32; ++s) {
@@ -222,7 +226,13 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
         for (int t = 0; t < R; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], b, acc[t], 0, 0, 0);
       }
     }
+  };
+  int c = 0;
+  for (; c + 1 < n_chunks; c += 2) {
+    step(reg0, c);
+    step(reg1, c + 1);
   }
+  if (c < n_chunks) step(reg0, c);
 }
 
 // fp32 rows -> fp16 rows (stride dp) + squared norms of the fp16-rounded rows.
