@@ -200,21 +200,24 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
   const int last = n_chunks - 1;
   const char* a_base = s_stage + (lane & 31) * STRIDE + 16 * (lane >> 5);
   const char* b_base = a_base + 32 * wave * STRIDE;
-  // Two register sets: chunk c + 2 is gathered while chunk c is multiplied,
-  // so each gather has two chunks of work to arrive in.
-  u32x4 reg0[LPT], reg1[LPT];
+  // NS register sets: chunk c + NS is gathered while chunk c is multiplied,
+  // so each gather has NS chunks of work to arrive in (four for the small
+  // neighbourhoods that dominate once the lists settle, two for the largest,
+  // whose registers bound the kernel's occupancy).
+  constexpr int NS = R <= 2 ? 4 : 2;
+  u32x4 reg[NS][LPT];
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) reg0[i] = *reinterpret_cast<const u32x4*>(src[i]);
+  for (int k = 0; k < NS; ++k)
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) reg1[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(1, last)) * CB);
-  auto step = [&](u32x4 (&reg)[LPT], int c) __attribute__((always_inline)) {
+    for (int i = 0; i < LPT; ++i) reg[k][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(k, last)) * CB);
+  auto step = [&](u32x4 (&rg)[LPT], int c) __attribute__((always_inline)) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = reg[i];
+    for (int i = 0; i < LPT; ++i) *reinterpret_cast<u32x4*>(s_stage + dst[i]) = rg[i];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < LPT; ++i)
-      reg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + 2, last)) * CB);
+      rg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + NS, last)) * CB);
     if (live) {
 #pragma unroll
       for (int s = 0; s < CB / 32; ++s) {
@@ -228,11 +231,13 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
     }
   };
   int c = 0;
-  for (; c + 1 < n_chunks; c += 2) {
-    step(reg0, c);
-    step(reg1, c + 1);
+  for (; c + NS <= n_chunks; c += NS) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) step(reg[k], c + k);
   }
-  if (c < n_chunks) step(reg0, c);
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    if (c + k < n_chunks) step(reg[k], c + k);
 }
 
 // fp32 rows -> fp16 rows (stride dp) + squared norms of the fp16-rounded rows.
