@@ -101,6 +101,8 @@ class BuildStats(ctypes.Structure):
 _SIGNATURES["cvs_cagra_build"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_uint32, c_uint32,
                                           c_float, c_uint64, c_void_p, c_int, POINTER(BuildStats)])
 
+_SIGNATURES["cvs_cagra_nav_nodes"] = (c_int, [c_int64, c_void_p, POINTER(c_int64)])
+
 # The bucketing permutation seed of the reference (src/metal_context.mm:803).
 DEFAULT_BUILD_SEED = 0xFEDCBA9876543210
 
@@ -141,6 +143,16 @@ def _check(status: int) -> None:
     if status in (CVS_ERR_INVALID_ARGUMENT, CVS_ERR_UNSUPPORTED):
         raise ValueError(msg)
     raise RuntimeError(f"cvs error {status}: {msg}")
+
+
+def cagra_nav_nodes(n: int) -> np.ndarray:
+    """Navigation (seed) node ids of an n-row graph index, as the
+    reference's cagra::build picks them (src/cagra.cpp:63-72)."""
+    cnt = c_int64(0)
+    _check(load().cvs_cagra_nav_nodes(int(n), None, byref(cnt)))
+    out = np.empty(cnt.value, np.uint32)
+    _check(load().cvs_cagra_nav_nodes(int(n), out.ctypes.data_as(c_void_p), byref(cnt)))
+    return out
 
 
 def device_count() -> int:

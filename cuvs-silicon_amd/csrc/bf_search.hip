@@ -1051,37 +1051,41 @@ int choose_kp(int64_t k) {
 }
 
 template <int KS, int KP>
-void launch_scan_kp(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode) {
+void launch_scan_kp(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode, hipEvent_t e0, hipEvent_t e1) {
   if (mode == kModeScan)
-    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeScan, KP>), grid, dim3(kThreads), 0, ctx->stream, args);
+    hipExtLaunchKernelGGL((bf_scan_kernel<KS, kModeScan, KP>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0,
+                          args);
   else
-    hipLaunchKernelGGL((bf_scan_kernel<KS, kModeSample, KP>), grid, dim3(kThreads), 0, ctx->stream,
-                       args);
+    hipExtLaunchKernelGGL((bf_scan_kernel<KS, kModeSample, KP>), grid, dim3(kThreads), 0, ctx->stream, e0, e1, 0,
+                          args);
 }
 
 template <int KS>
-void launch_scan_ks(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode) {
+void launch_scan_ks(cvs_context* ctx, dim3 grid, const ScanArgs& args, int mode, hipEvent_t e0, hipEvent_t e1) {
   if (mode == kModeSample) {
-    launch_scan_kp<KS, 16>(ctx, grid, args, mode);  // list geometry unused when sampling
+    launch_scan_kp<KS, 16>(ctx, grid, args, mode, e0, e1);  // list geometry unused when sampling
     return;
   }
   switch (args.kp) {
-    case 16: launch_scan_kp<KS, 16>(ctx, grid, args, mode); break;
-    case 32: launch_scan_kp<KS, 32>(ctx, grid, args, mode); break;
-    case 64: launch_scan_kp<KS, 64>(ctx, grid, args, mode); break;
-    case 128: launch_scan_kp<KS, 128>(ctx, grid, args, mode); break;
+    case 16: launch_scan_kp<KS, 16>(ctx, grid, args, mode, e0, e1); break;
+    case 32: launch_scan_kp<KS, 32>(ctx, grid, args, mode, e0, e1); break;
+    case 64: launch_scan_kp<KS, 64>(ctx, grid, args, mode, e0, e1); break;
+    case 128: launch_scan_kp<KS, 128>(ctx, grid, args, mode, e0, e1); break;
     default: fail(CVS_ERR_RUNTIME, "unsupported candidate count");
   }
 }
 
-void launch_scan(cvs_context* ctx, int ks, dim3 grid, const ScanArgs& args, int mode) {
+// Launches the scan kernel in `mode`; e0 / e1 (may be null) record the
+// dispatch's start / end for the timing facility.
+void launch_scan(cvs_context* ctx, int ks, dim3 grid, const ScanArgs& args, int mode, hipEvent_t e0 = nullptr,
+                 hipEvent_t e1 = nullptr) {
   switch (ks) {
-    case 2: launch_scan_ks<2>(ctx, grid, args, mode); break;
-    case 4: launch_scan_ks<4>(ctx, grid, args, mode); break;
-    case 8: launch_scan_ks<8>(ctx, grid, args, mode); break;
-    case 16: launch_scan_ks<16>(ctx, grid, args, mode); break;
-    case 32: launch_scan_ks<32>(ctx, grid, args, mode); break;
-    case 64: launch_scan_ks<64>(ctx, grid, args, mode); break;
+    case 2: launch_scan_ks<2>(ctx, grid, args, mode, e0, e1); break;
+    case 4: launch_scan_ks<4>(ctx, grid, args, mode, e0, e1); break;
+    case 8: launch_scan_ks<8>(ctx, grid, args, mode, e0, e1); break;
+    case 16: launch_scan_ks<16>(ctx, grid, args, mode, e0, e1); break;
+    case 32: launch_scan_ks<32>(ctx, grid, args, mode, e0, e1); break;
+    case 64: launch_scan_ks<64>(ctx, grid, args, mode, e0, e1); break;
     default: fail(CVS_ERR_UNSUPPORTED, "unsupported padded dimension");
   }
   after_launch(mode == kModeScan ? "bf_scan_kernel" : "bf_sample_kernel");
@@ -1168,39 +1172,35 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   args.n_qblocks = int(qblocks);
   const unsigned wave_blocks = unsigned((q + kWaves - 1) / kWaves);
 
-  hipEvent_t t0 = timer_begin(ctx, "bf_prep");
-  hipLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((q_tiles * 32 + kWaves - 1) / kWaves)), dim3(kThreads), 0,
-                     ctx->stream, queries, q, ds->d, ks, q_tiles * 32, qtiles, qnorms);
+  const TimerSpan t0 = timer_span(ctx, "bf_prep");
+  hipExtLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((q_tiles * 32 + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                        ctx->stream, t0.start, t0.stop, 0, queries, q, ds->d, ks, q_tiles * 32, qtiles, qnorms);
   after_launch("query_tiles_kernel");
-  timer_end(ctx, "bf_prep", t0);
 
-  hipEvent_t t1 = timer_begin(ctx, "bf_sample");
+  const TimerSpan t1 = timer_span(ctx, "bf_sample");
   args.n_ranges = Gs;
   args.qb_fast = 0;
-  launch_scan(ctx, ks, dim3(unsigned(Gs), qblocks), args, kModeSample);
-  hipLaunchKernelGGL(bf_select_kernel, dim3(wave_blocks), dim3(kThreads), 0, ctx->stream,
-                     static_cast<const float*>(sgmin), m_min, kp, int(q), thr0);
+  launch_scan(ctx, ks, dim3(unsigned(Gs), qblocks), args, kModeSample, t1.start, nullptr);
+  hipExtLaunchKernelGGL(bf_select_kernel, dim3(wave_blocks), dim3(kThreads), 0, ctx->stream, nullptr, t1.stop, 0,
+                        static_cast<const float*>(sgmin), m_min, kp, int(q), thr0);
   after_launch("bf_select_kernel");
-  timer_end(ctx, "bf_sample", t1);
 
-  hipEvent_t t2 = timer_begin(ctx, "bf_scan");
+  const TimerSpan t2 = timer_span(ctx, "bf_scan");
   args.n_ranges = G;
   args.qb_fast = large_batch ? 1 : 0;
   launch_scan(ctx, ks, large_batch ? dim3(unsigned(G) * qblocks, 1) : dim3(unsigned(G), qblocks), args,
-              kModeScan);
-  timer_end(ctx, "bf_scan", t2);
+              kModeScan, t2.start, t2.stop);
 
-  hipEvent_t t3 = timer_begin(ctx, "bf_merge");
+  const TimerSpan t3 = timer_span(ctx, "bf_merge");
   if (kp <= 64)
-    hipLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
-                       static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp,
-                       static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
+    hipExtLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
+                          t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp,
+                          static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   else
-    hipLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream,
-                       static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, stride,
-                       static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
+    hipExtLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start, t3.stop,
+                          0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, stride,
+                          static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   after_launch("bf_merge_kernel");
-  timer_end(ctx, "bf_merge", t3);
 }
 
 }  // namespace

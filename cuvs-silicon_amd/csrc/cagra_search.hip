@@ -445,21 +445,23 @@ int waves_per_query(int64_t q) {
 }
 
 template <int E, bool F16>
-void launch_search(int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a) {
+void launch_search(int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a, hipEvent_t e0,
+                   hipEvent_t e1) {
   switch (waves) {
-    case 1: hipLaunchKernelGGL((cagra_search_kernel<E, 1, F16>), grid, dim3(64), lds, stream, a); break;
-    case 2: hipLaunchKernelGGL((cagra_search_kernel<E, 2, F16>), grid, dim3(128), lds, stream, a); break;
-    case 4: hipLaunchKernelGGL((cagra_search_kernel<E, 4, F16>), grid, dim3(256), lds, stream, a); break;
-    default: hipLaunchKernelGGL((cagra_search_kernel<E, 8, F16>), grid, dim3(512), lds, stream, a); break;
+    case 1: hipExtLaunchKernelGGL((cagra_search_kernel<E, 1, F16>), grid, dim3(64), lds, stream, e0, e1, 0, a); break;
+    case 2: hipExtLaunchKernelGGL((cagra_search_kernel<E, 2, F16>), grid, dim3(128), lds, stream, e0, e1, 0, a); break;
+    case 4: hipExtLaunchKernelGGL((cagra_search_kernel<E, 4, F16>), grid, dim3(256), lds, stream, e0, e1, 0, a); break;
+    default: hipExtLaunchKernelGGL((cagra_search_kernel<E, 8, F16>), grid, dim3(512), lds, stream, e0, e1, 0, a); break;
   }
 }
 
 template <int E>
-void launch_search(bool f16, int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a) {
+void launch_search(bool f16, int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a,
+                   hipEvent_t e0, hipEvent_t e1) {
   if (f16)
-    launch_search<E, true>(waves, grid, lds, stream, a);
+    launch_search<E, true>(waves, grid, lds, stream, a, e0, e1);
   else
-    launch_search<E, false>(waves, grid, lds, stream, a);
+    launch_search<E, false>(waves, grid, lds, stream, a, e0, e1);
 }
 
 // Merge of the teams' lists of one query (one wave per query): the teams x
@@ -632,31 +634,33 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
     a.stats = nullptr;
   }
 
-  hipEvent_t t0 = timer_begin(ctx, "cagra_search");
+  const TimerSpan t0 = timer_span(ctx, "cagra_search");
   const dim3 grid(static_cast<unsigned>(q * teams));
   const int waves = waves_per_query(q * teams);
   const bool f16 = idx->traversal_bits == 16;
+  // The search kernel starts the span; the team merge (if any) ends it.
+  hipEvent_t e1 = teams > 1 ? nullptr : t0.stop;
   switch (e_slots) {
-    case 1: launch_search<1>(f16, waves, grid, lds, ctx->stream, a); break;
-    case 2: launch_search<2>(f16, waves, grid, lds, ctx->stream, a); break;
-    case 4: launch_search<4>(f16, waves, grid, lds, ctx->stream, a); break;
-    default: launch_search<8>(f16, waves, grid, lds, ctx->stream, a); break;
+    case 1: launch_search<1>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
+    case 2: launch_search<2>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
+    case 4: launch_search<4>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
+    default: launch_search<8>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
   }
   after_launch("cagra_search_kernel");
   if (teams > 1) {
     const int total = int(teams * itopk);
     const uint64_t* keys = a.team_keys;
+    const dim3 mg{unsigned(q)}, mb{64};
     if (total <= 64)
-      hipLaunchKernelGGL(team_merge_kernel<1>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+      hipExtLaunchKernelGGL(team_merge_kernel<1>, mg, mb, 0, ctx->stream, nullptr, t0.stop, 0, keys, total, int(k), nbr, dist);
     else if (total <= 128)
-      hipLaunchKernelGGL(team_merge_kernel<2>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+      hipExtLaunchKernelGGL(team_merge_kernel<2>, mg, mb, 0, ctx->stream, nullptr, t0.stop, 0, keys, total, int(k), nbr, dist);
     else if (total <= 256)
-      hipLaunchKernelGGL(team_merge_kernel<4>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+      hipExtLaunchKernelGGL(team_merge_kernel<4>, mg, mb, 0, ctx->stream, nullptr, t0.stop, 0, keys, total, int(k), nbr, dist);
     else
-      hipLaunchKernelGGL(team_merge_kernel<8>, dim3(unsigned(q)), dim3(64), 0, ctx->stream, keys, total, int(k), nbr, dist);
+      hipExtLaunchKernelGGL(team_merge_kernel<8>, mg, mb, 0, ctx->stream, nullptr, t0.stop, 0, keys, total, int(k), nbr, dist);
     after_launch("team_merge_kernel");
   }
-  timer_end(ctx, "cagra_search", t0);
 }
 
 }  // namespace
@@ -665,6 +669,23 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
 using namespace cvs;
 
 extern "C" {
+
+int cvs_cagra_nav_nodes(int64_t n, uint32_t* out_ids, int64_t* out_count) {
+  return guarded([&] {
+    if (!out_count) fail(CVS_ERR_INVALID_ARGUMENT, "null out_count");
+    if (n <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "row count must be positive");
+    if (n > int64_t(UINT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "row ids must fit in uint32");
+    // min(200, floor(sqrt(n))) rows, row i at floor(i * (n / n_nav)) with the
+    // spacing taken in double (src/cagra.cpp:65-72).
+    int64_t n_nav = static_cast<int64_t>(std::sqrt(static_cast<double>(n)));
+    if (n_nav > 200) n_nav = 200;
+    *out_count = n_nav;
+    if (out_ids) {
+      const double step = static_cast<double>(n) / static_cast<double>(n_nav);
+      for (int64_t i = 0; i < n_nav; ++i) out_ids[i] = static_cast<uint32_t>(static_cast<double>(i) * step);
+    }
+  });
+}
 
 int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
                            int rows_on_device, const uint32_t* graph, uint32_t degree,
@@ -744,12 +765,12 @@ int cvs_cagra_index_edge_distances(cvs_context* ctx, const cvs_cagra_index* inde
       ctx->ws_io.reserve(count * sizeof(float));
       dst = ctx->ws_io.as<float>();
     }
-    hipEvent_t t0 = timer_begin(ctx, "cagra_edge_distances");
-    hipLaunchKernelGGL(edge_distances_kernel, dim3(unsigned(index->n)), dim3(256), 0, ctx->stream,
-                       reinterpret_cast<const float4*>(index->rows), int(index->dpad / 4), int(index->dpad / 64),
-                       static_cast<const uint32_t*>(index->graph), int(index->degree), uint32_t(index->n), dst);
+    const TimerSpan t0 = timer_span(ctx, "cagra_edge_distances");
+    hipExtLaunchKernelGGL(edge_distances_kernel, dim3(unsigned(index->n)), dim3(256), 0, ctx->stream, t0.start,
+                          t0.stop, 0, reinterpret_cast<const float4*>(index->rows), int(index->dpad / 4),
+                          int(index->dpad / 64), static_cast<const uint32_t*>(index->graph), int(index->degree),
+                          uint32_t(index->n), dst);
     after_launch("edge_distances_kernel");
-    timer_end(ctx, "cagra_edge_distances", t0);
     if (!out_on_device) {
       CVS_HIP(hipMemcpyAsync(out_distances, dst, count * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
       CVS_HIP(hipStreamSynchronize(ctx->stream));

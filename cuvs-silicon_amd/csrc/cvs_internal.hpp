@@ -1,6 +1,7 @@
 // Internal definitions shared by the HIP translation units of libcvs_hip.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -126,9 +127,18 @@ void bind(cvs_context* ctx);
 void upload_rows(cvs_context* ctx, float* dst, int64_t pitch, const float* src, int64_t n, int64_t d,
                  int src_on_device);
 
-// Event bracketing for the timing facility.
-hipEvent_t timer_begin(cvs_context* ctx, const char* kernel);
-void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin);
+// Kernel timing.  While a context's timing is on, timer_span() hands out a
+// start and a stop event for one kernel family: the family's first launch
+// takes `start` and its last launch `stop` (hipExtLaunchKernelGGL), and the
+// runtime fills them from those dispatches' own timestamps.  No marker
+// packets go between kernels, so timing can stay on inside a timed loop
+// without changing it.  Both events are null while timing is off, which
+// makes the launches plain ones.
+struct TimerSpan {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+TimerSpan timer_span(cvs_context* ctx, const char* kernel);
 
 // Launch-site helper: checks the launch, counts the dispatch.
 inline void after_launch(const char* what) {

@@ -70,32 +70,20 @@ void upload_rows(cvs_context* ctx, float* dst, int64_t pitch, const float* src, 
   check_hip(e, "hipMemcpy2DAsync");
 }
 
-hipEvent_t timer_begin(cvs_context* ctx, const char* kernel) {
-  if (!ctx->timing) return nullptr;
+TimerSpan timer_span(cvs_context* ctx, const char* kernel) {
+  if (!ctx->timing) return {};
   KernelTimer& t = ctx->timers[kernel];
-  hipEvent_t e;
-  if (!t.pool.empty()) {
-    e = t.pool.back();
-    t.pool.pop_back();
-  } else {
-    CVS_HIP(hipEventCreate(&e));
+  hipEvent_t e[2];
+  for (auto& ev : e) {
+    if (!t.pool.empty()) {
+      ev = t.pool.back();
+      t.pool.pop_back();
+    } else {
+      CVS_HIP(hipEventCreate(&ev));
+    }
   }
-  CVS_HIP(hipEventRecord(e, ctx->stream));
-  return e;
-}
-
-void timer_end(cvs_context* ctx, const char* kernel, hipEvent_t begin) {
-  if (!ctx->timing || !begin) return;
-  KernelTimer& t = ctx->timers[kernel];
-  hipEvent_t e;
-  if (!t.pool.empty()) {
-    e = t.pool.back();
-    t.pool.pop_back();
-  } else {
-    CVS_HIP(hipEventCreate(&e));
-  }
-  CVS_HIP(hipEventRecord(e, ctx->stream));
-  t.pending.emplace_back(begin, e);
+  t.pending.emplace_back(e[0], e[1]);
+  return {e[0], e[1]};
 }
 
 // ---------------------------------------------------------------------------

@@ -84,10 +84,14 @@ int cvs_context_synchronize(cvs_context* ctx);
 int cvs_context_device_info(cvs_context* ctx, char* name, size_t name_len,
                             int* compute_units, int64_t* total_mem_bytes);
 
-/* Kernel timing: while enabled, the launches of each kernel family are
- * bracketed by HIP events on the context stream.  cvs_context_kernel_time()
- * synchronizes and returns the summed elapsed milliseconds and launch count
- * for `kernel` ("bf_scan", "bf_merge", "bf_prep", ...), then clears them. */
+/* Kernel timing: while enabled, each call times its kernel families with HIP
+ * events that the runtime fills from the dispatches' own start and end
+ * timestamps (the family's first launch starts the span, its last launch
+ * ends it), so timing inserts nothing between kernels on the stream.
+ * cvs_context_kernel_time() synchronizes and returns the summed elapsed
+ * milliseconds and the number of spans for `kernel` ("bf_prep", "bf_sample",
+ * "bf_scan", "bf_merge", "cagra_search", "cagra_edge_distances"), then
+ * clears them. */
 int cvs_context_set_timing(cvs_context* ctx, int enable);
 int cvs_context_kernel_time(cvs_context* ctx, const char* kernel,
                             double* total_ms, uint64_t* launches);
@@ -132,6 +136,13 @@ int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds,
                         uint32_t* out_neighbors_dev, float* out_distances_dev);
 
 /* ---- CAGRA graph search -------------------------------------------------- */
+
+/* Navigation (seed) nodes of an n-row graph index, as the reference's
+ * cagra::build chooses them (src/cagra.cpp:63-72): n_nav = min(200,
+ * floor(sqrt(n))) rows, row i at floor(i * (n / n_nav)) with the spacing in
+ * double.  Writes *out_count = n_nav and, when out_ids is non-null, the n_nav
+ * ids (the caller sizes it: at most 200).  Host only; no device is needed. */
+int cvs_cagra_nav_nodes(int64_t n, uint32_t* out_ids, int64_t* out_count);
 
 /* Upload a graph index: n x d fp32 rows, its n x degree uint32 neighbour
  * lists (entries >= n are ignored) and `n_seeds` seed node ids (the
