@@ -10,6 +10,7 @@ import this package, and only as the checker.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import subprocess
@@ -35,39 +36,83 @@ def build(with_reference: bool | None = None) -> None:
         subprocess.run(["make", "-s", "-C", ORACLE_DIR, "ref", f"REFERENCE={REFERENCE_DIR}"], check=True)
 
 
+def build_variant(plant: int, out_dir: str) -> str:
+    """Compiles a copy of liboracle.so with mistake number `plant` switched
+    on (ORACLE_PLANT in the C sources) into out_dir; returns its path.  For
+    the pinning tests, which show that their known answers reject it."""
+    out = os.path.join(out_dir, f"liboracle_plant{int(plant)}.so")
+    srcs = [os.path.join(ORACLE_DIR, f) for f in ("bf_oracle.c", "cagra_oracle.c", "cagra_build_oracle.c")]
+    subprocess.run(["gcc", "-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fopenmp", "-w", "-shared",
+                    f"-DORACLE_PLANT={int(plant)}", *srcs, "-lm", "-o", out], check=True)
+    return out
+
+
+@contextlib.contextmanager
+def variant(path: str):
+    """Routes every oracle call through another build of liboracle.so (a
+    planted-mistake copy from build_variant) inside the `with` block."""
+    global _lib
+    saved = _lib
+    _lib = _configure(ctypes.CDLL(path))
+    try:
+        yield
+    finally:
+        _lib = saved
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(ORACLE_LIB):
             build(with_reference=False)
-        L = ctypes.CDLL(ORACLE_LIB)
-        L.oracle_l2_128.restype = c_float
-        L.oracle_l2_128.argtypes = [c_void_p, c_void_p]
-        for name in ("oracle_bf_exact", "oracle_bf_fp64"):
-            fn = getattr(L, name)
-            fn.restype = None
-            fn.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int]
-        L.oracle_cagra_nav_nodes.restype = c_int64
-        L.oracle_cagra_nav_nodes.argtypes = [c_int64, c_void_p]
-        L.oracle_cagra_entry_points.restype = None
-        L.oracle_cagra_entry_points.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p]
-        L.oracle_cagra_search_policy.restype = None
-        L.oracle_cagra_search_policy.argtypes = [c_uint64, c_uint64, c_int64, POINTER(c_uint32), POINTER(c_uint32)]
-        L.oracle_cagra_search.restype = None
-        L.oracle_cagra_search.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int64,
-                                          c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_void_p, c_int]
-        L.oracle_cagra_build_ref.restype = c_int
-        L.oracle_cagra_build_ref.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
-        L.oracle_cagra_build_ref_ex.restype = c_int
-        L.oracle_cagra_build_ref_ex.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int, c_int64,
-                                                c_int64]
-        L.oracle_pq_train.restype = None
-        L.oracle_pq_train.argtypes = [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]
-        L.oracle_knn_graph.restype = None
-        L.oracle_knn_graph.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
-        L.oracle_edge_distances.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int]
-        _lib = L
+        _lib = _configure(ctypes.CDLL(ORACLE_LIB))
     return _lib
+
+
+def _configure(L: ctypes.CDLL) -> ctypes.CDLL:
+    """Declares the C signatures of a loaded liboracle.so."""
+    L.oracle_l2_128.restype = c_float
+    L.oracle_l2_128.argtypes = [c_void_p, c_void_p]
+    for name in ("oracle_bf_exact", "oracle_bf_fp64"):
+        fn = getattr(L, name)
+        fn.restype = None
+        fn.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int]
+    L.oracle_cagra_nav_nodes.restype = c_int64
+    L.oracle_cagra_nav_nodes.argtypes = [c_int64, c_void_p]
+    L.oracle_cagra_entry_points.restype = None
+    L.oracle_cagra_entry_points.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p]
+    L.oracle_cagra_search_policy.restype = None
+    L.oracle_cagra_search_policy.argtypes = [c_uint64, c_uint64, c_int64, POINTER(c_uint32), POINTER(c_uint32)]
+    L.oracle_cagra_search.restype = None
+    L.oracle_cagra_search.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int64,
+                                      c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_void_p, c_int]
+    L.oracle_cagra_build_ref.restype = c_int
+    L.oracle_cagra_build_ref.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
+    L.oracle_cagra_build_ref_ex.restype = c_int
+    L.oracle_cagra_build_ref_ex.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int, c_int64,
+                                            c_int64]
+    L.oracle_pq_train.restype = None
+    L.oracle_pq_train.argtypes = [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]
+    L.oracle_kmeans_init.restype = None
+    L.oracle_kmeans_init.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_void_p]
+    L.oracle_ivf_kmeans.restype = c_int
+    L.oracle_ivf_kmeans.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_void_p, c_int]
+    L.oracle_ivf_near_clusters.restype = None
+    L.oracle_ivf_near_clusters.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int]
+    L.oracle_ivf_seed.restype = None
+    L.oracle_ivf_seed.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int64, c_void_p, c_int64,
+                                  c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int]
+    L.oracle_bucketing_perm.restype = None
+    L.oracle_bucketing_perm.argtypes = [c_int64, c_void_p]
+    L.oracle_bucketing_merge.restype = None
+    L.oracle_bucketing_merge.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int64, c_void_p,
+                                         c_void_p, c_int]
+    L.oracle_nn_descent.restype = c_int
+    L.oracle_nn_descent.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_void_p, c_uint32, c_int]
+    L.oracle_knn_graph.restype = None
+    L.oracle_knn_graph.argtypes = [c_void_p, c_int64, c_int64, c_uint32, c_void_p, c_int]
+    L.oracle_edge_distances.argtypes = [c_void_p, c_int64, c_int64, c_void_p, c_uint32, c_void_p, c_int]
+    return L
 
 
 def have_reference() -> bool:
@@ -249,3 +294,90 @@ def pq_train(base, threads: int = 1):
     lut = np.empty((8, 256, 256), np.float32)
     lib().oracle_pq_train(_p(base), n, d, int(threads), _p(codes), _p(lut))
     return codes, lut
+
+
+# ---- stages of the restated reference build --------------------------------
+
+def _empty_graph(n: int, g: int):
+    return np.full((n, g), 0xFFFFFFFF, np.uint32), np.full((n, g), np.inf, np.float32)
+
+
+def kmeans_init(base, K: int) -> np.ndarray:
+    """Initial IVF centres (src/metal_context.mm:366-375)."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    out = np.empty((K, d), np.float32)
+    lib().oracle_kmeans_init(_p(base), n, d, int(K), _p(out))
+    return out
+
+
+def ivf_kmeans(base, centres, max_iter: int = 20, threads: int = 1):
+    """Lloyd iterations from `centres` (src/metal_context.mm:381-435):
+    returns (centres, assignment, E-steps run)."""
+    base = np.ascontiguousarray(base, np.float32)
+    cent = np.array(centres, np.float32, copy=True, order="C")
+    n, d = base.shape
+    assign = np.empty(n, np.uint32)
+    it = lib().oracle_ivf_kmeans(_p(base), n, d, cent.shape[0], int(max_iter), _p(cent), _p(assign), int(threads))
+    return cent, assign, int(it)
+
+
+def ivf_near_clusters(centres, n_probe: int = 3, threads: int = 1) -> np.ndarray:
+    """The n_probe nearest other centres of each centre (:583-611)."""
+    cent = np.ascontiguousarray(centres, np.float32)
+    K, d = cent.shape
+    out = np.empty((K, n_probe), np.uint32)
+    lib().oracle_ivf_near_clusters(_p(cent), K, d, int(n_probe), _p(out), int(threads))
+    return out
+
+
+def ivf_seed(base, g: int, assign, nearc, max_own: int, codes=None, lut=None, graph=None, gdist=None,
+             threads: int = 1):
+    """Per-cluster seeding (:576-582, :614-681, :712-792) into (graph,
+    gdist), fresh (all missing) unless given.  Returns (graph, gdist)."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    assign = np.ascontiguousarray(assign, np.uint32)
+    nearc = np.ascontiguousarray(nearc, np.uint32)
+    K = nearc.shape[0]
+    if graph is None:
+        graph, gdist = _empty_graph(n, g)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    gdist = np.ascontiguousarray(gdist, np.float32)
+    cp = None if codes is None else np.ascontiguousarray(codes, np.uint8)
+    lp = None if lut is None else np.ascontiguousarray(lut, np.float32)
+    lib().oracle_ivf_seed(_p(base), n, d, int(g), _p(assign), K, _p(nearc), nearc.shape[1], int(max_own),
+                          None if cp is None else _p(cp), None if lp is None else _p(lp), _p(graph), _p(gdist),
+                          int(threads))
+    return graph, gdist
+
+
+def bucketing_perm(n: int) -> np.ndarray:
+    """The bucketing permutation (src/metal_context.mm:802-810)."""
+    out = np.empty(int(n), np.uint32)
+    lib().oracle_bucketing_perm(int(n), _p(out))
+    return out
+
+
+def bucketing_merge(base, g: int, perm, bucket: int = 256, graph=None, gdist=None, threads: int = 1):
+    """One random-bucketing pass (shaders/cagra_kernels.metal:403-462)."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    perm = np.ascontiguousarray(perm, np.uint32)
+    if graph is None:
+        graph, gdist = _empty_graph(n, g)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    gdist = np.ascontiguousarray(gdist, np.float32)
+    lib().oracle_bucketing_merge(_p(base), n, d, int(g), _p(perm), int(bucket), _p(graph), _p(gdist), int(threads))
+    return graph, gdist
+
+
+def nn_descent(base, graph, gdist, max_iter: int, threads: int = 1):
+    """nn-descent (shaders/cagra_kernels.metal:334-395): returns (graph,
+    gdist, iterations run)."""
+    base = np.ascontiguousarray(base, np.float32)
+    n, d = base.shape
+    graph = np.array(graph, np.uint32, copy=True, order="C")
+    gdist = np.array(gdist, np.float32, copy=True, order="C")
+    it = lib().oracle_nn_descent(_p(base), n, d, graph.shape[1], _p(graph), _p(gdist), int(max_iter), int(threads))
+    return graph, gdist, int(it)

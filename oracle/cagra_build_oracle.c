@@ -21,6 +21,14 @@
 
 #define INVALID_ID 0xffffffffu
 
+/* ORACLE_PLANT selects one deliberate mistake for the pinning tests, which
+ * build such variants of this file into temporary libraries and check that
+ * their known answers reject them (tests/test_oracle_build.py).  0, the
+ * default, is the restatement itself. */
+#ifndef ORACLE_PLANT
+#define ORACLE_PLANT 0
+#endif
+
 /* Cross product in place of cblas_sgemm: eight interleaved fp32 partial sums
  * combined pairwise (the BLAS order is unspecified). */
 static float dot_blk(const float* a, const float* b, int64_t d) {
@@ -180,263 +188,278 @@ void oracle_pq_train(const float* data, int64_t n, int64_t d, int nt, uint8_t* c
   free(counts);
 }
 
-int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
-                           uint32_t* out_graph, int threads) {
-  return oracle_cagra_build_ref_ex(data, n, d, graph_degree, out_graph, threads, 50000, 200000);
+/* Initial k-means centres (src/metal_context.mm:366-375): centre k is row
+ * min(floor(k * s + s / 2), n - 1) with s = n / K in double. */
+void oracle_kmeans_init(const float* data, int64_t n, int64_t d, int64_t K, float* centres) {
+  const double stride = (double)n / (double)K;
+  for (int64_t k = 0; k < K; ++k) {
+    int64_t ix = (int64_t)((double)k * stride + (ORACLE_PLANT == 4 ? 0.0 : stride * 0.5));
+    if (ix > n - 1) ix = n - 1;
+    memcpy(centres + k * d, data + ix * d, sizeof(float) * (size_t)d);
+  }
 }
 
-int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
-                              uint32_t* out_graph, int threads, int64_t exact_limit, int64_t pq_limit) {
-  if (!data || !out_graph || n <= 0 || d <= 0 || exact_limit < 0 || pq_limit < 0) return 1;
-  /* N > pq_limit: product-quantised seeding over 8 x 128 dimensions */
-  const int pq = n > exact_limit && n > pq_limit;
-  if (pq && d < 1024) return 2;
+/* Lloyd iterations of the IVF k-means (src/metal_context.mm:381-435), from
+ * the centres given: each E-step assigns every row to the centre of least
+ * |x|^2 - 2 x.c + |c|^2 (first minimum wins; assignments start at 0, and
+ * the first E-step counts as a change); when no row changes centre the loop
+ * stops, otherwise the M-step sums each centre's rows in row order and
+ * scales by 1 / count, and a centre with no rows becomes the zero vector.
+ * Returns the number of E-steps run (at most max_iter). */
+int oracle_ivf_kmeans(const float* data, int64_t n, int64_t d, int64_t K, int max_iter, float* cent,
+                      uint32_t* assign, int threads) {
   const int nt = threads > 0 ? threads : 1;
-  /* src/cagra.cpp:47-59 */
-  const uint32_t g = graph_degree < (uint32_t)(n - 1) ? graph_degree : (uint32_t)(n - 1);
-  const uint32_t nd_iters = n <= exact_limit ? 20u : (n <= pq_limit ? 5u : 0u);
-  if (g == 0) return 0;
-
-  uint32_t* graph = out_graph;
-  float* gdist = (float*)malloc(sizeof(float) * (size_t)n * g);
   float* norms = (float*)malloc(sizeof(float) * (size_t)n);
-  for (int64_t i = 0; i < n * (int64_t)g; ++i) {
-    graph[i] = INVALID_ID;
-    gdist[i] = INFINITY;
+  float* cn = (float*)malloc(sizeof(float) * (size_t)K);
+  int64_t* counts = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+  for (int64_t i = 0; i < n; ++i) {
+    norms[i] = sq_norm(data + i * d, d);
+    assign[i] = 0;
   }
-  for (int64_t i = 0; i < n; ++i) norms[i] = sq_norm(data + i * d, d);
-
-  if (n <= exact_limit) {
-    /* Exact all-pairs seeding (:324-349), one row at a time. */
-#pragma omp parallel num_threads(nt)
-    {
-      float* key = (float*)malloc(sizeof(float) * (size_t)n);
-      uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
-#pragma omp for schedule(dynamic, 8)
-      for (int64_t i = 0; i < n; ++i) {
-        const float ni = norms[i];
-        for (int64_t a = 0; a < n; ++a) key[a] = ni - 2.f * dot_blk(data + i * d, data + a * d, d) + norms[a];
-        for (int64_t a = 0; a < n; ++a) idx[a] = (uint32_t)a;
-        idx[i] = idx[n - 1];
-        const int64_t take = (int64_t)g < n - 1 ? (int64_t)g : n - 1;
-        select_smallest(idx, n - 1, take, key);
-        for (int64_t k = 0; k < take; ++k) insert_neighbor(graph, gdist, g, i, idx[k], key[idx[k]]);
-      }
-      free(key);
-      free(idx);
-    }
-  } else {
-    /* IVF k-means seeding (:351-435). */
-    int64_t K = (int64_t)sqrt((double)n);
-    if (K < (int64_t)g + 1) K = (int64_t)g + 1;
-    if (K > 2000) K = 2000;
-    float* cent = (float*)malloc(sizeof(float) * (size_t)(K * d));
-    const double stride = (double)n / (double)K;
-    for (int64_t k = 0; k < K; ++k) {
-      int64_t ix = (int64_t)((double)k * stride + stride * 0.5);
-      if (ix > n - 1) ix = n - 1;
-      memcpy(cent + k * d, data + ix * d, sizeof(float) * (size_t)d);
-    }
-    uint32_t* assign = (uint32_t*)calloc((size_t)n, sizeof(uint32_t));
-    float* cn = (float*)malloc(sizeof(float) * (size_t)K);
-    int64_t* counts = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
-    for (int iter = 0; iter < 20; ++iter) {
-      for (int64_t k = 0; k < K; ++k) cn[k] = sq_norm(cent + k * d, d);
-      int changed = iter == 0;
-#pragma omp parallel for schedule(static) num_threads(nt) reduction(| : changed)
-      for (int64_t i = 0; i < n; ++i) {
-        const float ni = norms[i];
-        float best_d = INFINITY;
-        uint32_t best_k = 0;
-        for (int64_t k = 0; k < K; ++k) {
-          const float dd = ni - 2.f * dot_blk(data + i * d, cent + k * d, d) + cn[k];
-          if (dd < best_d) {
-            best_d = dd;
-            best_k = (uint32_t)k;
-          }
-        }
-        if (assign[i] != best_k) {
-          changed = 1;
-          assign[i] = best_k;
-        }
-      }
-      if (!changed) break;
-      /* M-step (:421-434): sums in row order, then scale by 1/count. */
-      memset(cent, 0, sizeof(float) * (size_t)(K * d));
-      memset(counts, 0, sizeof(int64_t) * (size_t)K);
-      for (int64_t i = 0; i < n; ++i) {
-        const uint32_t k = assign[i];
-        counts[k]++;
-        float* c = cent + (int64_t)k * d;
-        const float* x = data + i * d;
-        for (int64_t j = 0; j < d; ++j) c[j] += x[j];
-      }
-      for (int64_t k = 0; k < K; ++k)
-        if (counts[k] > 0) {
-          const float inv = 1.0f / (float)counts[k];
-          for (int64_t j = 0; j < d; ++j) cent[k * d + j] *= inv;
-        }
-    }
-    /* Cluster lists (:576-579) and the 3 nearest clusters (:583-611). */
-    int64_t* cstart = (int64_t*)calloc((size_t)K + 1, sizeof(int64_t));
-    uint32_t* members = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
-    for (int64_t i = 0; i < n; ++i) cstart[assign[i] + 1]++;
-    for (int64_t k = 0; k < K; ++k) cstart[k + 1] += cstart[k];
-    {
-      int64_t* fill = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
-      for (int64_t k = 0; k < K; ++k) fill[k] = cstart[k];
-      for (int64_t i = 0; i < n; ++i) members[fill[assign[i]]++] = (uint32_t)i;
-      free(fill);
-    }
+  int iters = 0;
+  for (int iter = 0; iter < max_iter; ++iter) {
+    ++iters;
     for (int64_t k = 0; k < K; ++k) cn[k] = sq_norm(cent + k * d, d);
-    const int64_t n_probe = K - 1 < 3 ? K - 1 : 3;
-    uint32_t* nearc = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(K * (n_probe > 0 ? n_probe : 1)));
-#pragma omp parallel num_threads(nt)
-    {
-      float* key = (float*)malloc(sizeof(float) * (size_t)K);
-      uint32_t* kidx = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)K);
-#pragma omp for schedule(static)
+    int changed = iter == 0;
+#pragma omp parallel for schedule(static) num_threads(nt) reduction(| : changed)
+    for (int64_t i = 0; i < n; ++i) {
+      const float ni = norms[i];
+      float best_d = INFINITY;
+      uint32_t best_k = 0;
       for (int64_t k = 0; k < K; ++k) {
-        for (int64_t a = 0; a < K; ++a) key[a] = cn[k] - 2.f * dot_blk(cent + k * d, cent + a * d, d) + cn[a];
-        for (int64_t a = 0; a < K; ++a) kidx[a] = (uint32_t)a;
-        kidx[k] = kidx[K - 1];
-        select_smallest(kidx, K - 1, n_probe, key);
-        for (int64_t t = 0; t < n_probe; ++t) nearc[k * n_probe + t] = kidx[t];
-      }
-      free(key);
-      free(kidx);
-    }
-    /* Per-cluster seeding: exact distances (:712-792), or PQ table sums
-     * (:614-681) followed by exact distances of every kept entry (:683-709). */
-    uint8_t* codes = NULL;
-    float* lut = NULL;
-    if (pq) {
-      codes = (uint8_t*)malloc((size_t)n * 8);
-      lut = (float*)malloc(sizeof(float) * 8 * 256 * 256);
-      oracle_pq_train(data, n, d, nt, codes, lut);
-    }
-    const int64_t max_own = (n / K) * 4 + 64;
-#pragma omp parallel num_threads(nt)
-    {
-      uint32_t* probe = (uint32_t*)malloc(sizeof(uint32_t) * 8192);
-      float* key = (float*)malloc(sizeof(float) * 8192);
-      uint32_t* midx = (uint32_t*)malloc(sizeof(uint32_t) * 8192);
-#pragma omp for schedule(dynamic, 1)
-      for (int64_t k = 0; k < K; ++k) {
-        const int64_t own_n = cstart[k + 1] - cstart[k];
-        if (own_n == 0) continue;
-        const uint32_t* own = members + cstart[k];
-        const int64_t nk = own_n < max_own ? own_n : max_own;
-        int64_t m = 0;
-        for (int64_t i = 0; i < nk && m < 8192; ++i) probe[m++] = own[i];
-        for (int64_t t = 0; t < n_probe; ++t) {
-          const uint32_t c = nearc[k * n_probe + t];
-          for (int64_t i = cstart[c]; i < cstart[c + 1] && m < 8192; ++i) probe[m++] = members[i];
-        }
-        if (m <= 1) continue;
-        const int64_t take = (int64_t)g < m - 1 ? (int64_t)g : m - 1;
-        for (int64_t i = 0; i < nk; ++i) {
-          const uint32_t vi = own[i];
-          const float ni = norms[vi];
-          for (int64_t p = 0; p < m; ++p) {
-            if (probe[p] == vi) {
-              key[p] = INFINITY;
-            } else if (pq) {
-              const uint8_t* ca = codes + (int64_t)vi * 8;
-              const uint8_t* cb = codes + (int64_t)probe[p] * 8;
-              float s2 = 0.f;
-              for (int sm = 0; sm < 8; ++sm) s2 += lut[((int64_t)sm * 256 + ca[sm]) * 256 + cb[sm]];
-              key[p] = s2;
-            } else {
-              key[p] = ni - 2.f * dot_blk(data + (int64_t)vi * d, data + (int64_t)probe[p] * d, d) + norms[probe[p]];
-            }
-            midx[p] = (uint32_t)p;
-          }
-          select_smallest(midx, m, take, key);
-          for (int64_t t = 0; t < take; ++t) {
-            const uint32_t nb = probe[midx[t]];
-            if (nb == vi) continue;
-            insert_neighbor(graph, gdist, g, vi, nb, key[midx[t]]);
-          }
+        const float dd = ni - 2.f * dot_blk(data + i * d, cent + k * d, d) + cn[k];
+        if (ORACLE_PLANT == 1 ? dd <= best_d : dd < best_d) {
+          best_d = dd;
+          best_k = (uint32_t)k;
         }
       }
-      free(probe);
-      free(key);
-      free(midx);
-    }
-    if (pq) {
-      /* Exact squared L2 of every entry (recompute_graph_distances,
-       * shaders/cagra_kernels.metal:658-681: float4 partial sums over
-       * 4 floor(d / 4) dimensions; entries that are not row ids get +inf). */
-#pragma omp parallel for schedule(static) num_threads(nt)
-      for (int64_t i = 0; i < n; ++i)
-        for (uint32_t e = 0; e < g; ++e) {
-          const uint32_t nb = graph[i * g + e];
-          gdist[i * g + e] = nb < (uint32_t)n ? l2_f4(data + i * d, data + (int64_t)nb * d, d) : INFINITY;
-        }
-      free(codes);
-      free(lut);
-    }
-    free(cent);
-    free(assign);
-    free(cn);
-    free(counts);
-    free(cstart);
-    free(members);
-    free(nearc);
-
-    /* Random bucketing (:795-851; kernel shaders/cagra_kernels.metal:403-462). */
-    uint32_t* rperm = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
-    for (int64_t i = 0; i < n; ++i) rperm[i] = (uint32_t)i;
-    uint64_t r = 0xFEDCBA9876543210ULL;
-    for (int64_t i = n - 1; i > 0; --i) {
-      r = r * 6364136223846793005ULL + 1442695040888963407ULL;
-      const int64_t j = (int64_t)(r >> 33) % (i + 1);
-      const uint32_t tmp = rperm[i];
-      rperm[i] = rperm[j];
-      rperm[j] = tmp;
-    }
-    const int64_t rbsz = 256;
-    const uint32_t take = g < 64 ? g : 64;
-#pragma omp parallel for schedule(dynamic, 64) num_threads(nt)
-    for (int64_t v = 0; v < n; ++v) {
-      const int64_t start = (v / rbsz) * rbsz;
-      const int64_t end = start + rbsz < n ? start + rbsz : n;
-      const int64_t t = v - start;
-      const uint32_t vi = rperm[v];
-      float hd[64];
-      uint32_t hn[64];
-      for (uint32_t h = 0; h < take; ++h) {
-        hd[h] = INFINITY;
-        hn[h] = INVALID_ID;
-      }
-      for (int64_t b = 0; b < end - start; ++b) {
-        if (b == t) continue;
-        const uint32_t nb = rperm[start + b];
-        const float dist = l2_f4(data + (int64_t)vi * d, data + (int64_t)nb * d, d);
-        float worst = hd[0];
-        uint32_t wi = 0;
-        for (uint32_t h = 1; h < take; ++h)
-          if (hd[h] > worst) {
-            worst = hd[h];
-            wi = h;
-          }
-        if (dist < worst) {
-          hd[wi] = dist;
-          hn[wi] = nb;
-        }
-      }
-      for (uint32_t h = 0; h < take; ++h) {
-        if (hn[h] == INVALID_ID) continue;
-        insert_neighbor(graph, gdist, g, vi, hn[h], hd[h]);
+      if (assign[i] != best_k) {
+        changed = 1;
+        assign[i] = best_k;
       }
     }
-    free(rperm);
+    if (!changed) break;
+    memset(counts, 0, sizeof(int64_t) * (size_t)K);
+    for (int64_t i = 0; i < n; ++i) counts[assign[i]]++;
+    for (int64_t k = 0; k < K; ++k)
+      if (ORACLE_PLANT != 2 || counts[k] > 0) memset(cent + k * d, 0, sizeof(float) * (size_t)d);
+    for (int64_t i = 0; i < n; ++i) {
+      float* c = cent + (int64_t)assign[i] * d;
+      const float* x = data + i * d;
+      for (int64_t j = 0; j < d; ++j) c[j] += x[j];
+    }
+    for (int64_t k = 0; k < K; ++k)
+      if (counts[k] > 0) {
+        const float inv = 1.0f / (float)(counts[k] + (ORACLE_PLANT == 3 ? 1 : 0));
+        for (int64_t j = 0; j < d; ++j) cent[k * d + j] *= inv;
+      }
   }
+  free(norms);
+  free(cn);
+  free(counts);
+  return iters;
+}
 
-  /* nn-descent (:853-911; kernel shaders/cagra_kernels.metal:334-395). */
+/* The n_probe nearest other centres of every centre (src/metal_context.mm:
+ * 583-611), by |c_k|^2 - 2 c_k.c_a + |c_a|^2, nearest first; the candidate
+ * order is 0..K-2 with centre k's own slot holding K-1, and a tie keeps the
+ * earlier candidate.  Writes K x n_probe ids. */
+void oracle_ivf_near_clusters(const float* cent, int64_t K, int64_t d, int64_t n_probe, uint32_t* nearc,
+                              int threads) {
+  const int nt = threads > 0 ? threads : 1;
+  float* cn = (float*)malloc(sizeof(float) * (size_t)K);
+  for (int64_t k = 0; k < K; ++k) cn[k] = sq_norm(cent + k * d, d);
+#pragma omp parallel num_threads(nt)
+  {
+    float* key = (float*)malloc(sizeof(float) * (size_t)K);
+    uint32_t* kidx = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int64_t k = 0; k < K; ++k) {
+      for (int64_t a = 0; a < K; ++a) key[a] = cn[k] - 2.f * dot_blk(cent + k * d, cent + a * d, d) + cn[a];
+      for (int64_t a = 0; a < K; ++a) kidx[a] = (uint32_t)a;
+      if (ORACLE_PLANT != 5) kidx[k] = kidx[K - 1];
+      select_smallest(kidx, K - 1, n_probe, key);
+      for (int64_t t = 0; t < n_probe; ++t) nearc[k * n_probe + t] = kidx[t];
+    }
+    free(key);
+    free(kidx);
+  }
+  free(cn);
+}
+
+/* Per-cluster seeding (src/metal_context.mm:576-582, :614-681, :712-792).
+ * For each cluster k with members (in row order): candidates = its first
+ * min(count, max_own) members, then all members of its n_probe near
+ * clusters in order, cut at 8,192.  Each of those first min(count,
+ * max_own) members takes the min(g, m - 1) candidates of least key (itself
+ * excluded; ties keep the earlier candidate) and inserts them into its row
+ * with insert_neighbor (src/metal_context.mm:315-322).  The key is the
+ * expanded-form squared distance |x|^2 - 2 x.y + |y|^2, or, when `codes`
+ * is given, the product-quantisation table sum over 8 subspaces
+ * lut[m][code_m(x)][code_m(y)] (:649-655), after which every entry's
+ * distance is replaced by its exact float4 squared L2 (recompute_graph_
+ * distances, shaders/cagra_kernels.metal:658-681; ids that are not rows
+ * get +inf).  Members past max_own seed nothing. */
+void oracle_ivf_seed(const float* data, int64_t n, int64_t d, uint32_t g, const uint32_t* assign, int64_t K,
+                     const uint32_t* nearc, int64_t n_probe, int64_t max_own, const uint8_t* codes,
+                     const float* lut, uint32_t* graph, float* gdist, int threads) {
+  const int nt = threads > 0 ? threads : 1;
+  const int pq = codes != NULL && lut != NULL;
+  float* norms = (float*)malloc(sizeof(float) * (size_t)n);
+  for (int64_t i = 0; i < n; ++i) norms[i] = sq_norm(data + i * d, d);
+  int64_t* cstart = (int64_t*)calloc((size_t)K + 1, sizeof(int64_t));
+  uint32_t* members = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+  for (int64_t i = 0; i < n; ++i) cstart[assign[i] + 1]++;
+  for (int64_t k = 0; k < K; ++k) cstart[k + 1] += cstart[k];
+  {
+    int64_t* fill = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+    for (int64_t k = 0; k < K; ++k) fill[k] = cstart[k];
+    for (int64_t i = 0; i < n; ++i) members[fill[assign[i]]++] = (uint32_t)i;
+    free(fill);
+  }
+#pragma omp parallel num_threads(nt)
+  {
+    uint32_t* probe = (uint32_t*)malloc(sizeof(uint32_t) * 8192);
+    float* key = (float*)malloc(sizeof(float) * 8192);
+    uint32_t* midx = (uint32_t*)malloc(sizeof(uint32_t) * 8192);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t own_n = cstart[k + 1] - cstart[k];
+      if (own_n == 0) continue;
+      const uint32_t* own = members + cstart[k];
+      const int64_t nk = (ORACLE_PLANT == 7 || own_n < max_own) ? own_n : max_own;
+      int64_t m = 0;
+      for (int64_t i = 0; i < nk && m < 8192; ++i) probe[m++] = own[i];
+      for (int64_t t = 0; t < (ORACLE_PLANT == 6 && n_probe > 2 ? 2 : n_probe); ++t) {
+        const uint32_t c = nearc[k * n_probe + t];
+        for (int64_t i = cstart[c]; i < cstart[c + 1] && m < 8192; ++i) probe[m++] = members[i];
+      }
+      if (m <= 1) continue;
+      const int64_t take = (int64_t)g < m - 1 ? (int64_t)g : m - 1;
+      for (int64_t i = 0; i < nk; ++i) {
+        const uint32_t vi = own[i];
+        const float ni = norms[vi];
+        for (int64_t p = 0; p < m; ++p) {
+          if (probe[p] == vi) {
+            key[p] = INFINITY;
+          } else if (pq) {
+            const uint8_t* ca = codes + (int64_t)vi * 8;
+            const uint8_t* cb = codes + (int64_t)probe[p] * 8;
+            float s2 = 0.f;
+            for (int sm = 0; sm < (ORACLE_PLANT == 8 ? 7 : 8); ++sm) s2 += lut[((int64_t)sm * 256 + ca[sm]) * 256 + cb[sm]];
+            key[p] = s2;
+          } else {
+            key[p] = ni - 2.f * dot_blk(data + (int64_t)vi * d, data + (int64_t)probe[p] * d, d) + norms[probe[p]];
+          }
+          midx[p] = (uint32_t)p;
+        }
+        select_smallest(midx, m, take, key);
+        for (int64_t t = 0; t < take; ++t) {
+          const uint32_t nb = probe[midx[t]];
+          if (nb == vi) continue;
+          insert_neighbor(graph, gdist, g, vi, nb, key[midx[t]]);
+        }
+      }
+    }
+    free(probe);
+    free(key);
+    free(midx);
+  }
+  if (pq) {
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (int64_t i = 0; i < n; ++i)
+      for (uint32_t e = 0; e < g; ++e) {
+        const uint32_t nb = graph[i * g + e];
+        gdist[i * g + e] = nb < (uint32_t)n ? l2_f4(data + i * d, data + (int64_t)nb * d, d) : INFINITY;
+      }
+  }
+  free(norms);
+  free(cstart);
+  free(members);
+}
+
+/* The bucketing permutation (src/metal_context.mm:802-810): identity, then
+ * for i = n-1 down to 1, r = r * 6364136223846793005 + 1442695040888963407
+ * (mod 2^64, r starting at 0xFEDCBA9876543210) and swap of positions i and
+ * (r >> 33) mod (i + 1). */
+void oracle_bucketing_perm(int64_t n, uint32_t* perm) {
+  for (int64_t i = 0; i < n; ++i) perm[i] = (uint32_t)i;
+  uint64_t r = 0xFEDCBA9876543210ULL;
+  for (int64_t i = n - 1; i > 0; --i) {
+    r = r * 6364136223846793005ULL + 1442695040888963407ULL;
+    const int64_t j = (int64_t)(r >> 33) % (i + 1);
+    const uint32_t tmp = perm[i];
+    perm[i] = perm[j];
+    perm[j] = tmp;
+  }
+}
+
+/* One random-bucketing pass (random_bucketing, shaders/cagra_kernels.metal:
+ * 403-462): positions [b * bucket, (b + 1) * bucket) of `perm` form bucket b.
+ * Each row keeps its take = min(g, 64) nearest bucket mates by float4
+ * squared L2 (a mate replaces the first slot of largest distance when
+ * strictly closer), then inserts them into its row with insert_neighbor in
+ * slot order, unreached slots skipped.  No duplicate check, as there. */
+void oracle_bucketing_merge(const float* data, int64_t n, int64_t d, uint32_t g, const uint32_t* perm,
+                            int64_t bucket, uint32_t* graph, float* gdist, int threads) {
+  const int nt = threads > 0 ? threads : 1;
+  const uint32_t take = g < 64 ? g : 64;
+#pragma omp parallel for schedule(dynamic, 64) num_threads(nt)
+  for (int64_t v = 0; v < n; ++v) {
+    const int64_t start = (v / bucket) * bucket;
+    const int64_t end = start + bucket < n ? start + bucket : n;
+    const int64_t t = v - start;
+    const uint32_t vi = perm[v];
+    float hd[64];
+    uint32_t hn[64];
+    for (uint32_t h = 0; h < take; ++h) {
+      hd[h] = INFINITY;
+      hn[h] = INVALID_ID;
+    }
+    for (int64_t b = 0; b < end - start; ++b) {
+      if (b == t) continue;
+      const uint32_t nb = perm[start + b];
+      const float dist = l2_f4(data + (int64_t)vi * d, data + (int64_t)nb * d, d);
+      float worst = hd[0];
+      uint32_t wi = 0;
+      for (uint32_t h = 1; h < take; ++h)
+        if (hd[h] > worst) {
+          worst = hd[h];
+          wi = h;
+        }
+      if (dist < worst) {
+        hd[wi] = dist;
+        hn[wi] = nb;
+      }
+    }
+    for (uint32_t h = 0; h < take; ++h) {
+      if (hn[h] == INVALID_ID) continue;
+      if (ORACLE_PLANT == 9) {
+        int dup = 0;
+        for (uint32_t j = 0; j < g; ++j) dup |= graph[(int64_t)vi * g + j] == hn[h];
+        if (dup) continue;
+      }
+      insert_neighbor(graph, gdist, g, vi, hn[h], hd[h]);
+    }
+  }
+}
+
+/* nn-descent (nn_descent, shaders/cagra_kernels.metal:334-395; host loop
+ * src/metal_context.mm:853-911), at most max_iter iterations.  Per node, in
+ * slot order of its current row: for each valid neighbour, each entry of
+ * that neighbour's row as it was when the iteration began (the schedule
+ * chosen for the reference's racy kernel) that is a row id, not the node,
+ * and not in the node's current row is a candidate; its float4 squared L2
+ * replaces the node's entry of largest distance (first such slot; distances
+ * above 0 only) when strictly smaller.  Stops after an iteration that
+ * changed no row.  Returns the number of iterations run. */
+int oracle_nn_descent(const float* data, int64_t n, int64_t d, uint32_t g, uint32_t* graph, float* gdist,
+                      uint32_t max_iter, int threads) {
+  const int nt = threads > 0 ? threads : 1;
   uint32_t* snap = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n * g);
-  for (uint32_t iter = 0; iter < nd_iters; ++iter) {
+  int iters = 0;
+  for (uint32_t iter = 0; iter < max_iter; ++iter) {
+    ++iters;
     memcpy(snap, graph, sizeof(uint32_t) * (size_t)n * g);
     int any = 0;
 #pragma omp parallel for schedule(dynamic, 32) num_threads(nt) reduction(| : any)
@@ -476,6 +499,7 @@ int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t 
                 worst_d = rowd[i];
                 worst_g = i;
               }
+            if (ORACLE_PLANT == 10 && worst_g < g) worst_g = 0;
             if (worst_g < g && dist4[c] < worst_d) {
               row[worst_g] = cd;
               rowd[worst_g] = dist4[c];
@@ -485,10 +509,98 @@ int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t 
         }
       }
     }
-    if (!any) break;
+    if (!any) {
+      if (ORACLE_PLANT == 11) --iters;
+      break;
+    }
   }
   free(snap);
+  return iters;
+}
+
+int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
+                           uint32_t* out_graph, int threads) {
+  return oracle_cagra_build_ref_ex(data, n, d, graph_degree, out_graph, threads, 50000, 200000);
+}
+
+int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
+                              uint32_t* out_graph, int threads, int64_t exact_limit, int64_t pq_limit) {
+  if (!data || !out_graph || n <= 0 || d <= 0 || exact_limit < 0 || pq_limit < 0) return 1;
+  /* N > pq_limit: product-quantised seeding over 8 x 128 dimensions */
+  const int pq = n > exact_limit && n > pq_limit;
+  if (pq && d < 1024) return 2;
+  const int nt = threads > 0 ? threads : 1;
+  /* src/cagra.cpp:47-59 */
+  const uint32_t g = graph_degree < (uint32_t)(n - 1) ? graph_degree : (uint32_t)(n - 1);
+  const uint32_t nd_iters = n <= exact_limit ? 20u : (n <= pq_limit ? 5u : 0u);
+  if (g == 0) return 0;
+
+  uint32_t* graph = out_graph;
+  float* gdist = (float*)malloc(sizeof(float) * (size_t)n * g);
+  for (int64_t i = 0; i < n * (int64_t)g; ++i) {
+    graph[i] = INVALID_ID;
+    gdist[i] = INFINITY;
+  }
+
+  if (n <= exact_limit) {
+    /* Exact all-pairs seeding (:324-349), one row at a time. */
+    float* norms = (float*)malloc(sizeof(float) * (size_t)n);
+    for (int64_t i = 0; i < n; ++i) norms[i] = sq_norm(data + i * d, d);
+#pragma omp parallel num_threads(nt)
+    {
+      float* key = (float*)malloc(sizeof(float) * (size_t)n);
+      uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+#pragma omp for schedule(dynamic, 8)
+      for (int64_t i = 0; i < n; ++i) {
+        const float ni = norms[i];
+        for (int64_t a = 0; a < n; ++a) key[a] = ni - 2.f * dot_blk(data + i * d, data + a * d, d) + norms[a];
+        for (int64_t a = 0; a < n; ++a) idx[a] = (uint32_t)a;
+        idx[i] = idx[n - 1];
+        const int64_t take = (int64_t)g < n - 1 ? (int64_t)g : n - 1;
+        select_smallest(idx, n - 1, take, key);
+        for (int64_t k = 0; k < take; ++k) insert_neighbor(graph, gdist, g, i, idx[k], key[idx[k]]);
+      }
+      free(key);
+      free(idx);
+    }
+    free(norms);
+  } else {
+    /* IVF seeding (:351-435, :576-792): K = clamp(floor(sqrt n), G + 1,
+     * 2000) centres, 20 Lloyd iterations, the 3 nearest clusters, at most
+     * (n / K) * 4 + 64 own members per cluster. */
+    int64_t K = (int64_t)sqrt((double)n);
+    if (K < (int64_t)g + 1) K = (int64_t)g + 1;
+    if (K > 2000) K = 2000;
+    float* cent = (float*)malloc(sizeof(float) * (size_t)(K * d));
+    uint32_t* assign = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    oracle_kmeans_init(data, n, d, K, cent);
+    oracle_ivf_kmeans(data, n, d, K, 20, cent, assign, nt);
+    const int64_t n_probe = K - 1 < 3 ? K - 1 : 3;
+    uint32_t* nearc = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(K * (n_probe > 0 ? n_probe : 1)));
+    oracle_ivf_near_clusters(cent, K, d, n_probe, nearc, nt);
+    uint8_t* codes = NULL;
+    float* lut = NULL;
+    if (pq) {
+      codes = (uint8_t*)malloc((size_t)n * 8);
+      lut = (float*)malloc(sizeof(float) * 8 * 256 * 256);
+      oracle_pq_train(data, n, d, nt, codes, lut);
+    }
+    oracle_ivf_seed(data, n, d, g, assign, K, nearc, n_probe, (n / K) * 4 + 64, codes, lut, graph, gdist, nt);
+    free(codes);
+    free(lut);
+    free(cent);
+    free(assign);
+    free(nearc);
+
+    /* One random-bucketing pass (:795-851), buckets of 256. */
+    uint32_t* rperm = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    oracle_bucketing_perm(n, rperm);
+    oracle_bucketing_merge(data, n, d, g, rperm, 256, graph, gdist, nt);
+    free(rperm);
+  }
+
+  /* nn-descent (:853-911). */
+  oracle_nn_descent(data, n, d, g, graph, gdist, nd_iters, nt);
   free(gdist);
-  free(norms);
   return 0;
 }

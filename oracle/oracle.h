@@ -93,35 +93,92 @@ void oracle_knn_graph(const float* base, int64_t n, int64_t d, uint32_t g, uint3
 
 /* The reference's graph build for n <= 200,000 (src/cagra.cpp:47-59 ->
  * src/metal_context.mm:289-914): G = min(graph_degree, n - 1); n <= 50,000:
- * exact all-pairs seeding; otherwise IVF k-means (K = clamp(sqrt n, G+1,
- * 2000), 20 iterations, stride initialisation), exact seeding of each
- * cluster's rows against their own and the 3 nearest clusters' rows (at most
- * 8,192), then one random bucketing pass (LCG Fisher-Yates, buckets of 256,
- * top-min(G, 64) merged per row); then nn-descent for 20 (n <= 50,000) or 5
- * iterations.  Writes n x G ids (UINT32_MAX for missing).  Cross products use
- * a fixed 8-way summation where the reference calls cblas_sgemm; nn-descent
- * reads other nodes' lists as of the start of each iteration (one legal
- * schedule of the reference's racy kernel).  For n > 200,000 the per-cluster
- * seeding ranks candidates by product-quantisation table sums
- * (src/metal_context.mm:437-568, :614-681; 8 subspaces of 128 dimensions,
- * 256 centres) and re-scores the kept entries exactly (:683-709), with no
- * nn-descent.  Returns 0, 1 on bad arguments, 2 when the PQ path meets
- * d < 1024.  Pinned: equals the exact
- * kNN graph on integer data through the exact-seeding path; on the IVF path,
- * rows are full, in range, free of self edges and hold most exact neighbours
- * (tests/test_oracle_build.py).  Bit-exact graphs are parity unpinned (the
- * reference's own result depends on a GPU race and on BLAS order). */
+ * exact all-pairs seeding; otherwise the IVF stages below in the
+ * reference's order and settings (oracle_kmeans_init, oracle_ivf_kmeans
+ * with K = clamp(floor(sqrt n), G+1, 2000) and 20 iterations,
+ * oracle_ivf_near_clusters with 3 probes, oracle_ivf_seed with max_own =
+ * (n / K) * 4 + 64, oracle_bucketing_perm + oracle_bucketing_merge with
+ * buckets of 256); then oracle_nn_descent for 20 (n <= 50,000) or 5
+ * iterations.  Writes n x G ids (UINT32_MAX for missing).  Cross products
+ * use a fixed 8-way summation where the reference calls cblas_sgemm.  For
+ * n > 200,000 the seeding ranks candidates by product-quantisation table
+ * sums (oracle_pq_train; src/metal_context.mm:437-568, :614-681) and
+ * re-scores the kept entries exactly (:683-709), with no nn-descent.
+ * Returns 0, 1 on bad arguments, 2 when the PQ path meets d < 1024.
+ * Pinned: the exact-seeding path equals the exact kNN graph on integer data;
+ * the IVF path equals the composition of the stage functions with the
+ * reference's constants, each of which changes the graph on the test data
+ * (tests/test_oracle_build.py).  Bit-exact graphs of the reference itself
+ * are parity unpinned (they depend on a GPU race and on BLAS order). */
 int oracle_cagra_build_ref(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
                            uint32_t* out_graph, int threads);
 
 /* oracle_cagra_build_ref with the size limits as arguments (exact seeding
  * for n <= exact_limit, PQ seeding for n > max(exact_limit, pq_limit); the
  * reference's limits are 50,000 and 200,000), so that tests can run the
- * large-N phases at small n.  The PQ seeding is pinned by its equivalence
- * with exact per-cluster seeding over the rows rebuilt from their codes
- * (tests/test_oracle_build.py). */
+ * large-N phases at small n. */
 int oracle_cagra_build_ref_ex(const float* data, int64_t n, int64_t d, uint32_t graph_degree,
                               uint32_t* out_graph, int threads, int64_t exact_limit, int64_t pq_limit);
+
+/* ---- stages of the build (pinned one by one in tests/test_oracle_build.py) */
+
+/* Initial IVF centres (src/metal_context.mm:366-375): centre k = row
+ * min(floor(k * s + s / 2), n - 1), s = n / K in double.  Pinned: the row
+ * indices at n = 1000, K = 7 written out. */
+void oracle_kmeans_init(const float* data, int64_t n, int64_t d, int64_t K, float* centres);
+
+/* Lloyd iterations from the given centres (src/metal_context.mm:381-435):
+ * E-step argmin of |x|^2 - 2 x.c + |c|^2 (first minimum wins), stop when no
+ * row changes; M-step sums in row order times 1 / count; an empty centre
+ * becomes zero.  Updates `centres`, writes `assign`, returns the E-steps
+ * run (<= max_iter).  Pinned: a hand-worked case in which duplicated
+ * initial centres tie (the lower index takes every row), the empty centre
+ * becomes zero and then captures the rows near the origin; planted mistakes
+ * (higher index wins, empty centre kept, wrong divisor) fail it. */
+int oracle_ivf_kmeans(const float* data, int64_t n, int64_t d, int64_t K, int max_iter, float* centres,
+                      uint32_t* assign, int threads);
+
+/* The n_probe nearest other centres of each centre, nearest first
+ * (src/metal_context.mm:583-611).  Pinned: centres on a parabola, where the
+ * answer is written out. */
+void oracle_ivf_near_clusters(const float* centres, int64_t K, int64_t d, int64_t n_probe, uint32_t* nearc,
+                              int threads);
+
+/* Per-cluster seeding (src/metal_context.mm:576-582, :614-681, :712-792):
+ * the first min(count, max_own) members of each cluster take their g
+ * nearest among those members and all members of the cluster's n_probe near
+ * clusters (at most 8,192 candidates), inserted with insert_neighbor;
+ * members past max_own seed nothing.  Exact expanded-form keys, or with
+ * `codes`/`lut` the product-quantisation table sums followed by exact float4
+ * distances of the kept entries.  Pinned: integer clusters where a true
+ * neighbour lies only in the third near cluster, and the cap leaves later
+ * members empty (brute force over the candidate sets); the PQ form equals
+ * the exact form on rows built from the quantisation prototypes. */
+void oracle_ivf_seed(const float* data, int64_t n, int64_t d, uint32_t g, const uint32_t* assign, int64_t K,
+                     const uint32_t* nearc, int64_t n_probe, int64_t max_own, const uint8_t* codes,
+                     const float* lut, uint32_t* graph, float* gdist, int threads);
+
+/* The bucketing permutation (src/metal_context.mm:802-810).  Pinned: a
+ * permutation; its values against a second restatement from the
+ * reference's text (parity unpinned beyond that: the reference ships no
+ * permutation output). */
+void oracle_bucketing_perm(int64_t n, uint32_t* perm);
+
+/* One random-bucketing pass (shaders/cagra_kernels.metal:403-462) over
+ * buckets of `bucket` consecutive positions of perm.  Pinned: with the
+ * identity permutation on integer data every row receives its min(g, 64)
+ * nearest bucket mates (brute force), a mate already in the row is inserted
+ * again (the reference's duplicates), and bucket edges are respected. */
+void oracle_bucketing_merge(const float* data, int64_t n, int64_t d, uint32_t g, const uint32_t* perm,
+                            int64_t bucket, uint32_t* graph, float* gdist, int threads);
+
+/* nn-descent over 2-hop neighbours (shaders/cagra_kernels.metal:334-395,
+ * src/metal_context.mm:853-911), at most max_iter iterations; neighbour rows
+ * are read as they were when each iteration began.  Returns the iterations
+ * run.  Pinned: a chain in which each iteration can only move one hop,
+ * whose state after t iterations is written out, and the early stop. */
+int oracle_nn_descent(const float* data, int64_t n, int64_t d, uint32_t g, uint32_t* graph, float* gdist,
+                      uint32_t max_iter, int threads);
 
 /* The product-quantisation training of the build's PQ path, exposed for its
  * pinning tests: codes n x 8 (uint8), lut 8 x 256 x 256. */
