@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 
 import numpy as np
@@ -218,9 +219,18 @@ class Context:
         h = c_void_p()
         _check(load().cvs_context_create(int(device), byref(h)))
         self.handle = h
+        # Datasets and graph indexes made on this context: the C library
+        # refuses to destroy a context that still owns any, so close() closes
+        # the live ones first.
+        self._children = weakref.WeakSet()
+
+    def _adopt(self, child) -> None:
+        self._children.add(child)
 
     def close(self) -> None:
         if self.handle is not None:
+            for child in list(self._children):
+                child.close()
             _check(load().cvs_context_destroy(self.handle))
             self.handle = None
 
@@ -326,11 +336,13 @@ class Dataset:
             _check(load().cvs_dataset_create(ctx.handle, rows.ctypes.data_as(c_void_p), n, d, 0, byref(h)))
         self.handle = h
         self.n, self.d = int(n), int(d)
+        ctx._adopt(self)
 
     def close(self) -> None:
-        if self.handle is not None:
+        # A dataset dies with its context (Context.close closes it first).
+        if self.handle is not None and self.ctx.handle is not None:
             _check(load().cvs_dataset_destroy(self.handle))
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
@@ -389,6 +401,7 @@ class CagraIndex:
                                              byref(h)))
         self.handle = h
         self.n, self.d, self.degree = int(n), int(d), int(degree)
+        ctx._adopt(self)
         self.set_traversal(traversal_bits)
 
     def edge_distances(self, out: "DeviceArray" = None):
@@ -412,9 +425,10 @@ class CagraIndex:
         self.traversal_bits = int(bits)
 
     def close(self) -> None:
-        if self.handle is not None:
+        # An index dies with its context (Context.close closes it first).
+        if self.handle is not None and self.ctx.handle is not None:
             _check(load().cvs_cagra_index_destroy(self.handle))
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:

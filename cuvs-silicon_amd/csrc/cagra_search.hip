@@ -736,6 +736,7 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
       delete ix;
       throw;
     }
+    ++ctx->live_children;
     *out_index = ix;
   });
 }
@@ -749,6 +750,7 @@ int cvs_cagra_index_destroy(cvs_cagra_index* index) {
     (void)hipFree(index->rows16);
     (void)hipFree(index->graph);
     if (index->seeds) (void)hipFree(index->seeds);
+    --index->ctx->live_children;
     delete index;
   });
 }

@@ -76,6 +76,10 @@ struct KernelTimer {
 
 struct cvs_context {
   int device = 0;
+  // Datasets and graph indexes created on this context and not yet
+  // destroyed; cvs_context_destroy refuses while any is alive, since each
+  // of them uses the context's stream and device at its own destruction.
+  int live_children = 0;
   hipStream_t stream = nullptr;
   int compute_units = 0;
   int64_t total_mem = 0;

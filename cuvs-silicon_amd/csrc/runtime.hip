@@ -8,6 +8,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <string>
 
 #include "cvs_internal.hpp"
 
@@ -206,6 +207,9 @@ int cvs_context_create(int device, cvs_context** out_ctx) {
 int cvs_context_destroy(cvs_context* ctx) {
   return guarded([&] {
     if (!ctx) return;
+    if (ctx->live_children > 0)
+      fail(CVS_ERR_INVALID_ARGUMENT, "context still owns " + std::to_string(ctx->live_children) +
+                                         " dataset(s) or graph index(es): destroy them first");
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->timers) {
@@ -218,6 +222,7 @@ int cvs_context_destroy(cvs_context* ctx) {
     ctx->ws_queries.release();
     ctx->ws_partial.release();
     ctx->ws_io.release();
+    ctx->ws_teams.release();
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
   });
@@ -349,6 +354,7 @@ int cvs_dataset_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d
       delete ds;
       throw;
     }
+    ++ctx->live_children;
     *out_ds = ds;
   });
 }
@@ -361,6 +367,7 @@ int cvs_dataset_destroy(cvs_dataset* ds) {
     (void)hipFree(ds->rows);
     (void)hipFree(ds->tiles);
     (void)hipFree(ds->norms);
+    --ds->ctx->live_children;
     delete ds;
   });
 }

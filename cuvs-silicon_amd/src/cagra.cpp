@@ -90,16 +90,14 @@ index<float, std::uint32_t> build<float, std::int64_t>(
 
     // Navigation nodes: min(200, floor(sqrt(N))) evenly spaced rows and
     // their vectors (src/cagra.cpp:63-82); search seeds from them.
-    const std::int64_t n_nav =
-        std::min<std::int64_t>(200, static_cast<std::int64_t>(std::sqrt(static_cast<double>(n))));
+    std::int64_t n_nav = 0;
+    check(cvs_cagra_nav_nodes(n, nullptr, &n_nav));
     std::vector<std::uint32_t> nav(static_cast<std::size_t>(n_nav));
+    check(cvs_cagra_nav_nodes(n, nav.data(), &n_nav));
     std::vector<float> nav_vectors(static_cast<std::size_t>(n_nav * d));
-    const double step = static_cast<double>(n) / static_cast<double>(n_nav);
-    for (std::int64_t i = 0; i < n_nav; ++i) {
-      nav[static_cast<std::size_t>(i)] = static_cast<std::uint32_t>(static_cast<double>(i) * step);
+    for (std::int64_t i = 0; i < n_nav; ++i)
       std::copy_n(data + static_cast<std::int64_t>(nav[static_cast<std::size_t>(i)]) * d,
                   static_cast<std::size_t>(d), nav_vectors.data() + i * d);
-    }
     idx.set_nav_nodes(std::move(nav));
     idx.set_nav_vectors(std::move(nav_vectors));
   }

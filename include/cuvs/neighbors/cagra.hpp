@@ -107,8 +107,16 @@ class index {
   // entry point; nav_vectors() caches their vectors (n_nav x D).
   const std::vector<IndexT>& nav_nodes() const noexcept { return nav_nodes_; }
   const std::vector<DataT>& nav_vectors() const noexcept { return nav_vectors_; }
-  void set_nav_nodes(std::vector<IndexT> n) { nav_nodes_ = std::move(n); }
-  void set_nav_vectors(std::vector<DataT> v) { nav_vectors_ = std::move(v); }
+  // The device copy seeds searches from the nav nodes, so it is dropped
+  // whenever they change (the reference reads them on every search).
+  void set_nav_nodes(std::vector<IndexT> n) {
+    nav_nodes_ = std::move(n);
+    device_.reset();
+  }
+  void set_nav_vectors(std::vector<DataT> v) {
+    nav_vectors_ = std::move(v);
+    device_.reset();
+  }
 
   // Backend cache (device copies); filled lazily by search().
   std::shared_ptr<detail::device_state>& device_cache() const noexcept { return device_; }

@@ -227,6 +227,47 @@ void build_save_load_search(const std::string& scratch) {
   CHECK(mrecall >= recall - 0.05);
 }
 
+// Changing an index's navigation nodes changes where the next search
+// starts (the device copy is refreshed).  The graph has no edges, so a
+// search returns its best start candidates: with row B (the query's exact
+// nearest row) among the navigation nodes it is found, and after the nodes
+// are replaced by a far row it is not (the hashed extra seeds of this query
+// do not include B).
+void nav_change_reseeds() {
+  const std::int64_t N = 100000, D = 8, K = 4;
+  const std::uint32_t B = 77777, far_row = 5;
+  std::vector<float> base(N * D);
+  for (std::int64_t i = 0; i < N; ++i)
+    for (std::int64_t j = 0; j < D; ++j) base[i * D + j] = float(100 + (i * 7 + j * 13) % 997);
+  for (std::int64_t j = 0; j < D; ++j) base[B * D + j] = 0.f;
+  std::vector<float> q(D, 0.5f);
+  cagra::index<float, std::uint32_t> idx{base, N, D};
+  idx.set_knn_graph(std::vector<std::uint32_t>(N * 4, 0xFFFFFFFFu), 4);
+  auto nav_to = [&](std::uint32_t row) {
+    idx.set_nav_nodes({row});
+    idx.set_nav_vectors(std::vector<float>(base.begin() + row * D, base.begin() + (row + 1) * D));
+  };
+  raft::resources res;
+  cagra::search_params sp;
+  std::vector<std::uint32_t> nbr(K);
+  std::vector<float> dist(K);
+  auto run = [&] {
+    cagra::search(res, sp, idx, raft::make_device_matrix_view<const float, std::int64_t>(q.data(), 1, D),
+                  raft::make_device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), 1, K),
+                  raft::make_device_matrix_view<float, std::int64_t>(dist.data(), 1, K));
+  };
+  nav_to(B);
+  run();
+  CHECK(nbr[0] == B && dist[0] == 2.f);  // 8 x 0.5^2
+  nav_to(far_row);
+  run();
+  CHECK(nbr[0] != B);
+  for (int i = 0; i < K; ++i) CHECK(nbr[i] != B);
+  nav_to(B);
+  run();
+  CHECK(nbr[0] == B);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -234,5 +275,6 @@ int main(int argc, char** argv) {
   faiss_smoke();
   dispatch_test();
   build_save_load_search(scratch);
+  nav_change_reseeds();
   return apitest::finish("test_api_gpu");
 }
