@@ -11,12 +11,14 @@ Gates:
     recall of the restated reference search on the reference's own graph
     for n <= 50,000 (exact all-pairs seeding, src/metal_context.mm:324-349,
     which the oracle's exact kNN graph stands for) at equal degree and itopk,
-    minus 0.01;
+    by the paired gate of tests/search_metrics.py;
   - nn-descent convergence: the last iteration's insertion rate is below the
     threshold unless the iteration cap was reached.
 """
 import numpy as np
 import pytest
+
+from search_metrics import assert_recall_not_below, exact_knn
 
 pytestmark = pytest.mark.gpu
 
@@ -84,9 +86,8 @@ def test_downstream_recall_at_least_reference(ctx, oracle, n, d, g, itopk):
     ours, _ = ctx.cagra_index(base, graph, nav).search(qs, 10, itopk_size=itopk)
     ref_graph = oracle.knn_graph(base, g, threads=16)
     ref, _ = oracle.cagra_reference_search(base, ref_graph, nav, qs, 10, itopk_size=itopk, threads=16)
-    r_ours, r_ref = recall(ours, gt, 10), recall(ref, gt, 10)
-    print(f"recall@10 built graph + GPU search {r_ours:.4f}; exact graph + restated reference search {r_ref:.4f}")
-    assert r_ours >= r_ref - 0.01
+    assert_recall_not_below(ours, ref, gt, 10, f"n={n} d={d}: built graph + GPU search vs exact graph + "
+                                               "restated reference search")
 
 
 def test_device_output_matches_shape(ctx, cvs):
@@ -111,12 +112,16 @@ def test_c5_full_size_build(ctx, cvs, oracle):
     """N=1,000,000, D=1024, intermediate degree 128 -> 64 on the clustered
     distribution: the graph invariants row by row (vectorised), nn-descent
     convergence below 0.1% insertions within the iteration cap, and graph
-    search recall@10 at itopk 64 on 200 queries against exact k-NN.  The
-    reference's own 1M graph reached recall 0.72 at itopk 512; this gate
-    (0.6 at itopk 64) guards against a broken build, not a quality target."""
+    search recall@10 at itopk 64 on 500 queries against exact k-NN (numpy):
+    at least that of the graph the reference's own algorithm builds at this
+    size (its N > 200,000 path: PQ seeding + one bucketing pass, no
+    nn-descent; cvs_cagra_build_reference, checked against the oracle's
+    restatement at n = 6,000 below) at equal degree and itopk, by the paired
+    gate, and above 0.6 (a broken build)."""
     n, d, g = 1_000_000, 1024, 64
     base = cvs.synth_clustered(12345, cvs.STREAM_BASE, n, d)
-    qs = cvs.synth_clustered(12345, cvs.STREAM_QUERIES, 200, d)
+    qs = cvs.synth_clustered(12345, cvs.STREAM_QUERIES, 500, d)
+    print("[c5] building N=1M", flush=True)
     graph, st = ctx.cagra_build(base, intermediate_degree=128, graph_degree=g)
     assert graph.shape == (n, g)
     assert (graph < n).all()
@@ -125,12 +130,21 @@ def test_c5_full_size_build(ctx, cvs, oracle):
     assert not (srt[:, 1:] == srt[:, :-1]).any(), "a row repeats an id"
     assert st["iterations"] <= 20
     assert st["final_update_rate"] < 0.001 or st["iterations"] == 20
-    gt, _ = ctx.dataset(base).bf_search(qs, 10)
-    idx = ctx.cagra_index(base, graph, oracle.cagra_nav_nodes(n))
+    print("[c5] exact ground truth", flush=True)
+    gt = exact_knn(base, qs, 10)
+    nav = cvs.cagra_nav_nodes(n)
+    idx = ctx.cagra_index(base, graph, nav)
     nbr, _ = idx.search(qs, 10, itopk_size=64)
+    idx.close()
     r = recall(nbr, gt, 10)
     print(f"N=1M build: {st['seconds_total']:.2f} s, {st['iterations']} iterations, recall@10 {r:.4f}")
     assert r >= 0.6, r
+    print("[c5] the reference's algorithm at N=1M", flush=True)
+    rgraph, _ = ctx.cagra_build_reference(base, g)
+    ridx = ctx.cagra_index(base, rgraph, nav)
+    rnbr, _ = ridx.search(qs, 10, itopk_size=64)
+    ridx.close()
+    assert_recall_not_below(nbr, rnbr, gt, 10, "N=1M this build vs the reference algorithm's graph, itopk 64")
 
 
 def neighbour_recall(graph, exact, k):
@@ -143,8 +157,9 @@ def test_reference_build_matches_oracle(ctx, cvs, oracle, n, d, g):
     """cvs_cagra_build_reference (the reference's build, src/metal_context.mm:
     289-914, on the GPU) against the oracle's restatement of it on the same
     data: the same graph invariants (no repeated ids, which the reference
-    itself allows), neighbour quality within 0.02 of the restated graph's,
-    and the restated reference search on each graph within 0.02 recall.
+    itself allows), and neighbour quality and the restated reference
+    search's recall on each graph not below the restated graph's (paired
+    gates over rows and queries).
     n = 3000: the exact path (exact kNN graph: all but ties equal); n = 60,000:
     k-means + per-cluster seeding, bucketing and nn-descent."""
     base = cvs.synth_clustered(4242, cvs.STREAM_BASE, n, d)
@@ -169,8 +184,8 @@ def test_reference_build_matches_oracle(ctx, cvs, oracle, n, d, g):
     else:
         assert st["clusters"] == int(np.sqrt(n)) and 1 <= st["kmeans_iterations"] <= 20
         assert 1 <= st["descent_iterations"] <= 5
-    assert q_gpu >= q_ref - 0.02
-    assert r_gpu >= r_ref - 0.02
+    assert_recall_not_below(graph[sample], ref[sample], exact, 10, f"n={n} neighbour recall", whole_rows=True)
+    assert_recall_not_below(s_gpu, s_ref, gt, 10, f"n={n} search recall on the GPU graph vs the oracle's graph")
 
 
 @pytest.mark.gpu
@@ -181,7 +196,8 @@ def test_reference_pq_build_matches_oracle(ctx, cvs, oracle):
     restatement.  The GPU ranks candidates by the squared distance of the rows
     rebuilt from their codes, the oracle by summing the symmetric PQ table
     (two formulations of the same distance), so graphs agree up to fp32 ties:
-    neighbour recall and the restated reference search recall within 0.03."""
+    neighbour recall and the restated reference search recall not below the
+    oracle graph's (paired gates)."""
     n, d, g = 6000, 1024, 32
     base = cvs.synth_clustered(77, cvs.STREAM_BASE, n, d)
     qs = cvs.synth_clustered(77, cvs.STREAM_QUERIES, 300, d)
@@ -202,7 +218,7 @@ def test_reference_pq_build_matches_oracle(ctx, cvs, oracle):
     print(f"stats {st}; neighbour recall@10 gpu {q_gpu:.4f} oracle {q_ref:.4f}; "
           f"search recall gpu graph {r_gpu:.4f} oracle graph {r_ref:.4f}")
     assert st["descent_iterations"] == 0 and 8 <= st["pq_iterations"] <= 80
-    assert q_gpu >= q_ref - 0.03
-    assert r_gpu >= r_ref - 0.03
+    assert_recall_not_below(graph[sample], ref[sample], exact, 10, "PQ path neighbour recall", whole_rows=True)
+    assert_recall_not_below(s_gpu, s_ref, gt, 10, "PQ path search recall on the GPU graph vs the oracle's graph")
     with pytest.raises(ValueError):  # CVS_ERR_UNSUPPORTED: the PQ path needs d = 1024
         ctx.cagra_build_reference(base[:, :512], g, exact_limit=0, pq_limit=0)

@@ -7,12 +7,15 @@ Gates:
     distance 100 and the k > N padding; the hand-traced path-graph walk;
   - recall@k vs exact ground truth at least the restated reference search's
     (oracle.cagra_reference_search) on the same graph, navigation nodes and
-    itopk, minus 0.01 (a few queries may differ either way);
+    itopk, by the paired gate of tests/search_metrics.py (the mean per-query
+    difference of hits no more than 3 standard errors below zero);
   - invariants: rows sorted by (distance, id), unique ids, in range, and
     every distance equal to the exact fp32 distance of its id (1e-5 rel).
 """
 import numpy as np
 import pytest
+
+from search_metrics import assert_recall_not_below
 
 pytestmark = pytest.mark.gpu
 
@@ -109,10 +112,8 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width, bits):
     idx = ctx.cagra_index(base, graph, nav, traversal_bits=bits)
     nbr, dist = idx.search(qs, k, itopk_size=itopk, search_width=width)
     check_invariants(base, qs, nbr, dist)
-    r_gpu, r_ref = recall(nbr, gt, k), recall(ref_nbr, gt, k)
-    print(f"recall@{k}: gpu {r_gpu:.4f} restated reference {r_ref:.4f}")
-    assert r_gpu >= r_ref - 0.01, (r_gpu, r_ref)
-    assert r_gpu > 0.8
+    assert_recall_not_below(nbr, ref_nbr, gt, k, f"n={n} d={d} itopk={itopk} width={width} {bits}-bit")
+    assert recall(nbr, gt, k) > 0.8
 
 
 @pytest.mark.parametrize("bits", [32, 16])
@@ -196,32 +197,29 @@ def test_argument_errors(ctx, oracle):
         idx.set_traversal(8)
 
 
-@pytest.mark.parametrize("n,d,q", [(60_000, 128, 500), (100_000, 1024, 1000)])
+@pytest.mark.parametrize("n,d,q", [(60_000, 128, 2000)])
 def test_recall_on_reference_built_graph(ctx, cvs, oracle, n, d, q):
     """The graph-search gate on the reference's own graph: the restated
     reference build (IVF seeding + random bucketing + 5 nn-descent
     iterations, the reference's path for 50,000 < N <= 200,000) of the
     benchmark distribution (64 centres, sigma 0.3, L2-normalised), degree
     64, itopk 64.  GPU search recall@10 (search_width 1 and 4) must be at
-    least the restated reference search's; the second case is the full
-    N=100,000 D=1024 configuration.  Both traversal precisions."""
+    least the restated reference search's.  Both traversal precisions.  The
+    full N=100,000 D=1024 configuration is tests/test_cagra_c4_gpu.py."""
     base = cvs.synth_clustered(12345, cvs.STREAM_BASE, n, d)
     qs = cvs.synth_clustered(12345, cvs.STREAM_QUERIES, q, d)
     graph = oracle.cagra_build_reference(base, 64, threads=16)
     nav = oracle.cagra_nav_nodes(n)
     gt, _ = oracle.bf_exact(base, qs, 10, threads=16)
     ref, _ = oracle.cagra_reference_search(base, graph, nav, qs, 10, itopk_size=64, threads=16)
-    r_ref = recall(ref, gt, 10)
     idx = ctx.cagra_index(base, graph, nav)
     for bits in (16, 32):
         idx.set_traversal(bits)
         for width in (1, 4):
             nbr, dist = idx.search(qs, 10, itopk_size=64, search_width=width)
             check_invariants(base, qs, nbr, dist)
-            r_gpu = recall(nbr, gt, 10)
-            print(f"N={n} D={d} reference-built graph, {bits}-bit traversal, width {width}: recall@10 gpu "
-                  f"{r_gpu:.4f} restated reference {r_ref:.4f}")
-            assert r_gpu >= r_ref - 0.01
+            assert_recall_not_below(nbr, ref, gt, 10, f"N={n} D={d} reference-built graph, {bits}-bit, "
+                                                      f"width {width}")
 
 
 @pytest.mark.parametrize("n,d,g", [(2000, 128, 32), (1500, 100, 16), (700, 1024, 64)])
@@ -270,8 +268,8 @@ def test_teams_complete_graph_known_answers(ctx, oracle, bits):
 def test_teams_recall_and_invariants(ctx, oracle, teams, itopk, bits):
     """Multi-team search on a kNN graph: rows sorted by (distance, id), ids
     unique (a row found by several teams is kept once), exact distances, and
-    recall@10 at least the single search's with a list of the same total
-    length capped at 64, minus 0.02."""
+    recall@10 at least the restated reference search's with a beam of the
+    per-team itopk (paired gate)."""
     rng = np.random.default_rng(teams * 100 + itopk)
     n, d, g, k = 4000, 96, 32, 10
     centers = rng.standard_normal((16, d)).astype(np.float32)
@@ -282,10 +280,9 @@ def test_teams_recall_and_invariants(ctx, oracle, teams, itopk, bits):
     gt, _ = oracle.bf_exact(base, qs, k, threads=16)
     nbr, dist = idx.search_teams(qs, k, teams, itopk_size=itopk)
     check_invariants(base, qs, nbr, dist)
-    single, _ = idx.search(qs, k, itopk_size=min(64, teams * itopk))
-    r_teams, r_single = recall(nbr, gt, k), recall(single, gt, k)
-    print(f"{teams} teams x itopk {itopk}: recall@10 {r_teams:.4f}, single search {r_single:.4f}")
-    assert r_teams >= r_single - 0.02
+    ref, _ = oracle.cagra_reference_search(base, graph, oracle.cagra_nav_nodes(n), qs, k, itopk_size=itopk,
+                                           threads=16)
+    assert_recall_not_below(nbr, ref, gt, k, f"{teams} teams x itopk {itopk}, {bits}-bit")
 
 
 def test_teams_argument_errors(ctx, oracle):
