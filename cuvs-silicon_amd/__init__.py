@@ -102,6 +102,7 @@ class BuildStats(ctypes.Structure):
 _SIGNATURES["cvs_cagra_build"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_uint32, c_uint32,
                                           c_float, c_uint64, c_void_p, c_int, POINTER(BuildStats)])
 
+_SIGNATURES["cvs_bf_search_noalloc"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p])
 _SIGNATURES["cvs_cagra_nav_nodes"] = (c_int, [c_int64, c_void_p, POINTER(c_int64)])
 
 # The bucketing permutation seed of the reference (src/metal_context.mm:803).
@@ -361,6 +362,12 @@ class Dataset:
         _check(load().cvs_bf_search(self.ctx.handle, self.handle, queries.ctypes.data_as(c_void_p), q, int(k),
                                     nbr.ctypes.data_as(c_void_p), dist.ctypes.data_as(c_void_p)))
         return nbr, dist
+
+    def bf_search_noalloc(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray) -> None:
+        """bf_search_async with the library's per-device scratch array
+        (cvs_bf_search_noalloc): no device allocation."""
+        _check(load().cvs_bf_search_noalloc(self.ctx.handle, self.handle, queries.ptr, queries.shape[0], int(k),
+                                            nbr.ptr, dist.ptr))
 
     def bf_search_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray) -> None:
         _check(load().cvs_bf_search_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0], int(k),

@@ -49,6 +49,8 @@
 // far below the gap between rank k and rank kp on the target data.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "cvs_internal.hpp"
@@ -1091,8 +1093,26 @@ void launch_scan(cvs_context* ctx, int ks, dim3 grid, const ScanArgs& args, int 
   after_launch(mode == kModeScan ? "bf_scan_kernel" : "bf_sample_kernel");
 }
 
-void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q,
-                      int64_t k, uint32_t* nbr, float* dist) {
+// Launch geometry and workspace layout of one brute-force call.
+struct BfPlan {
+  int ks = 0;              // k-steps per tile (padded dimension / 16)
+  int64_t n_units = 0;     // 2-stage units in the dataset
+  int kp = 0;              // candidates per (dataset range, query)
+  unsigned qblocks = 0;    // 128-query blocks
+  bool large_batch = false;
+  int G = 0;               // dataset ranges of the scan
+  int stride = 0;          // keys per (query, range) list in the workspace
+  int64_t s_units = 0, s_stride = 0;  // threshold sample
+  int Gs = 0;              // dataset ranges of the sample
+  int m_min = 0;           // sample minima per query
+  int64_t q_tiles = 0;     // 32-query tiles
+  // Workspace: query tiles | query norms | thresholds | sample minima |
+  // list minima | candidate lists, each 256-byte aligned.
+  size_t off_qnorm = 0, off_thr = 0, off_smin = 0, off_lmin = 0, off_part = 0, total = 0;
+};
+
+BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
+               const uint32_t* nbr, const float* dist) {
   if (!ds || ds->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "dataset does not belong to context");
   if (!queries || !nbr || !dist) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
   if (q <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count must be positive");
@@ -1102,23 +1122,25 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
     fail(CVS_ERR_UNSUPPORTED, "dimension exceeds CVS_BF_MAX_DIM for the fused kernel");
   if (q > (int64_t(1) << 24)) fail(CVS_ERR_UNSUPPORTED, "too many queries in one call");
 
-  const int ks = int(ds->dp / kStepCols);
-  const int rpu = 2 * kStageBlocks * 32 / ks;  // rows per unit
-  const int64_t n_units = ds->n_tiles * ks / (2 * kStageBlocks);
-  const int kp = choose_kp(k);
-  const unsigned qblocks = unsigned((q + kQB - 1) / kQB);
-  const bool global_lists = kp > 64;
+  BfPlan p;
+  p.ks = int(ds->dp / kStepCols);
+  const int rpu = 2 * kStageBlocks * 32 / p.ks;  // rows per unit
+  p.n_units = ds->n_tiles * p.ks / (2 * kStageBlocks);
+  p.kp = choose_kp(k);
+  p.qblocks = unsigned((q + kQB - 1) / kQB);
+  const bool global_lists = p.kp > 64;
   // Dataset ranges (workgroups along N): one per compute unit, at most 128
   // with kp = 128, and 32 for large batches, whose 128-query blocks then run
   // range-major so that the blocks sharing a range stream it together
   // through L2 / MALL.
-  const bool large_batch = qblocks > 8;
+  p.large_batch = p.qblocks > 8;
   int G = ctx->compute_units;
   if (G > 256) G = 256;
   if (global_lists && G > 128) G = 128;
-  if (large_batch && G > 32) G = 32;
-  if (int64_t(G) > n_units) G = int(n_units);
-  const int stride = global_lists ? Lists<128, kModeScan>::CAP : kp;
+  if (p.large_batch && G > 32) G = 32;
+  if (int64_t(G) > p.n_units) G = int(p.n_units);
+  p.G = G;
+  p.stride = global_lists ? Lists<128, kModeScan>::CAP : p.kp;
 
   // Sample: 32,768 rows for small batches, 65,536 for large ones, in whole
   // units, evenly strided, over Gs workgroups; 2 minima per (query,
@@ -1127,80 +1149,120 @@ void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* quer
   // kp * n / (sample * G) appends per query over its range: large batches
   // (kp = 128 and only 32 dataset ranges) need the larger sample to keep
   // appends and list compactions off the scan's critical path.
-  int64_t s_units = (large_batch ? 65536 : 32768) / rpu;
-  if (s_units < 1) s_units = 1;
-  if (s_units > n_units) s_units = n_units;
-  const int64_t s_stride = n_units / s_units;
-  int Gs = std::min(ctx->compute_units, 256);
-  if (int64_t(Gs) > s_units) Gs = int(s_units);
-  const int m_min = 2 * Gs;
+  p.s_units = (p.large_batch ? 65536 : 32768) / rpu;
+  if (p.s_units < 1) p.s_units = 1;
+  if (p.s_units > p.n_units) p.s_units = p.n_units;
+  p.s_stride = p.n_units / p.s_units;
+  p.Gs = std::min(ctx->compute_units, 256);
+  if (int64_t(p.Gs) > p.s_units) p.Gs = int(p.s_units);
+  p.m_min = 2 * p.Gs;
 
-  // Workspaces: query tiles | query norms | thresholds | sample minima |
-  // list minima; lists.
-  const int64_t q_tiles = (q + 31) / 32;
+  p.q_tiles = (q + 31) / 32;
   auto align = [](size_t b) { return (b + 255) / 256 * 256; };
-  const size_t qtile_bytes = align(size_t(q_tiles) * size_t(ks) * kStepBytes);
-  const size_t qnorm_bytes = align(size_t(q_tiles) * 32 * sizeof(float));
-  const size_t thr_bytes = align(size_t(q) * sizeof(float));
-  const size_t smin_bytes = align(size_t(q) * size_t(m_min) * sizeof(float));
-  const size_t lmin_bytes = align(size_t(q) * size_t(G) * sizeof(uint64_t));
-  ctx->ws_queries.reserve(qtile_bytes + qnorm_bytes + thr_bytes + smin_bytes + lmin_bytes);
-  char* wsq = ctx->ws_queries.as<char>();
-  u32x4* qtiles = reinterpret_cast<u32x4*>(wsq);
-  float* qnorms = reinterpret_cast<float*>(wsq + qtile_bytes);
-  float* thr0 = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes);
-  float* sgmin = reinterpret_cast<float*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes);
-  uint64_t* lmin = reinterpret_cast<uint64_t*>(wsq + qtile_bytes + qnorm_bytes + thr_bytes + smin_bytes);
-  ctx->ws_partial.reserve(size_t(q) * size_t(G) * size_t(stride) * sizeof(uint64_t));
-  uint64_t* part = ctx->ws_partial.as<uint64_t>();
+  p.off_qnorm = align(size_t(p.q_tiles) * size_t(p.ks) * kStepBytes);
+  p.off_thr = p.off_qnorm + align(size_t(p.q_tiles) * 32 * sizeof(float));
+  p.off_smin = p.off_thr + align(size_t(q) * sizeof(float));
+  p.off_lmin = p.off_smin + align(size_t(q) * size_t(p.m_min) * sizeof(float));
+  p.off_part = p.off_lmin + align(size_t(q) * size_t(G) * sizeof(uint64_t));
+  p.total = p.off_part + align(size_t(q) * size_t(G) * size_t(p.stride) * sizeof(uint64_t));
+  return p;
+}
+
+// Enqueues the five launches of one search on the context stream, with the
+// workspace at `ws` (p.total bytes; nothing in it needs to start at zero:
+// every byte a launch reads was written by an earlier launch of the same
+// call).  `timed` = false skips the timing facility (no events).
+void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const float* queries, int64_t q,
+               int64_t k, uint32_t* nbr, float* dist, char* ws, bool timed) {
+  u32x4* qtiles = reinterpret_cast<u32x4*>(ws);
+  float* qnorms = reinterpret_cast<float*>(ws + p.off_qnorm);
+  float* thr0 = reinterpret_cast<float*>(ws + p.off_thr);
+  float* sgmin = reinterpret_cast<float*>(ws + p.off_smin);
+  uint64_t* lmin = reinterpret_cast<uint64_t*>(ws + p.off_lmin);
+  uint64_t* part = reinterpret_cast<uint64_t*>(ws + p.off_part);
+  const int G = p.G, kp = p.kp;
 
   ScanArgs args{};
   args.tiles = reinterpret_cast<const u32x4*>(ds->tiles);
   args.norms = reinterpret_cast<const f32x4*>(ds->norms);
-  args.n_units = n_units;
+  args.n_units = p.n_units;
   args.qtiles = qtiles;
   args.qnorms = qnorms;
   args.nq = int(q);
-  args.n_qtiles = int(q_tiles);
+  args.n_qtiles = int(p.q_tiles);
   args.kp = kp;
   args.thr0 = thr0;
   args.part = part;
   args.sgmin = sgmin;
   args.lmin = lmin;
-  args.s_units = s_units;
-  args.s_stride = s_stride;
-  args.n_qblocks = int(qblocks);
+  args.s_units = p.s_units;
+  args.s_stride = p.s_stride;
+  args.n_qblocks = int(p.qblocks);
   const unsigned wave_blocks = unsigned((q + kWaves - 1) / kWaves);
 
-  const TimerSpan t0 = timer_span(ctx, "bf_prep");
-  hipExtLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((q_tiles * 32 + kWaves - 1) / kWaves)), dim3(kThreads), 0,
-                        ctx->stream, t0.start, t0.stop, 0, queries, q, ds->d, ks, q_tiles * 32, qtiles, qnorms);
+  const TimerSpan t0 = timed ? timer_span(ctx, "bf_prep") : TimerSpan{};
+  hipExtLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((p.q_tiles * 32 + kWaves - 1) / kWaves)),
+                        dim3(kThreads), 0, ctx->stream, t0.start, t0.stop, 0, queries, q, ds->d, p.ks,
+                        p.q_tiles * 32, qtiles, qnorms);
   after_launch("query_tiles_kernel");
 
-  const TimerSpan t1 = timer_span(ctx, "bf_sample");
-  args.n_ranges = Gs;
+  const TimerSpan t1 = timed ? timer_span(ctx, "bf_sample") : TimerSpan{};
+  args.n_ranges = p.Gs;
   args.qb_fast = 0;
-  launch_scan(ctx, ks, dim3(unsigned(Gs), qblocks), args, kModeSample, t1.start, nullptr);
+  launch_scan(ctx, p.ks, dim3(unsigned(p.Gs), p.qblocks), args, kModeSample, t1.start, nullptr);
   hipExtLaunchKernelGGL(bf_select_kernel, dim3(wave_blocks), dim3(kThreads), 0, ctx->stream, nullptr, t1.stop, 0,
-                        static_cast<const float*>(sgmin), m_min, kp, int(q), thr0);
+                        static_cast<const float*>(sgmin), p.m_min, kp, int(q), thr0);
   after_launch("bf_select_kernel");
 
-  const TimerSpan t2 = timer_span(ctx, "bf_scan");
+  const TimerSpan t2 = timed ? timer_span(ctx, "bf_scan") : TimerSpan{};
   args.n_ranges = G;
-  args.qb_fast = large_batch ? 1 : 0;
-  launch_scan(ctx, ks, large_batch ? dim3(unsigned(G) * qblocks, 1) : dim3(unsigned(G), qblocks), args,
+  args.qb_fast = p.large_batch ? 1 : 0;
+  launch_scan(ctx, p.ks, p.large_batch ? dim3(unsigned(G) * p.qblocks, 1) : dim3(unsigned(G), p.qblocks), args,
               kModeScan, t2.start, t2.stop);
 
-  const TimerSpan t3 = timer_span(ctx, "bf_merge");
+  const TimerSpan t3 = timed ? timer_span(ctx, "bf_merge") : TimerSpan{};
   if (kp <= 64)
     hipExtLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
                           t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp,
                           static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   else
     hipExtLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start, t3.stop,
-                          0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, stride,
+                          0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, p.stride,
                           static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
   after_launch("bf_merge_kernel");
+}
+
+void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q,
+                      int64_t k, uint32_t* nbr, float* dist) {
+  const BfPlan p = plan_bf(ctx, ds, queries, q, k, nbr, dist);
+  ctx->ws_search.reserve(p.total);
+  bf_launch(ctx, ds, p, queries, q, k, nbr, dist, ctx->ws_search.as<char>(), true);
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point cvs_bf_search_noalloc: one
+// array per device, loaded with the code object and held until the process
+// ends.  In host code `scratch` only names the symbol; its device address
+// comes from hipGetSymbolAddress, once per device, with that device
+// current.  Every call on a device shares its array.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+char* scratch_on(int device) {
+  if (device < 0 || device >= kMaxDevices) fail(CVS_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    CVS_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) fail(CVS_ERR_RUNTIME, "scratch array has no device address");
+    g_scratch_ptr[device] = ptr;
+  }
+  return static_cast<char*>(g_scratch_ptr[device]);
 }
 
 }  // namespace
@@ -1216,6 +1278,20 @@ int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds, const float* qu
   return guarded([&] {
     bind(ctx);
     bf_search_device(ctx, ds, queries_dev, q, k, out_neighbors_dev, out_distances_dev);
+  });
+}
+
+int cvs_bf_search_noalloc(cvs_context* ctx, const cvs_dataset* ds, const float* queries_dev, int64_t q,
+                          int64_t k, uint32_t* out_neighbors_dev, float* out_distances_dev) {
+  return guarded([&] {
+    bind(ctx);
+    const BfPlan p = plan_bf(ctx, ds, queries_dev, q, k, out_neighbors_dev, out_distances_dev);
+    if (p.total > kScratchBytes)
+      fail(CVS_ERR_UNSUPPORTED, "cvs_bf_search_noalloc: this call needs " + std::to_string(p.total) +
+                                    " bytes of scratch, more than the " + std::to_string(kScratchBytes) +
+                                    " the library holds per device (use fewer queries or a smaller k)");
+    char* ws = scratch_on(ctx->device);
+    bf_launch(ctx, ds, p, queries_dev, q, k, out_neighbors_dev, out_distances_dev, ws, false);
   });
 }
 

@@ -87,8 +87,7 @@ struct cvs_context {
   bool timing = false;
   std::map<std::string, cvs::KernelTimer> timers;
   // Workspaces reused across calls (never shrink).
-  cvs::DeviceBuffer ws_queries;   // fp16 query tiles + query norms
-  cvs::DeviceBuffer ws_partial;   // per-workgroup candidate lists
+  cvs::DeviceBuffer ws_search;    // brute force: query tiles, thresholds, candidate lists
   cvs::DeviceBuffer ws_io;        // staging of host queries / results
   cvs::DeviceBuffer ws_teams;     // per-team lists of multi-team graph search
 };

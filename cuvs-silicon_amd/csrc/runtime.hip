@@ -219,8 +219,7 @@ int cvs_context_destroy(cvs_context* ctx) {
       }
       for (auto e : kv.second.pool) (void)hipEventDestroy(e);
     }
-    ctx->ws_queries.release();
-    ctx->ws_partial.release();
+    ctx->ws_search.release();
     ctx->ws_io.release();
     ctx->ws_teams.release();
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

@@ -135,6 +135,22 @@ int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds,
                         const float* queries_dev, int64_t q, int64_t k,
                         uint32_t* out_neighbors_dev, float* out_distances_dev);
 
+/* cvs_bf_search_async without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace (query tiles, thresholds, sample minima, candidate lists) lives in
+ * a 64 MiB array that the library holds on each device it runs on until the
+ * process ends; a call whose workspace would exceed it fails with
+ * CVS_ERR_UNSUPPORTED and a message giving the bytes needed (on 256
+ * compute units at D = 1024, every q up to 7,936 fits for k <= 10, 935 for
+ * k <= 24, 488 for k <= 48 and 332 for k <= 112).  Device pointers; enqueued on the context stream; no events.
+ * Calls that overlap on one GPU (several contexts or threads on the same
+ * device) share that array and race: serialise them. */
+#define CVS_BF_NOALLOC_SCRATCH_BYTES (64u << 20)
+int cvs_bf_search_noalloc(cvs_context* ctx, const cvs_dataset* ds,
+                          const float* queries_dev, int64_t q, int64_t k,
+                          uint32_t* out_neighbors_dev, float* out_distances_dev);
+
 /* ---- CAGRA graph search -------------------------------------------------- */
 
 /* Navigation (seed) nodes of an n-row graph index, as the reference's
