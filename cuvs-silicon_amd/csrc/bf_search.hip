@@ -53,18 +53,14 @@
 #include <string>
 #include <type_traits>
 
+#include "bf_common.hpp"
 #include "cvs_internal.hpp"
 #include "device_util.hpp"
 
 namespace cvs {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-#define CVS_INLINE __attribute__((always_inline))
+using namespace bf;
 
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kWaves = 4;
@@ -72,13 +68,6 @@ constexpr int kQB = 128;                                // queries per workgroup
 constexpr int kStageBlocks = 32;                        // 1 KiB blocks per stage
 constexpr int kStageVecs = kStageBlocks * 64;           // 16-byte vectors per stage
 constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 8 16-byte loads per thread and stage
-constexpr uint64_t kSentinel = ~0ull;
-// Buffer resource word 3 for raw (untyped) buffer access on gfx9-family
-// targets, and the non-temporal cache policy for the streamed dataset.
-constexpr int kRsrcWord3 = 0x00020000;
-constexpr int kAuxNT = 2;
-
-enum { kModeScan = 0, kModeSample = 1 };
 
 template <int KS>
 struct Cfg {
@@ -87,26 +76,6 @@ struct Cfg {
   static constexpr int RPU = 2 * kStageBlocks * 32 / KS;  // rows per 2-stage unit
   static constexpr int NF = TPS * 32;                     // norms per stage
   static_assert(KS >= 2 && KS <= 64, "k-steps per tile");
-};
-
-// List geometry per kp.  Each (workgroup, query) list is split into two
-// halves, one per lane holding that query (lanes l and l + 32 see different
-// rows of every tile), so each lane appends to its own half with a counter
-// in a register and no atomics.  A lane adds at most one key between two
-// fill checks; a half that fills up (HALF keys) rebalances the query's list
-// to its kp smallest keys, kp/2 per half, so the slack HALF - kp/2 sets how
-// many appends one compaction is amortized over.  Lists of kp <= 64 live in
-// LDS (bounded by the 160 KiB budget next to the stage buffers); kp = 128
-// lists (large k) live in global memory, one per (query, workgroup), since
-// 128 queries x 192 keys exceed the LDS budget and appends are rare once the
-// sampled threshold is in place.
-template <int KP, int MODE>
-struct Lists {
-  static constexpr bool GL = MODE == 0 && KP > 64;  // lists in global memory
-  static constexpr int HALF = MODE != 0 ? 1 : (KP == 16 ? 40 : (KP <= 64 ? 44 : 96));
-  static constexpr int CAP = 2 * HALF;
-  static constexpr int NS = (CAP + 63) / 64;  // list entries per lane in a compaction
-  static_assert(MODE != 0 || HALF >= KP / 2 + 8, "list slack");
 };
 
 struct ScanArgs {
@@ -129,76 +98,6 @@ struct ScanArgs {
   int64_t s_units;      // sample: number of sampled units
   int64_t s_stride;     // sample: unit stride
 };
-
-// Rewrites the two-half list of one query (c0 keys at list[0..), c1 keys at
-// list[half..)) as its kp smallest keys, the first kp/2 in half 0 and the
-// rest in half 1, and returns the order image of the kp-th smallest distance
-// (0xffffffff when c0 + c1 <= kp: every key is kept and the threshold stays).
-// All 64 lanes take part (list, c0 and c1 are wave-uniform); entry e lives in
-// lane e % 64, slot e / 64.  Every entry is read before any is written.
-template <int NS>
-__device__ __forceinline__ uint32_t compact_query(uint64_t* list, int half, uint32_t c0, uint32_t c1,
-                                                  int kp) {
-  const int lane = __lane_id();
-  const uint32_t cnt = c0 + c1;
-  bool v[NS];
-  uint64_t k[NS];
-  uint32_t h[NS], l[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint32_t e = uint32_t(lane + 64 * s);
-    v[s] = e < uint32_t(half) ? e < c0 : (e - uint32_t(half)) < c1;
-    k[s] = v[s] ? list[e] : kSentinel;
-    h[s] = uint32_t(k[s] >> 32);
-    l[s] = uint32_t(k[s]);
-  }
-  uint32_t kth_hi = 0xffffffffu, kth_lo = 0xffffffffu;
-  if (cnt > uint32_t(kp)) {
-    int need = kp;
-    uint32_t pre = 0;
-    for (int b = 31; b >= 0; --b) {
-      int c = 0;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && ((h[s] ^ pre) >> b) == 0));
-      if (c < need) {
-        need -= c;
-        pre |= 1u << b;
-      }
-    }
-    kth_hi = pre;
-    int lt = 0, eq = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      lt += popc(__ballot(v[s] && h[s] < kth_hi));
-      eq += popc(__ballot(v[s] && h[s] == kth_hi));
-    }
-    if (eq > kp - lt) {  // ties on the distance word: select on the row id
-      int need2 = kp - lt;
-      uint32_t pre2 = 0;
-      for (int b = 31; b >= 0; --b) {
-        int c = 0;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) c += popc(__ballot(v[s] && h[s] == kth_hi && ((l[s] ^ pre2) >> b) == 0));
-        if (c < need2) {
-          need2 -= c;
-          pre2 |= 1u << b;
-        }
-      }
-      kth_lo = pre2;
-    }
-  }
-  const int kh = kp / 2;
-  int base = 0;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const bool keep = v[s] && (h[s] < kth_hi || (h[s] == kth_hi && l[s] <= kth_lo));
-    const uint64_t m = __ballot(keep);
-    const int p = base + mbcnt(m);
-    if (keep) list[p < kh ? p : half + (p - kh)] = k[s];
-    base += popc(m);
-  }
-  return cnt > uint32_t(kp) ? kth_hi : 0xffffffffu;
-}
 
 template <int KS, int MODE, int KP>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
@@ -782,7 +681,7 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 template <int E>
 __device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s_cd, int kp, const float* rows,
-                                                 int64_t d, const float* qv, int64_t q, int64_t k,
+                                                 int64_t n, int64_t d, const float* qv, int64_t q, int64_t k,
                                                  uint32_t* out_nbr, float* out_dist) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(qv) & 15) == 0 &&
@@ -791,7 +690,11 @@ __device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     uint32_t id[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) id[u] = c + u < kp ? s_cid[c + u] : 0xffffffffu;
+    for (int u = 0; u < 4; ++u) {
+      // An id that is not a row (never produced by a scan) counts as empty.
+      id[u] = c + u < kp ? s_cid[c + u] : 0xffffffffu;
+      if (int64_t(id[u]) >= n) id[u] = 0xffffffffu;
+    }
     if (vec) {
       // Four 256-column chunks per pass, all loads issued before the first
       // is used (one HBM round trip per pass for d <= 1024).
@@ -841,7 +744,7 @@ __device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s
   for (int e = 0; e < E; ++e) {
     const int pos = e * 64 + lane;
     const uint32_t id = pos < kp ? s_cid[pos] : 0xffffffffu;
-    fin[e] = id == 0xffffffffu ? kSentinel : (uint64_t(ord_f32(s_cd[pos])) << 32) | id;
+    fin[e] = int64_t(id) >= n ? kSentinel : (uint64_t(ord_f32(s_cd[pos])) << 32) | id;
   }
   wave_sort_e<E>(fin);
 #pragma unroll
@@ -869,7 +772,7 @@ __device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __restrict__ part,
                                                               const uint64_t* __restrict__ lmin, int G, int kp,
-                                                              const float* __restrict__ rows, int64_t d,
+                                                              const float* __restrict__ rows, int64_t n, int64_t d,
                                                               const float* __restrict__ queries, int64_t k,
                                                               uint32_t* __restrict__ out_nbr,
                                                               float* __restrict__ out_dist) {
@@ -946,7 +849,7 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
     s_cid[lane] = (lane < kp && run[0] != kSentinel) ? uint32_t(run[0]) : 0xffffffffu;
   }
   __syncthreads();
-  rerank_and_write<1>(s_cid, s_cd, kp, rows, d, queries + q * d, q, k, out_nbr, out_dist);
+  rerank_and_write<1>(s_cid, s_cd, kp, rows, n, d, queries + q * d, q, k, out_nbr, out_dist);
 }
 
 // ---------------------------------------------------------------------------
@@ -967,7 +870,8 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
 template <int E>
 __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restrict__ part,
                                                        const uint64_t* __restrict__ lmin, int G, int kp,
-                                                       int stride, const float* __restrict__ rows, int64_t d,
+                                                       int stride, const float* __restrict__ rows, int64_t n,
+                                                       int64_t d,
                                                        const float* __restrict__ queries, int64_t k,
                                                        uint32_t* __restrict__ out_nbr,
                                                        float* __restrict__ out_dist) {
@@ -1039,7 +943,7 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
     }
   }
   __syncthreads();
-  rerank_and_write<E>(s_cid, s_cd, kp, rows, d, queries + q * d, q, k, out_nbr, out_dist);
+  rerank_and_write<E>(s_cid, s_cd, kp, rows, n, d, queries + q * d, q, k, out_nbr, out_dist);
 }
 
 // ---------------------------------------------------------------------------
@@ -1100,7 +1004,9 @@ struct BfPlan {
   int kp = 0;              // candidates per (dataset range, query)
   unsigned qblocks = 0;    // 128-query blocks
   bool large_batch = false;
-  int G = 0;               // dataset ranges of the scan
+  bool gemm = false;       // large batch, kp = 128: the register-blocked scan (bf_gemm.hip)
+  int gemm_wg = 0;         // its workgroups
+  int G = 0;               // candidate lists per query: dataset ranges of the streaming scan
   int stride = 0;          // keys per (query, range) list in the workspace
   int64_t s_units = 0, s_stride = 0;  // threshold sample
   int Gs = 0;              // dataset ranges of the sample
@@ -1139,6 +1045,16 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   if (global_lists && G > 128) G = 128;
   if (p.large_batch && G > 32) G = 32;
   if (int64_t(G) > p.n_units) G = int(p.n_units);
+  // Large batches with kp = 128 run the register-blocked scan: persistent
+  // workgroups over (query block, row block) units, n_lists lists per query.
+  if (p.large_batch) {
+    const GemmPlan gp = plan_gemm_scan(p.ks, p.kp, ds->n_tiles / 4, int((q + 31) / 32), ctx->compute_units);
+    if (gp.ok) {
+      p.gemm = true;
+      p.gemm_wg = gp.n_wg;
+      G = gp.n_lists;
+    }
+  }
   p.G = G;
   p.stride = global_lists ? Lists<128, kModeScan>::CAP : p.kp;
 
@@ -1215,20 +1131,37 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
   after_launch("bf_select_kernel");
 
   const TimerSpan t2 = timed ? timer_span(ctx, "bf_scan") : TimerSpan{};
-  args.n_ranges = G;
-  args.qb_fast = p.large_batch ? 1 : 0;
-  launch_scan(ctx, p.ks, p.large_batch ? dim3(unsigned(G) * p.qblocks, 1) : dim3(unsigned(G), p.qblocks), args,
-              kModeScan, t2.start, t2.stop);
+  if (p.gemm) {
+    GemmArgs ga{};
+    ga.tiles = args.tiles;
+    ga.norms = ds->norms;
+    ga.n_rt = ds->n_tiles / 4;
+    ga.ks = p.ks;
+    ga.qtiles = qtiles;
+    ga.qnorms = qnorms;
+    ga.nq = int(q);
+    ga.n_qtiles = int(p.q_tiles);
+    ga.thr0 = thr0;
+    ga.part = part;
+    ga.lmin = lmin;
+    ga.n_lists = G;
+    launch_gemm_scan(ctx, ga, p.gemm_wg, t2.start, t2.stop);
+  } else {
+    args.n_ranges = G;
+    args.qb_fast = p.large_batch ? 1 : 0;
+    launch_scan(ctx, p.ks, p.large_batch ? dim3(unsigned(G) * p.qblocks, 1) : dim3(unsigned(G), p.qblocks), args,
+                kModeScan, t2.start, t2.stop);
+  }
 
   const TimerSpan t3 = timed ? timer_span(ctx, "bf_merge") : TimerSpan{};
   if (kp <= 64)
     hipExtLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
                           t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp,
-                          static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
+                          static_cast<const float*>(ds->rows), ds->n, ds->d, queries, k, nbr, dist);
   else
     hipExtLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start, t3.stop,
                           0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, p.stride,
-                          static_cast<const float*>(ds->rows), ds->d, queries, k, nbr, dist);
+                          static_cast<const float*>(ds->rows), ds->n, ds->d, queries, k, nbr, dist);
   after_launch("bf_merge_kernel");
 }
 

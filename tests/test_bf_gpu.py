@@ -118,8 +118,12 @@ def test_random_shapes(ctx, oracle, n, d, q, k):
 
 @pytest.mark.parametrize("n,d,q,k", [
     (30000, 64, 1500, 10),    # > 8 query blocks: range-major launch, LDS lists
-    (30000, 64, 1500, 100),   # range-major launch, global-memory lists
-    (8000, 1024, 1100, 64),
+    (30000, 64, 1500, 100),   # range-major launch, global-memory lists (8 k-steps or fewer)
+    (8000, 1024, 1100, 64),   # register-blocked scan (bf_gemm.hip): 3 query blocks
+    (3000, 128, 2000, 100),   # 8 k-steps, one 128-row block per span
+    (500, 256, 1200, 100),    # half the spans empty
+    (20000, 1000, 1500, 100), # d padded to 1024
+    (20000, 512, 5000, 112),  # 10 query blocks: two per XCD for XCDs 0 and 1, largest k
 ])
 def test_large_batches(ctx, oracle, n, d, q, k):
     rng = np.random.default_rng(q + k)
