@@ -1058,14 +1058,16 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   p.G = G;
   p.stride = global_lists ? Lists<128, kModeScan>::CAP : p.kp;
 
-  // Sample: 32,768 rows for small batches, 65,536 for large ones, in whole
+  // Sample: 16,384 rows for small batches, 65,536 for large ones, in whole
   // units, evenly strided, over Gs workgroups; 2 minima per (query,
   // workgroup).  The initial threshold then sits near rank kp * n / sample
   // of each query's distances, so a workgroup's lists see about
-  // kp * n / (sample * G) appends per query over its range: large batches
-  // (kp = 128 and only 32 dataset ranges) need the larger sample to keep
-  // appends and list compactions off the scan's critical path.
-  p.s_units = (p.large_batch ? 65536 : 32768) / rpu;
+  // kp * n / (sample * G) appends per query over its range.  Small batches
+  // are bound by the scan's HBM stream, where a few more appends cost
+  // nothing and the sample's own latency is what shows; large batches
+  // (kp = 128 lists) need the larger sample to keep appends and list
+  // compactions off the scan's critical path.
+  p.s_units = (p.large_batch ? 65536 : 16384) / rpu;
   if (p.s_units < 1) p.s_units = 1;
   if (p.s_units > p.n_units) p.s_units = p.n_units;
   p.s_stride = p.n_units / p.s_units;
