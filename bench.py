@@ -819,6 +819,27 @@ def run_cagra_build(args) -> int:
                            "achieved_gbs": e_bytes / (ems * 1e-3) / 1e9 if ems else None,
                            "hbm_frac": e_bytes / (ems * 1e-3) / 1e9 / HBM_PEAK_GBS if ems else None},
     }
+    # The same build with the final intermediate lists re-ranked by exact
+    # fp32 distances before pruning (cvs_cagra_build_ex): time and recall
+    # against the fp16-ranked build above.
+    if not args.no_recall:
+        log("building with the fp32 re-score before pruning")
+        g2 = cvs.DeviceArray(ctx, (n, args.degree), np.uint32)
+        t = time.perf_counter()
+        _, bst2 = ctx.cagra_build(drows, intermediate_degree=2 * args.degree, graph_degree=args.degree, out=g2,
+                                  rescore_fp32=True)
+        wall2 = time.perf_counter() - t
+        idx2 = ctx.cagra_index(drows, g2, nav)
+        rec2 = {}
+        for it in (args.itopk, 512):
+            r_on, _ = idx.search(qs, k, itopk_size=it)
+            r_rs, _ = idx2.search(qs, k, itopk_size=it)
+            rec2[f"itopk {it}"] = {"fp16_ranked": recall_at_k(r_on, gt, k), "fp32_rescored": recall_at_k(r_rs, gt, k)}
+        idx2.close()
+        g2.free()
+        out["rescore_fp32"] = {"seconds": wall2, "seconds_rescore": bst2["seconds_rescore"],
+                               "iterations": bst2["iterations"], "recall_at_10": rec2, "queries": q}
+        log(json.dumps(out["rescore_fp32"]))
     # The reference's own build algorithm at this size, on the GPU, for
     # comparison (above 200,000 rows: IVF k-means, product-quantised
     # per-cluster seeding re-scored exactly, one bucketing round, no

@@ -93,7 +93,7 @@ class BuildStats(ctypes.Structure):
                 ("final_update_rate", c_double), ("seconds_seed", c_double), ("seconds_descent", c_double),
                 ("seconds_prune", c_double), ("seconds_total", c_double), ("join_ms", c_double),
                 ("join_bytes", c_double), ("join_members", c_uint64), ("updates_emitted", c_uint64),
-                ("updates_kept", c_uint64), ("insertions", c_uint64)]
+                ("updates_kept", c_uint64), ("insertions", c_uint64), ("seconds_rescore", c_double)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -101,6 +101,16 @@ class BuildStats(ctypes.Structure):
 
 _SIGNATURES["cvs_cagra_build"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_uint32, c_uint32,
                                           c_float, c_uint64, c_void_p, c_int, POINTER(BuildStats)])
+
+
+class BuildOptions(ctypes.Structure):
+    """cvs_build_options (include/cvs_hip.h)."""
+    _fields_ = [("rescore_fp32", c_int)]
+
+
+_SIGNATURES["cvs_cagra_build_ex"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_uint32,
+                                             c_uint32, c_float, c_uint64, POINTER(BuildOptions), c_void_p, c_int,
+                                             POINTER(BuildStats)])
 
 _SIGNATURES["cvs_bf_search_noalloc"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p])
 _SIGNATURES["cvs_cagra_nav_nodes"] = (c_int, [c_int64, c_void_p, POINTER(c_int64)])
@@ -295,9 +305,12 @@ class Context:
         return host, st.as_dict()
 
     def cagra_build(self, rows, intermediate_degree: int = 128, graph_degree: int = 64, max_iterations: int = 20,
-                    termination_threshold: float = 0.001, seed: int = DEFAULT_BUILD_SEED, out: "DeviceArray" = None):
+                    termination_threshold: float = 0.001, seed: int = DEFAULT_BUILD_SEED, out: "DeviceArray" = None,
+                    rescore_fp32: bool = False):
         """GPU graph build.  Returns (graph, stats): graph is a host uint32
-        array (n, g), or `out` (a device array of that shape) when given."""
+        array (n, g), or `out` (a device array of that shape) when given.
+        rescore_fp32 re-ranks the final intermediate lists by exact fp32
+        distances before pruning (cvs_cagra_build_ex)."""
         st = BuildStats()
         if isinstance(rows, DeviceArray):
             n, d = rows.shape
@@ -314,9 +327,15 @@ class Context:
         else:
             host = np.empty((n, max(g, 1)), np.uint32)
             gptr, gdev = host.ctypes.data_as(c_void_p), 0
-        _check(load().cvs_cagra_build(self.handle, rptr, n, d, rdev, int(intermediate_degree), int(graph_degree),
-                                      int(max_iterations), float(termination_threshold), int(seed), gptr, gdev,
-                                      byref(st)))
+        if rescore_fp32:
+            opts = BuildOptions(rescore_fp32=1)
+            _check(load().cvs_cagra_build_ex(self.handle, rptr, n, d, rdev, int(intermediate_degree),
+                                             int(graph_degree), int(max_iterations), float(termination_threshold),
+                                             int(seed), byref(opts), gptr, gdev, byref(st)))
+        else:
+            _check(load().cvs_cagra_build(self.handle, rptr, n, d, rdev, int(intermediate_degree),
+                                          int(graph_degree), int(max_iterations), float(termination_threshold),
+                                          int(seed), gptr, gdev, byref(st)))
         return (out if out is not None else host), st.as_dict()
 
 

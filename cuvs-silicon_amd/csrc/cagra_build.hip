@@ -628,6 +628,64 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
   }
 }
 
+// Per node (one workgroup): exact fp32 squared L2 distance to each entry of
+// its list (a 16-lane team per entry, summing over the fp32 rows), then the
+// list re-keyed with those distances and re-sorted by (distance, id), so
+// that the pruning ranks neighbours by exact distances instead of the build's
+// fp16-input expanded-form estimates.
+template <int E>
+__global__ __launch_bounds__(256) void rescore_kernel(const float* __restrict__ rows, int64_t d, BuildArgs a) {
+  __shared__ float s_d[kMaxKd];
+  const int tid = threadIdx.x, team = tid >> 4, tp = tid & 15, lane = tid & 63;
+  const int64_t u = blockIdx.x;
+  uint64_t* lst = a.lists + u * a.kp;
+  const float* x = rows + u * d;
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
+  for (int e = team; e < a.kd; e += 16) {
+    const uint64_t key = lst[e];
+    float acc = INFINITY;
+    if (key != kEmpty) {
+      const float* y = rows + int64_t(key_id(key)) * d;
+      float sum = 0.f;
+      if (vec) {
+#pragma unroll 4
+        for (int64_t i = 4 * int64_t(tp); i < d; i += 64) {
+          const float4 xa = *reinterpret_cast<const float4*>(x + i);
+          const float4 ya = *reinterpret_cast<const float4*>(y + i);
+          const float t0 = xa.x - ya.x, t1 = xa.y - ya.y, t2 = xa.z - ya.z, t3 = xa.w - ya.w;
+          sum += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+        }
+      } else {
+        for (int64_t i = tp; i < d; i += 16) {
+          const float t = x[i] - y[i];
+          sum += t * t;
+        }
+      }
+      sum += xor_lanes_f(sum, 8);
+      sum += xor_lanes_f(sum, 4);
+      sum += xor_lanes_f(sum, 2);
+      sum += xor_lanes_f(sum, 1);
+      acc = sum;
+    }
+    if (tp == 0) s_d[e] = acc;
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    const uint64_t key = p < a.kd ? lst[p] : kEmpty;
+    v[e] = key == kEmpty ? kEmpty : (uint64_t(ord_f32(s_d[p])) << 32) | (key & 0xffffffffull);
+  }
+  wave_sort_e<E>(v);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int p = e * 64 + lane;
+    if (p < a.kd) lst[p] = v[e];
+  }
+}
+
 // Lists -> id rows (n x kd) for pruning.
 __global__ __launch_bounds__(256) void list_ids_kernel(const uint64_t* __restrict__ lists, int64_t n, int kd, int kp,
                                                        uint32_t* __restrict__ ids) {
@@ -671,22 +729,41 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   // Edge u -> v_j is detourable via v_i when max(i, rank of v_j in v_i's list) < j.
-  for (int i = 0; i < valid_n; ++i) {
-    const uint32_t vi = s_nb[wave][i];
-    const uint32_t* li = ids + int64_t(vi) * kd;
-    for (int p = lane; p < kd; p += 64) {
-      const uint32_t w = li[p];
-      if (w == kInvalid) continue;
-      uint32_t s = (w * 0x9E3779B1u) >> 23;
-      for (;;) {
-        const uint32_t cur = hk[s];
-        if (cur == kInvalid) break;
-        if (cur == w) {
-          const int j = int(hv[s]);
-          if (i < j && p < j) atomicAdd(&s_det[wave][j], 1u);
-          break;
+  // The lists of U neighbours are loaded together, so that their latencies
+  // overlap instead of adding up neighbour by neighbour.
+  constexpr int U = 4;
+  for (int i0 = 0; i0 < valid_n; i0 += U) {
+    uint32_t wv[U][E];
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu) {
+      const uint32_t vi = s_nb[wave][i0 + uu < valid_n ? i0 + uu : i0];
+      const uint32_t* li = ids + int64_t(vi) * kd;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int p = e * 64 + lane;
+        wv[uu][e] = p < kd ? li[p] : kInvalid;
+      }
+    }
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu) {
+      const int i = i0 + uu;
+      if (i >= valid_n) break;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int p = e * 64 + lane;
+        const uint32_t w = wv[uu][e];
+        if (w == kInvalid) continue;
+        uint32_t s = (w * 0x9E3779B1u) >> 23;
+        for (;;) {
+          const uint32_t cur = hk[s];
+          if (cur == kInvalid) break;
+          if (cur == w) {
+            const int j = int(hv[s]);
+            if (i < j && p < j) atomicAdd(&s_det[wave][j], 1u);
+            break;
+          }
+          s = (s + 1u) & 511u;
         }
-        s = (s + 1u) & 511u;
       }
     }
   }
@@ -722,46 +799,72 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
 }
 
 // Per node (one wave): closest g/2 kept edges, then up to g/2 reverse
-// edges, then the remaining kept edges; no duplicates.
+// edges, then the remaining kept edges, then the remaining reverse edges,
+// until g; no duplicates.  Each phase checks its candidates against a wave
+// hash set of the ids placed so far and takes the new ones in order (ballot
+// prefix ranks).  The candidates of one phase are distinct (kept edges come
+// from a duplicate-free list, and a node appears at most once in another's
+// reverse list), so a phase's checks need not see its own insertions.
 __global__ __launch_bounds__(256) void merge_reverse_kernel(const uint32_t* __restrict__ kept,
                                                             const uint32_t* __restrict__ rev,
                                                             const uint32_t* __restrict__ rev_cnt, int64_t n, int g,
                                                             uint32_t* __restrict__ out) {
-  __shared__ uint32_t s_out[4][1024];
+  constexpr int kHash = 1024;  // at most g <= 256 ids are placed: a quarter full at most
+  __shared__ uint32_t s_hash[4][kHash];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t u = int64_t(blockIdx.x) * 4 + wave;
   if (u >= n) return;
-  uint32_t* so = s_out[wave];
-  if (lane == 0) {
-    const uint32_t* kr = kept + u * g;
-    const uint32_t* rr = rev + u * g;
-    const int rc = int(min(rev_cnt[u], uint32_t(g)));
-    int m = 0;
-    auto has = [&](uint32_t w) {
-      for (int i = 0; i < m; ++i)
-        if (so[i] == w) return true;
-      return false;
-    };
-    const int half = g / 2;
-    for (int i = 0; i < half; ++i)
-      if (kr[i] != kInvalid && !has(kr[i])) so[m++] = kr[i];
-    int added = 0;
-    for (int i = 0; i < rc && added < g - half && m < g; ++i)
-      if (!has(rr[i])) {
-        so[m++] = rr[i];
-        ++added;
-      }
-    for (int i = half; i < g && m < g; ++i)
-      if (kr[i] != kInvalid && !has(kr[i])) so[m++] = kr[i];
-    // Reverse edges that duplicated a kept edge leave room: fill it with the
-    // remaining reverse edges.
-    for (int i = 0; i < rc && m < g; ++i)
-      if (!has(rr[i])) so[m++] = rr[i];
-    for (int i = m; i < g; ++i) so[i] = kInvalid;
-  }
+  uint32_t* hs = s_hash[wave];
+  for (int i = lane; i < kHash; i += 64) hs[i] = kInvalid;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  for (int i = lane; i < g; i += 64) out[u * g + i] = so[i];
+  auto has = [&](uint32_t w) {
+    uint32_t s = (w * 0x9E3779B1u) >> 22;
+    for (;;) {
+      const uint32_t cur = hs[s];
+      if (cur == w) return true;
+      if (cur == kInvalid) return false;
+      s = (s + 1u) & uint32_t(kHash - 1);
+    }
+  };
+  auto insert = [&](uint32_t w) {
+    uint32_t s = (w * 0x9E3779B1u) >> 22;
+    while (atomicCAS(&hs[s], kInvalid, w) != kInvalid) s = (s + 1u) & uint32_t(kHash - 1);
+  };
+  const uint32_t* kr = kept + u * g;
+  const uint32_t* rr = rev + u * g;
+  const int rc = int(min(rev_cnt[u], uint32_t(g)));
+  const int half = g / 2;
+  uint32_t* dst = out + u * g;
+  int m = 0;
+  // Takes, in index order, candidates src[i] for i in [lo, hi) that are valid
+  // and new, until `quota` are taken or the list is full.
+  auto phase = [&](const uint32_t* src, int lo, int hi, int quota) {
+    int taken = 0;
+    for (int c = lo; c < hi && taken < quota && m < g; c += 64) {
+      const int i = c + lane;
+      const uint32_t w = i < hi ? src[i] : kInvalid;
+      const bool cand = w != kInvalid && !has(w);
+      const uint64_t mask = __ballot(cand);
+      const int rank = int(mbcnt(mask));
+      const int room = min(quota - taken, g - m);
+      const bool take = cand && rank < room;
+      if (take) {
+        dst[m + rank] = w;
+        insert(w);
+      }
+      const int nt = min(int(popc(mask)), room);
+      m += nt;
+      taken += nt;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    }
+  };
+  phase(kr, 0, half, g);
+  phase(rr, 0, rc, g - half);
+  phase(kr, half, g, g);
+  phase(rr, 0, rc, g);
+  for (int i = m + lane; i < g; i += 64) dst[i] = kInvalid;
 }
 
 template <typename K>
@@ -802,7 +905,8 @@ double elapsed_s(std::chrono::steady_clock::time_point t0) {
 void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
                         uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
                         float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
-                        cvs_build_stats* stats) {
+                        const cvs_build_options* opts, cvs_build_stats* stats) {
+  const bool rescore = opts && opts->rescore_fp32;
   const auto t_start = std::chrono::steady_clock::now();
   if (!rows || n <= 0 || d <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "dataset must be non-null and non-empty");
   if (!out_graph) fail(CVS_ERR_INVALID_ARGUMENT, "null out_graph");
@@ -824,17 +928,16 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   DevMem mem;
   _Float16* x16 = mem.alloc<_Float16>(size_t(n) * dp);
   float* norms = mem.alloc<float>(size_t(n));
-  {
-    const float* src = rows;
-    if (!rows_on_device) {
-      float* tmp = mem.alloc<float>(size_t(n) * d);
-      CVS_HIP(hipMemcpyAsync(tmp, rows, size_t(n) * d * sizeof(float), hipMemcpyHostToDevice, st));
-      src = tmp;
-    }
-    hipLaunchKernelGGL(to_half_rows_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, src, n, d, dp, x16,
-                       norms);
-    after_launch("to_half_rows_kernel");
+  // fp32 rows on the device (kept for the re-score).
+  const float* rows32 = rows;
+  if (!rows_on_device) {
+    float* tmp = mem.alloc<float>(size_t(n) * d);
+    CVS_HIP(hipMemcpyAsync(tmp, rows, size_t(n) * d * sizeof(float), hipMemcpyHostToDevice, st));
+    rows32 = tmp;
   }
+  hipLaunchKernelGGL(to_half_rows_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, rows32, n, d, dp, x16,
+                     norms);
+  after_launch("to_half_rows_kernel");
   // Random permutations: the reference's LCG Fisher-Yates
   // (src/metal_context.mm:802-810); later rounds continue the sequence.
   std::vector<uint32_t> perm(static_cast<size_t>(n));
@@ -936,6 +1039,19 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   s.join_bytes = double(s.join_members) * double(dp) * 2.0;
   s.seconds_descent = elapsed_s(t_nd);
 
+  // Optional exact fp32 re-score of the final lists.
+  if (rescore) {
+    const auto t_rs = std::chrono::steady_clock::now();
+    switch (e_slots) {
+      case 1: hipLaunchKernelGGL(rescore_kernel<1>, dim3(unsigned(n)), dim3(256), 0, st, rows32, d, a); break;
+      case 2: hipLaunchKernelGGL(rescore_kernel<2>, dim3(unsigned(n)), dim3(256), 0, st, rows32, d, a); break;
+      default: hipLaunchKernelGGL(rescore_kernel<4>, dim3(unsigned(n)), dim3(256), 0, st, rows32, d, a); break;
+    }
+    after_launch("rescore_kernel");
+    CVS_HIP(hipStreamSynchronize(st));
+    s.seconds_rescore = elapsed_s(t_rs);
+  }
+
   // Prune + reverse edges.
   const auto t_pr = std::chrono::steady_clock::now();
   uint32_t* ids = mem.alloc<uint32_t>(size_t(n) * kd);
@@ -980,7 +1096,18 @@ int cvs_cagra_build(cvs_context* ctx, const float* rows, int64_t n, int64_t d, i
   return guarded([&] {
     bind(ctx);
     cagra_build_device(ctx, rows, n, d, rows_on_device, intermediate_degree, graph_degree, max_iterations,
-                       termination_threshold, seed, out_graph, graph_on_device, stats);
+                       termination_threshold, seed, out_graph, graph_on_device, nullptr, stats);
+  });
+}
+
+int cvs_cagra_build_ex(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                       uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
+                       float termination_threshold, uint64_t seed, const cvs_build_options* options,
+                       uint32_t* out_graph, int graph_on_device, cvs_build_stats* stats) {
+  return guarded([&] {
+    bind(ctx);
+    cagra_build_device(ctx, rows, n, d, rows_on_device, intermediate_degree, graph_degree, max_iterations,
+                       termination_threshold, seed, out_graph, graph_on_device, options, stats);
   });
 }
 

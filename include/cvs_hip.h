@@ -249,6 +249,7 @@ typedef struct cvs_build_stats {
   uint64_t updates_emitted;     /* candidate neighbours the joins appended to update bins */
   uint64_t updates_kept;        /* bin entries left after deduplication against the lists */
   uint64_t insertions;          /* entries that entered a list */
+  double seconds_rescore;       /* exact fp32 re-score of the final lists (cvs_cagra_build_ex), else 0 */
 } cvs_build_stats;
 
 /* Builds a fixed-degree search graph of an n x d fp32 dataset on the GPU:
@@ -265,6 +266,25 @@ int cvs_cagra_build(cvs_context* ctx, const float* rows, int64_t n, int64_t d, i
                     uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
                     float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
                     cvs_build_stats* stats);
+
+/* Options of cvs_cagra_build_ex. */
+typedef struct cvs_build_options {
+  /* 1: before pruning, re-score every node's intermediate list with exact
+   * fp32 squared L2 distances from the fp32 rows and re-sort it, so that the
+   * rank-based pruning orders neighbours as the reference's fp32 build does
+   * (src/metal_context.mm:289-914 ranks by BLAS fp32 distances); 0: rank by
+   * the build's fp16-input estimates, as cvs_cagra_build does.  Reads
+   * n * intermediate_degree fp32 rows once more. */
+  int rescore_fp32;
+} cvs_build_options;
+
+/* cvs_cagra_build with options (NULL: those of cvs_cagra_build).  No
+ * counterpart in the reference, whose build has no such knob; it serves
+ * callers that want the exact-distance ranking at a known cost. */
+int cvs_cagra_build_ex(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
+                       uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
+                       float termination_threshold, uint64_t seed, const cvs_build_options* options,
+                       uint32_t* out_graph, int graph_on_device, cvs_build_stats* stats);
 
 /* Phase timings and counters of one cvs_cagra_build_reference call. */
 typedef struct cvs_ref_build_stats {
