@@ -729,9 +729,11 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   // Edge u -> v_j is detourable via v_i when max(i, rank of v_j in v_i's list) < j.
-  // The lists of U neighbours are loaded together, so that their latencies
-  // overlap instead of adding up neighbour by neighbour.
-  constexpr int U = 4;
+  // The lists of U neighbours are loaded together, and the first hash slot
+  // of every entry is read before any is resolved, so that memory and LDS
+  // latencies overlap; the table is at most a quarter full, so a further
+  // probe is rare.
+  constexpr int U = 8;
   for (int i0 = 0; i0 < valid_n; i0 += U) {
     uint32_t wv[U][E];
 #pragma unroll
@@ -741,28 +743,33 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int p = e * 64 + lane;
-        wv[uu][e] = p < kd ? li[p] : kInvalid;
+        wv[uu][e] = p < kd && i0 + uu < valid_n ? li[p] : kInvalid;
       }
     }
+    uint32_t slot[U][E], cur[U][E];
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        slot[uu][e] = (wv[uu][e] * 0x9E3779B1u) >> 23;
+        cur[uu][e] = hk[slot[uu][e]];
+      }
 #pragma unroll
     for (int uu = 0; uu < U; ++uu) {
       const int i = i0 + uu;
-      if (i >= valid_n) break;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int p = e * 64 + lane;
         const uint32_t w = wv[uu][e];
         if (w == kInvalid) continue;
-        uint32_t s = (w * 0x9E3779B1u) >> 23;
-        for (;;) {
-          const uint32_t cur = hk[s];
-          if (cur == kInvalid) break;
-          if (cur == w) {
-            const int j = int(hv[s]);
-            if (i < j && p < j) atomicAdd(&s_det[wave][j], 1u);
-            break;
-          }
+        uint32_t s = slot[uu][e], c = cur[uu][e];
+        while (c != kInvalid && c != w) {
           s = (s + 1u) & 511u;
+          c = hk[s];
+        }
+        if (c == w) {
+          const int j = int(hv[s]);
+          if (i < j && p < j) atomicAdd(&s_det[wave][j], 1u);
         }
       }
     }

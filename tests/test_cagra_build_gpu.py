@@ -74,13 +74,18 @@ def test_neighbour_quality_and_convergence(ctx, oracle):
     assert share > 0.9
 
 
-@pytest.mark.parametrize("n,d,g,itopk", [(8000, 128, 32, 64), (5000, 1024, 64, 64)])
-def test_downstream_recall_at_least_reference(ctx, oracle, n, d, g, itopk):
+@pytest.mark.parametrize("n,d,g,itopk,rescore", [(8000, 128, 32, 64, False), (5000, 1024, 64, 64, False),
+                                                 (5000, 1024, 64, 64, True), (6000, 99, 32, 64, True)])
+def test_downstream_recall_at_least_reference(ctx, oracle, n, d, g, itopk, rescore):
+    """rescore: the final intermediate lists re-ranked by exact fp32
+    distances before pruning (cvs_cagra_build_ex; d = 99 takes its
+    scalar path)."""
     rng = np.random.default_rng(n + d)
     base = clustered(rng, n, d)
     qs = clustered(np.random.default_rng(7), 300, d)
-    graph, st = ctx.cagra_build(base, intermediate_degree=2 * g, graph_degree=g)
+    graph, st = ctx.cagra_build(base, intermediate_degree=2 * g, graph_degree=g, rescore_fp32=rescore)
     check_graph(graph, n, g)
+    assert (st["seconds_rescore"] > 0) == rescore
     nav = oracle.cagra_nav_nodes(n)
     gt, _ = oracle.bf_exact(base, qs, 10, threads=16)
     ours, _ = ctx.cagra_index(base, graph, nav).search(qs, 10, itopk_size=itopk)
