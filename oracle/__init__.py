@@ -1,7 +1,8 @@
 """ctypes access to the oracle (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this package, and only as the checker.
+import this package, and only to check results against it (or, in
+bench.py, to time the reference CPU path).
 
 - liboracle.so: the C restatement of the reference search path (oracle.h).
 - _ref/libref.so: the reference's own CPU sources compiled in place

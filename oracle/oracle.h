@@ -2,8 +2,9 @@
  * oracle.h - CPU restatement of the reference's search path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the
- * checker; the product (libcvs_hip, libcuvs_silicon) never links it.
+ * cpu_baseline leg of bench.py may load this library, and only to check
+ * results against it; the product (libcvs_hip, libcuvs_silicon) never
+ * links it.
  *
  * Each function cites the reference lines it restates.  Pinning (how each
  * function is itself checked) is listed per function; see tests/test_oracle.py.
