@@ -172,8 +172,14 @@ def calibrate_copy(mib: int) -> int:
     end.record()
     torch.cuda.synchronize()
     copy_gbs = 2 * n * 4 * reps / (start.elapsed_time(end) * 1e-3) / 1e9
+    # The library's own streaming read (cvs_calibrate_stream_read): each
+    # workgroup reads one contiguous share with non-temporal 16-byte loads,
+    # as the brute-force scan reads its row range.
+    cvs = load_package()
+    with cvs.Context(0) as ctx:
+        stream = {str(g): ctx.calibrate_stream_read(n * 4, g) for g in (256, 512, 1024, 2048, 4096, 8192)}
     print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": 5, "read_gbs": read_gbs,
-                      "copy_gbs_read_plus_write": copy_gbs}), flush=True)
+                      "copy_gbs_read_plus_write": copy_gbs, "stream_read_gbs_by_workgroups": stream}), flush=True)
     return 0
 
 

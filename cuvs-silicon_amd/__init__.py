@@ -43,6 +43,7 @@ _SIGNATURES = {
     "cvs_reset_dispatch_count": (None, []),
     "cvs_device_count": (c_int, [POINTER(c_int)]),
     "cvs_context_create": (c_int, [c_int, POINTER(c_void_p)]),
+    "cvs_calibrate_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_int, POINTER(c_double)]),
     "cvs_context_destroy": (c_int, [c_void_p]),
     "cvs_context_synchronize": (c_int, [c_void_p]),
     "cvs_context_device_info": (c_int, [c_void_p, c_char_p, c_size_t, POINTER(c_int), POINTER(c_int64)]),
@@ -266,6 +267,12 @@ class Context:
         mem = c_int64(0)
         _check(load().cvs_context_device_info(self.handle, name, 256, byref(cu), byref(mem)))
         return {"name": name.value.decode(), "compute_units": cu.value, "total_mem_bytes": mem.value}
+
+    def calibrate_stream_read(self, nbytes: int, workgroups: int, reps: int = 20) -> float:
+        """Achievable streaming-read rate in GB/s (C: cvs_calibrate_stream_read)."""
+        gbs = c_double(0)
+        _check(load().cvs_calibrate_stream_read(self.handle, int(nbytes), int(workgroups), int(reps), byref(gbs)))
+        return gbs.value
 
     def set_timing(self, enable: bool) -> None:
         _check(load().cvs_context_set_timing(self.handle, 1 if enable else 0))

@@ -154,6 +154,50 @@ void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, 
   after_launch("to_tiles_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Device calibration: the achievable HBM streaming-read rate, the bound a
+// streaming kernel is measured against next to the nominal 8 TB/s.  Each
+// workgroup reads one contiguous share of the buffer (as the brute-force
+// scan reads its row range) in steps of 32 KiB, 8 non-temporal 16-byte loads
+// per thread, with two steps in flight (two register sets, each reloaded two
+// steps ahead as soon as it is consumed, as the scan keeps its stages).
+// Loads are buffer loads over the share, so a step past its end reads zeros
+// without a memory access and no load sits behind a branch.  The XOR of the
+// data decides a store that never happens in practice but keeps every load.
+// ---------------------------------------------------------------------------
+typedef uint32_t stream_vec __attribute__((ext_vector_type(4)));
+constexpr int kStreamLoads = 8;
+constexpr uint64_t kStreamStepVecs = uint64_t(kStreamLoads) * 256;  // 16-byte vectors per step
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const stream_vec* __restrict__ src, uint64_t steps_per_wg,
+                                                          uint32_t* __restrict__ sink) {
+  const uint32_t step_bytes = uint32_t(kStreamStepVecs * 16);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<stream_vec*>(src + uint64_t(blockIdx.x) * steps_per_wg * kStreamStepVecs), 0,
+      int(uint32_t(steps_per_wg) * step_bytes), 0x00020000);
+  auto load = [&](stream_vec (&v)[kStreamLoads], uint64_t step) {
+    const uint32_t off = uint32_t(step) * step_bytes + threadIdx.x * 16u;
+#pragma unroll
+    for (int i = 0; i < kStreamLoads; ++i)
+      v[i] = __builtin_bit_cast(stream_vec, __builtin_amdgcn_raw_buffer_load_b128(rs, off + uint32_t(i) * 4096u, 0, 2));
+  };
+  uint32_t acc = 0;
+  auto consume = [&](const stream_vec (&v)[kStreamLoads]) {
+#pragma unroll
+    for (int i = 0; i < kStreamLoads; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  };
+  stream_vec a[kStreamLoads], b[kStreamLoads];
+  load(a, 0);
+  load(b, 1);
+  for (uint64_t s = 0; s < steps_per_wg; s += 2) {
+    consume(a);
+    load(a, s + 2);
+    consume(b);
+    load(b, s + 3);
+  }
+  if (acc == 0x9E3779B9u) sink[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
 }  // namespace cvs
 
 using namespace cvs;
@@ -276,6 +320,53 @@ int cvs_context_kernel_time(cvs_context* ctx, const char* kernel, double* total_
     }
     *total_ms = sum;
     *launches = cnt;
+  });
+}
+
+int cvs_calibrate_stream_read(cvs_context* ctx, size_t bytes, int workgroups, int reps, double* out_gbs) {
+  return guarded([&] {
+    bind(ctx);
+    if (!out_gbs) fail(CVS_ERR_INVALID_ARGUMENT, "null out_gbs");
+    if (workgroups < 1 || reps < 1) fail(CVS_ERR_INVALID_ARGUMENT, "workgroups and reps must be positive");
+    const uint64_t step_bytes = kStreamStepVecs * 16;
+    const uint64_t steps = uint64_t(bytes) / (step_bytes * uint64_t(workgroups));
+    if (steps == 0) fail(CVS_ERR_INVALID_ARGUMENT, "fewer than 32 KiB per workgroup");
+    if (steps * step_bytes >= (uint64_t(1) << 31))
+      fail(CVS_ERR_UNSUPPORTED, "a workgroup's share must stay below 2 GiB (use more workgroups)");
+    const size_t used = size_t(steps * step_bytes * uint64_t(workgroups));
+    void* buf = nullptr;
+    void* sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto cleanup = [&] {
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+      if (buf) (void)hipFree(buf);
+      if (sink) (void)hipFree(sink);
+    };
+    try {
+      CVS_HIP(hipMalloc(&buf, used));
+      CVS_HIP(hipMalloc(&sink, size_t(workgroups) * 256 * sizeof(uint32_t)));
+      CVS_HIP(hipMemsetAsync(buf, 0x5a, used, ctx->stream));
+      CVS_HIP(hipEventCreate(&e0));
+      CVS_HIP(hipEventCreate(&e1));
+      auto launch = [&] {
+        hipLaunchKernelGGL(stream_read_kernel, dim3(unsigned(workgroups)), dim3(256), 0, ctx->stream,
+                           static_cast<const stream_vec*>(buf), steps, static_cast<uint32_t*>(sink));
+        after_launch("stream_read_kernel");
+      };
+      for (int i = 0; i < 2; ++i) launch();  // warm-up
+      CVS_HIP(hipEventRecord(e0, ctx->stream));
+      for (int i = 0; i < reps; ++i) launch();
+      CVS_HIP(hipEventRecord(e1, ctx->stream));
+      CVS_HIP(hipEventSynchronize(e1));
+      float ms = 0.f;
+      CVS_HIP(hipEventElapsedTime(&ms, e0, e1));
+      *out_gbs = double(used) * reps / (double(ms) * 1e-3) / 1e9;
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
   });
 }
 

@@ -96,6 +96,16 @@ int cvs_context_set_timing(cvs_context* ctx, int enable);
 int cvs_context_kernel_time(cvs_context* ctx, const char* kernel,
                             double* total_ms, uint64_t* launches);
 
+/* Device calibration; no counterpart in the reference (its roofline figures
+ * are nominal).  Streams `bytes` of device memory, rounded down to whole
+ * 32 KiB steps per workgroup, with `workgroups` workgroups of 256 threads,
+ * each reading one contiguous share with 16-byte non-temporal loads, `reps`
+ * times after two warm-up passes, and returns the read rate in GB/s: the
+ * achievable bound next to the nominal HBM peak.  Allocates and frees its
+ * own buffer; synchronizes. */
+int cvs_calibrate_stream_read(cvs_context* ctx, size_t bytes, int workgroups, int reps,
+                              double* out_gbs);
+
 /* ---- device memory helpers (device-resident benchmarking and tests) ----- */
 
 int cvs_device_alloc(cvs_context* ctx, size_t bytes, void** out_ptr);
