@@ -10,8 +10,9 @@
 //
 //  prep     queries fp32 -> fp16 32-row tiles + norms (the dataset layout),
 //           one wave per query.
-//  sample   the scan kernel over an evenly strided sample of 32,768 rows
-//           (65,536 for large batches); each lane keeps the minimum distance
+//  sample   the scan kernel over an evenly strided sample of 16,384 rows
+//           (65,536 for large batches, 131,072 when the register-blocked
+//           scan of bf_gemm.hip follows); each lane keeps the minimum distance
 //           of the rows it sees, so every (query, workgroup, half-wave)
 //           yields one minimum.
 //  select   per query (one wave), the kp-th smallest of those minima, T0.
@@ -1058,16 +1059,18 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   p.G = G;
   p.stride = global_lists ? Lists<128, kModeScan>::CAP : p.kp;
 
-  // Sample: 16,384 rows for small batches, 65,536 for large ones, in whole
-  // units, evenly strided, over Gs workgroups; 2 minima per (query,
-  // workgroup).  The initial threshold then sits near rank kp * n / sample
-  // of each query's distances, so a workgroup's lists see about
-  // kp * n / (sample * G) appends per query over its range.  Small batches
-  // are bound by the scan's HBM stream, where a few more appends cost
-  // nothing and the sample's own latency is what shows; large batches
-  // (kp = 128 lists) need the larger sample to keep appends and list
-  // compactions off the scan's critical path.
-  p.s_units = (p.large_batch ? 65536 : 16384) / rpu;
+  // Sample: 16,384 rows for small batches, 65,536 for other large ones and
+  // 131,072 for the register-blocked scan, in whole units, evenly strided,
+  // over Gs workgroups; 2 minima per (query, workgroup).  The initial
+  // threshold then sits near rank kp * n / sample of each query's
+  // distances, so a workgroup's lists see about kp * n / (sample * G)
+  // appends per query over its range.  Small batches are bound by the
+  // scan's HBM stream, where a few more appends cost little and the
+  // sample's own latency is what shows.  The register-blocked scan's appends
+  // and compactions sit on its critical path: at N=1M D=1024 Q=10,000
+  // K=100 its launch takes 26.9 / 24.7 / 22.5 ms after samples of
+  // 32,768 / 65,536 / 131,072 rows, which themselves take 1.2 / 2.1 / 4.1 ms.
+  p.s_units = (p.gemm ? 131072 : p.large_batch ? 65536 : 16384) / rpu;
   if (p.s_units < 1) p.s_units = 1;
   if (p.s_units > p.n_units) p.s_units = p.n_units;
   p.s_stride = p.n_units / p.s_units;
