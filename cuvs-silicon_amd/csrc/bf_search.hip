@@ -1128,9 +1128,13 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
   after_launch("query_tiles_kernel");
 
   const TimerSpan t1 = timed ? timer_span(ctx, "bf_sample") : TimerSpan{};
+  // Large batches sample range-major (the workgroups of one sampled range
+  // for every query block dispatched together), so that the sampled rows are
+  // read from HBM about once and then from L2, not once per query block.
   args.n_ranges = p.Gs;
-  args.qb_fast = 0;
-  launch_scan(ctx, p.ks, dim3(unsigned(p.Gs), p.qblocks), args, kModeSample, t1.start, nullptr);
+  args.qb_fast = p.large_batch ? 1 : 0;
+  launch_scan(ctx, p.ks, p.large_batch ? dim3(unsigned(p.Gs) * p.qblocks, 1) : dim3(unsigned(p.Gs), p.qblocks), args,
+              kModeSample, t1.start, nullptr);
   hipExtLaunchKernelGGL(bf_select_kernel, dim3(wave_blocks), dim3(kThreads), 0, ctx->stream, nullptr, t1.stop, 0,
                         static_cast<const float*>(sgmin), p.m_min, kp, int(q), thr0);
   after_launch("bf_select_kernel");
