@@ -124,6 +124,8 @@ def test_random_shapes(ctx, oracle, n, d, q, k):
     (500, 256, 1200, 100),    # half the spans empty
     (20000, 1000, 1500, 100), # d padded to 1024
     (20000, 512, 5000, 112),  # 10 query blocks: two per XCD for XCDs 0 and 1, largest k
+    (12000, 1024, 1300, 10),  # range-major pipelined scan (64 k-steps), kp = 16 LDS lists
+    (12000, 512, 1100, 40),   # range-major pipelined scan (32 k-steps), kp = 64 LDS lists
 ])
 def test_large_batches(ctx, oracle, n, d, q, k):
     rng = np.random.default_rng(q + k)
