@@ -8,6 +8,9 @@
   dispatch test with its exact answers, the exact route and the brute_force
   namespace, build -> save -> load -> search recall.
 - test_loaders (no GPU): fvecs/ivecs and Cohere .bin readers.
+- asan_test_api_cpu, asan_test_loaders (no GPU): the two above with the
+  library's host sources compiled in under AddressSanitizer (leaks
+  included) and UndefinedBehaviorSanitizer.
 - cohere_wiki_validation (GPU): the reference's end-to-end harness CLI on
   synthetic Cohere-format files, exact route and graph route, with the index
   saved by one run and loaded by the next.
@@ -24,11 +27,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 BIN = os.path.join(HERE, "cpp", "bin")
 
 
-def run(name, *args):
+def run(name, *args, env=None):
     exe = os.path.join(BIN, name)
     if not os.path.exists(exe):
         pytest.fail(f"{exe} is missing: build with `make -C tests/cpp` (or __graft_entry__.build())")
-    p = subprocess.run([exe, *args], capture_output=True, text=True, timeout=600)
+    p = subprocess.run([exe, *args], capture_output=True, text=True, timeout=600,
+                       env=None if env is None else {**os.environ, **env})
     print(p.stdout)
     print(p.stderr)
     assert p.returncode == 0, p.stderr
@@ -46,6 +50,16 @@ def test_api_gpu(tmp_path):
 
 def test_loaders(tmp_path):
     run("test_loaders", str(tmp_path))
+
+
+SANITIZE = {"ASAN_OPTIONS": "detect_leaks=1:abort_on_error=1", "UBSAN_OPTIONS": "print_stacktrace=1:halt_on_error=1"}
+
+
+def test_host_code_under_sanitizers(tmp_path):
+    for sub in ("api", "loaders"):
+        (tmp_path / sub).mkdir()
+    run("asan_test_api_cpu", os.path.join(HERE, "golden"), str(tmp_path / "api"), env=SANITIZE)
+    run("asan_test_loaders", str(tmp_path / "loaders"), env=SANITIZE)
 
 
 def write_bin(path, a):
