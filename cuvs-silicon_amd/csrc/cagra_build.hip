@@ -544,6 +544,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 template <int E>
 __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
   __shared__ uint32_t s_hash[4][512];
+  __shared__ uint64_t s_keep[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t u = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (u >= a.n) return;
@@ -608,9 +609,30 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
     nk[e] = keep ? ((by_id[e] & 0xffffffffull) << 32) | (uint64_t(bid) << 1) | 1ull : kEmpty;
     n_keep += popc(__ballot(keep));
   }
-  wave_sort_e<2>(nk);
-  wave_merge<E>(v, nk[0]);
-  wave_merge<E>(v, nk[1]);
+  if (n_keep <= 64) {
+    // Usually a few dozen kept: packed into one key per lane (through LDS,
+    // in bin order), one 64-wide sort and one merge.
+    uint64_t* kp = s_keep[wave];
+    kp[lane] = kEmpty;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    int base = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint64_t m = __ballot(nk[e] != kEmpty);
+      if (nk[e] != kEmpty) kp[base + mbcnt(m)] = nk[e];
+      base += popc(m);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    uint64_t c[1] = {kp[lane]};
+    wave_sort_e<1>(c);
+    wave_merge<E>(v, c[0]);
+  } else {
+    wave_sort_e<2>(nk);
+    wave_merge<E>(v, nk[0]);
+    wave_merge<E>(v, nk[1]);
+  }
   int inserted = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
