@@ -48,6 +48,7 @@
 #include <chrono>
 #include <cmath>
 #include <numeric>
+#include <type_traits>
 #include <vector>
 
 #include "cvs_internal.hpp"
@@ -167,14 +168,21 @@ __device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t
 }
 
 // Gram columns of the local join: rows s_ids[0..m), 32 < m <= 32*R (or
-// m <= 32 with R = 1), staged CB bytes per row and step.  Wave w < R computes
-// column tile w against the R row tiles into acc[0..R); waves >= R only
-// stage.  All tile guards are resolved by the template and one uniform branch
-// per chunk, so each k-step's LDS operand reads (one B tile, R A tiles) sit in
-// one basic block with its R MFMAs and can be issued ahead of them.
-template <int R, int CB>
+// m <= 32 with R = 1), staged CB bytes per row and step.  The calling wave
+// computes column tile `wave` against row tiles 0..T-1 into acc[0..T)
+// (T = 0: it only stages).  Every wave of the workgroup runs the same chunk
+// steps and barriers whatever its T, so waves may run different T.  All tile
+// guards are resolved by the template, so each k-step's LDS operand reads
+// (one B tile, T A tiles) sit in one basic block with its T MFMAs and can be
+// issued ahead of them.
+// after_issue() runs once the first NS chunks' gathers are issued: loads it
+// makes and waits for overlap them, and registers it holds are free again
+// before the Gram loop.
+template <int R, int T, int CB, class AfterIssue>
 __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t row_bytes, int m,
-                                          const uint32_t* s_ids, char* s_stage, int wave, f32x16 (&acc)[4]) {
+                                          const uint32_t* s_ids, char* s_stage, int wave, f32x16 (&acc)[4],
+                                          AfterIssue&& after_issue) {
+  static_assert(T >= 0 && T <= R, "row tiles");
   constexpr int M = 32 * R;
   constexpr int SEG = CB / 16;
   constexpr int STRIDE = CB + 16;
@@ -196,7 +204,6 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
-  const bool live = wave < R;
   const int last = n_chunks - 1;
   const char* a_base = s_stage + (lane & 31) * STRIDE + 16 * (lane >> 5);
   const char* b_base = a_base + 32 * wave * STRIDE;
@@ -210,6 +217,9 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
   for (int k = 0; k < NS; ++k)
 #pragma unroll
     for (int i = 0; i < LPT; ++i) reg[k][i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(k, last)) * CB);
+  __builtin_amdgcn_sched_barrier(0);
+  after_issue();
+  __builtin_amdgcn_sched_barrier(0);
   auto step = [&](u32x4 (&rg)[LPT], int c) __attribute__((always_inline)) {
     __syncthreads();
 #pragma unroll
@@ -218,15 +228,15 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
 #pragma unroll
     for (int i = 0; i < LPT; ++i)
       rg[i] = *reinterpret_cast<const u32x4*>(src[i] + int64_t(min(c + NS, last)) * CB);
-    if (live) {
+    if constexpr (T > 0) {
 #pragma unroll
       for (int s = 0; s < CB / 32; ++s) {
         const half8 b = *reinterpret_cast<const half8*>(b_base + s * 32);
-        half8 av[R];
+        half8 av[T];
 #pragma unroll
-        for (int t = 0; t < R; ++t) av[t] = *reinterpret_cast<const half8*>(a_base + 32 * t * STRIDE + s * 32);
+        for (int t = 0; t < T; ++t) av[t] = *reinterpret_cast<const half8*>(a_base + 32 * t * STRIDE + s * 32);
 #pragma unroll
-        for (int t = 0; t < R; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], b, acc[t], 0, 0, 0);
+        for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], b, acc[t], 0, 0, 0);
       }
     }
   };
@@ -393,27 +403,30 @@ __global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
 // to its update bin.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void join_kernel(BuildArgs a) {
   __shared__ __attribute__((aligned(16))) char s_stage[kJoinM * (kJoinChunkBytes + 16)];
-  __shared__ uint32_t s_ids[kJoinM];
-  __shared__ float s_norm[kJoinM];
-  __shared__ uint64_t s_worst[kJoinM];
+  __shared__ uint32_t s_ids[kJoinM + 1];  // + a spare slot for unused list entries
+  __shared__ float s_norm[kJoinM + 1];
+  __shared__ uint64_t s_worst[kJoinM + 1];
   __shared__ int s_m[2];  // members, new members
   __shared__ unsigned int s_emit;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t u = blockIdx.x;
   if (tid < 64) {
-    // Lane-parallel member list: new forward, new reverse, old forward, old reverse.
+    // Lane-parallel member list: new forward, new reverse, old forward, old
+    // reverse.  Lanes 0-31 take the new samples, lanes 32-63 the old.  Both
+    // lists are loaded whole, in the same round trip as the counts, and
+    // stored without branches: entries past a count (in bounds, stale) go to
+    // the spare slot s_ids[kJoinM].  A load under a branch of its own would
+    // be waited for before the next.
+    const int t = tid & (kSample - 1);
+    const uint32_t idf = a.fwd[u * 2 * kSample + tid];
+    const uint32_t idr = a.rev[u * 2 * kSample + tid];
     const uint32_t fn = a.fwd_cnt[2 * u], fo = a.fwd_cnt[2 * u + 1];
     const uint32_t rn = min(a.rev_cnt[2 * u], uint32_t(kSample));
     const uint32_t ro = min(a.rev_cnt[2 * u + 1], uint32_t(kSample));
-    const uint32_t* fw = a.fwd + u * 2 * kSample;
-    const uint32_t* rv = a.rev + u * 2 * kSample;
     const int o1 = int(fn), o2 = o1 + int(rn), o3 = o2 + int(fo);
-    if (tid < kSample) {
-      if (uint32_t(tid) < fn) s_ids[tid] = fw[tid];
-      if (uint32_t(tid) < rn) s_ids[o1 + tid] = rv[tid];
-      if (uint32_t(tid) < fo) s_ids[o2 + tid] = fw[kSample + tid];
-      if (uint32_t(tid) < ro) s_ids[o3 + tid] = rv[kSample + tid];
-    }
+    const bool old = tid >= kSample;
+    s_ids[uint32_t(t) < (old ? fo : fn) ? (old ? o2 : 0) + t : kJoinM] = idf;
+    s_ids[uint32_t(t) < (old ? ro : rn) ? (old ? o3 : o1) + t : kJoinM] = idr;
     if (tid == 0) {
       s_m[0] = o3 + int(ro);
       s_m[1] = o2;
@@ -425,30 +438,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   // tile and row guards below are scalar branches.
   const int m = __builtin_amdgcn_readfirstlane(s_m[0]), mnew = __builtin_amdgcn_readfirstlane(s_m[1]);
   if (mnew == 0 || m < 2) return;
-  // Norm and current worst key of member tid: loaded now, stored after the
-  // Gram matrix, so that their latency overlaps the first row gathers.
-  float member_norm;
-  uint64_t member_worst;
-  {
-    const uint32_t id = s_ids[tid < m ? tid : 0];
-    member_norm = a.norms[id];
-    member_worst = a.lists[int64_t(id) * a.kp + a.kd - 1] | 1ull;
-  }
+  // Norm and current worst key of member tid, loaded once the first row
+  // gathers are issued and stored to LDS for the emit: the wait for them
+  // overlaps the gathers', and no register holds them through the Gram loop
+  // (for the largest neighbourhoods that would spill, and the spill's store
+  // would wait for these loads before any gather is issued).  Threads past
+  // the last member store to the spare slot kJoinM.
+  const uint32_t member_id = s_ids[tid < m ? tid : 0];
+  const int member_slot = tid < m ? tid : kJoinM;
+  auto member_side = [&]() __attribute__((always_inline)) {
+    const float nrm = a.norms[member_id];
+    const uint64_t worst = a.lists[int64_t(member_id) * a.kp + a.kd - 1];
+    s_norm[member_slot] = nrm;
+    s_worst[member_slot] = worst | 1ull;
+  };
   // Row tiles in use: most nodes hold at most 64 members once the lists
   // settle, and stage only those rows.
+  // The members are ordered new first, and the join uses no pair of two old
+  // members: a wave whose column tile holds no new member multiplies only the
+  // row tiles that do.
   f32x16 acc[4];
-  if (m <= 32)
-    gram_join<1, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
-  else if (m <= 64)
-    gram_join<2, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
-  else if (m <= 96)
-    gram_join<3, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
-  else
-    gram_join<4, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc);
-  if (tid < m) {
-    s_norm[tid] = member_norm;
-    s_worst[tid] = member_worst;
-  }
+  const int new_tiles = (mnew + 31) / 32;
+  auto gram = [&](auto r_c) __attribute__((always_inline)) {
+    constexpr int R = decltype(r_c)::value;
+    const int tiles = wave >= R ? 0 : 32 * wave < mnew ? R : min(R, new_tiles);
+    auto run = [&](auto t_c) __attribute__((always_inline)) {
+      gram_join<R, decltype(t_c)::value, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc,
+                                                          member_side);
+    };
+    if (tiles == R) run(std::integral_constant<int, R>());
+    else if (tiles == 0) run(std::integral_constant<int, 0>());
+    else if constexpr (R >= 2) {
+      if (tiles == 1) run(std::integral_constant<int, 1>());
+      else if constexpr (R >= 3) {
+        if (tiles == 2) run(std::integral_constant<int, 2>());
+        else if constexpr (R >= 4) run(std::integral_constant<int, 3>());
+      }
+    }
+  };
+  if (m <= 32) gram(std::integral_constant<int, 1>());
+  else if (m <= 64) gram(std::integral_constant<int, 2>());
+  else if (m <= 96) gram(std::integral_constant<int, 3>());
+  else gram(std::integral_constant<int, 4>());
   __syncthreads();
 
   const int col = 32 * wave + (lane & 31);
