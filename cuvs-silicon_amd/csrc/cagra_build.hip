@@ -73,7 +73,7 @@ constexpr int kRowAlignDims = 128;  // fp16 row stride: d rounded up to this
 constexpr int kSample = 32;       // sampled forward/reverse new/old neighbours
 constexpr int kJoinM = 4 * kSample;
 constexpr int kBin = 128;         // update bin capacity per node
-constexpr int kSlots = 256;       // spread of the global work counters
+constexpr int kStatGroups = 256;  // workgroups of the per-iteration statistics reduction
 constexpr int kEmit = 8;          // partners emitted per member and join
 constexpr int kBucket = 256;
 constexpr int kBucketRounds = 4;   // random bucketings merged into the initial lists
@@ -286,9 +286,11 @@ struct BuildArgs {
   uint32_t* rev_cnt;     // n x 2
   uint64_t* bins;        // n x kBin
   uint32_t* bin_cnt;     // n
-  // Work counters, each spread over kSlots addresses:
-  // [0] insertions, [1] join members, [2] updates emitted, [3] bin entries kept.
-  unsigned long long* counters;
+  // Per-node work statistics of the current iteration, written with plain
+  // stores (global atomics on a few shared counters, hit by every workgroup
+  // from every XCD, cost the join 4%): [0] join members, [1] updates emitted
+  // (join), [2] insertions, [3] bin entries kept (apply).
+  uint4* stats;
 };
 
 // One workgroup per bucket of up to 256 permuted rows.  First round
@@ -355,7 +357,10 @@ __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t
 }
 
 // Per node (one wave): sample new/old neighbours, mark sampled new ones old,
-// append reverse edges.
+// append reverse edges.  The list keys are loaded together, then every
+// reverse-slot atomic is issued, then the stores: three round trips in all
+// (a load or atomic whose result a later branch waits for would make each
+// step wait for everything issued before it).
 template <int E>
 __global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
   const int lane = threadIdx.x & 63;
@@ -363,29 +368,40 @@ __global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
   if (u >= a.n) return;
   uint64_t* lst = a.lists + u * a.kp;
   uint32_t* fw = a.fwd + u * 2 * kSample;
+  uint64_t key[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) key[e] = lst[min(e * 64 + lane, a.kd - 1)];
   int n_new = 0, n_old = 0;
+  bool take_new[E], take_old[E];
+  int pos[E];  // position in the forward sample (new: 0.., old: kSample..)
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int p = e * 64 + lane;
-    const uint64_t key = p < a.kd ? lst[p] : kEmpty;
-    const bool valid = key != kEmpty;
-    const bool is_new = valid && (key & 1ull);
+    if (e * 64 + lane >= a.kd) key[e] = kEmpty;
+    const bool valid = key[e] != kEmpty;
+    const bool is_new = valid && (key[e] & 1ull);
     const uint64_t mn = __ballot(is_new), mo = __ballot(valid && !is_new);
     const int rn = mbcnt(mn), ro = mbcnt(mo);
-    const uint32_t id = key_id(key);
-    if (is_new && n_new + rn < kSample) {
-      fw[n_new + rn] = id;
-      lst[p] = key & ~1ull;
-      const uint32_t slot = atomicAdd(&a.rev_cnt[2 * int64_t(id)], 1u);
-      if (slot < kSample) a.rev[int64_t(id) * 2 * kSample + slot] = uint32_t(u);
-    }
-    if (valid && !is_new && n_old + ro < kSample) {
-      fw[kSample + n_old + ro] = id;
-      const uint32_t slot = atomicAdd(&a.rev_cnt[2 * int64_t(id) + 1], 1u);
-      if (slot < kSample) a.rev[int64_t(id) * 2 * kSample + kSample + slot] = uint32_t(u);
-    }
+    take_new[e] = is_new && n_new + rn < kSample;
+    take_old[e] = valid && !is_new && n_old + ro < kSample;
+    pos[e] = take_new[e] ? n_new + rn : kSample + n_old + ro;
     n_new = std::min(kSample, n_new + popc(mn));
     n_old = std::min(kSample, n_old + popc(mo));
+  }
+  uint32_t slot[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    slot[e] = kInvalid;
+    if (take_new[e] || take_old[e])
+      slot[e] = atomicAdd(&a.rev_cnt[2 * int64_t(key_id(key[e])) + (take_new[e] ? 0 : 1)], 1u);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if (!(take_new[e] || take_old[e])) continue;
+    const uint32_t id = key_id(key[e]);
+    fw[pos[e]] = id;
+    if (take_new[e]) lst[e * 64 + lane] = key[e] & ~1ull;
+    if (slot[e] < uint32_t(kSample))
+      a.rev[int64_t(id) * 2 * kSample + (take_new[e] ? 0 : kSample) + slot[e]] = uint32_t(u);
   }
   if (lane == 0) {
     a.fwd_cnt[2 * u] = uint32_t(n_new);
@@ -437,7 +453,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   // Wave-uniform in registers the compiler knows to be scalar, so that the
   // tile and row guards below are scalar branches.
   const int m = __builtin_amdgcn_readfirstlane(s_m[0]), mnew = __builtin_amdgcn_readfirstlane(s_m[1]);
-  if (mnew == 0 || m < 2) return;
+  if (mnew == 0 || m < 2) {
+    if (tid == 0) *reinterpret_cast<uint2*>(&a.stats[u]) = make_uint2(0u, 0u);
+    return;
+  }
   // Norm and current worst key of member tid, loaded once the first row
   // gathers are issued and stored to LDS for the emit: the wait for them
   // overlaps the gathers', and no register holds them through the Gram loop
@@ -551,24 +570,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     if (half == 0 && cnt > 0) {
       const uint32_t base = atomicAdd(&a.bin_cnt[cid], uint32_t(cnt));
       uint64_t* bin = a.bins + int64_t(cid) * kBin;
-      uint32_t q = base;
+      // Slots first, without branches, so that the atomic is waited for once:
+      // a count advanced inside the store branches below made the compiler
+      // wait for every outstanding store (a full round trip) before each one.
+      uint32_t q[kEmit];
+      uint32_t next = base;
 #pragma unroll
       for (int p = 0; p < kEmit; ++p) {
-        if (keep[p]) {
-          if (q < uint32_t(kBin)) bin[q] = mg[p];
-          ++q;
-        }
+        q[p] = next;
+        next += keep[p] ? 1u : 0u;
       }
+#pragma unroll
+      for (int p = 0; p < kEmit; ++p)
+        if (keep[p] && q[p] < uint32_t(kBin)) bin[q[p]] = mg[p];
       emitted = unsigned(cnt);
     }
   }
   atomicAdd(&s_emit, emitted);
   __syncthreads();
-  if (tid == 0) {
-    const int slot = int(u & (kSlots - 1));
-    atomicAdd(&a.counters[1 * kSlots + slot], (unsigned long long)m);
-    atomicAdd(&a.counters[2 * kSlots + slot], (unsigned long long)s_emit);
-  }
+  if (tid == 0) *reinterpret_cast<uint2*>(&a.stats[u]) = make_uint2(uint32_t(m), s_emit);
 }
 
 // Per node (one wave): merge the update bin into the list.
@@ -579,20 +599,33 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t u = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (u >= a.n) return;
+  uint32_t* stat = &a.stats[u].z;
   const uint32_t cnt = a.bin_cnt[u];
-  if (cnt == 0) return;
+  if (cnt == 0) {
+    if (lane == 0) *reinterpret_cast<uint2*>(stat) = make_uint2(0u, 0u);
+    return;
+  }
   const int c = int(min(cnt, uint32_t(kBin)));
   uint32_t* h = s_hash[wave];
   for (int i = lane; i < 512; i += 64) h[i] = kInvalid;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   uint64_t* lst = a.lists + u * a.kp;
+  // The list and the whole bin are loaded together (bin entries past the
+  // count are in bounds and dropped below), before the list's hash inserts
+  // wait for the list: one round trip instead of two.
   uint64_t v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int p = e * 64 + lane;
-    v[e] = p < a.kd ? lst[p] : kEmpty;
+    v[e] = lst[p < a.kd ? p : 0];
   }
+  uint64_t bin_raw[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) bin_raw[e] = a.bins[u * kBin + e * 64 + lane];
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (e * 64 + lane >= a.kd) v[e] = kEmpty;
   auto insert = [&](uint32_t id) -> bool {  // true if newly inserted
     uint32_t s = (id * 0x9E3779B1u) >> 23;
     for (;;) {
@@ -622,7 +655,7 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int pos = e * 64 + lane;
-    const uint64_t b = pos < c ? a.bins[u * kBin + pos] : kEmpty;
+    const uint64_t b = pos < c ? bin_raw[e] : kEmpty;
     by_id[e] = b == kEmpty ? kEmpty : (uint64_t(key_id(b)) << 32) | (b >> 32);
   }
   wave_sort_e<2>(by_id);
@@ -675,10 +708,34 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
   }
   if (lane == 0) {
     a.bin_cnt[u] = 0;
-    const int slot = int(u & (kSlots - 1));
-    if (inserted) atomicAdd(&a.counters[0 * kSlots + slot], (unsigned long long)inserted);
-    if (n_keep) atomicAdd(&a.counters[3 * kSlots + slot], (unsigned long long)n_keep);
+    *reinterpret_cast<uint2*>(stat) = make_uint2(uint32_t(inserted), uint32_t(n_keep));
   }
+}
+
+// Sums of the per-node statistics: workgroup g writes its partial sums of the
+// four fields to partial[4 g .. 4 g + 3].
+__global__ __launch_bounds__(256) void stats_reduce_kernel(const uint4* __restrict__ stats, int64_t n,
+                                                           unsigned long long* __restrict__ partial) {
+  __shared__ unsigned long long s_sum[4][4];
+  unsigned long long sum[4] = {0, 0, 0, 0};
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const uint4 v = stats[i];
+    sum[0] += v.x;
+    sum[1] += v.y;
+    sum[2] += v.z;
+    sum[3] += v.w;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum[k] += shfl_xor_u64(sum[k], o);
+    if (lane == 0) s_sum[wave][k] = sum[k];
+  }
+  __syncthreads();
+  if (threadIdx.x < 4)
+    partial[4 * blockIdx.x + threadIdx.x] =
+        s_sum[0][threadIdx.x] + s_sum[1][threadIdx.x] + s_sum[2][threadIdx.x] + s_sum[3][threadIdx.x];
 }
 
 // Per node (one workgroup): exact fp32 squared L2 distance to each entry of
@@ -1026,9 +1083,9 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   a.rev_cnt = mem.alloc<uint32_t>(size_t(n) * 2);
   a.bins = mem.alloc<uint64_t>(size_t(n) * kBin);
   a.bin_cnt = mem.alloc<uint32_t>(size_t(n));
-  a.counters = mem.alloc<unsigned long long>(4 * kSlots);
+  a.stats = mem.alloc<uint4>(size_t(n));
+  unsigned long long* d_partial = mem.alloc<unsigned long long>(4 * kStatGroups);
   CVS_HIP(hipMemsetAsync(a.bin_cnt, 0, size_t(n) * sizeof(uint32_t), st));
-  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * kSlots * sizeof(unsigned long long), st));
 
   const int64_t n_buckets = (n + kBucket - 1) / kBucket;
   const dim3 wave_grid(unsigned((n + 3) / 4));
@@ -1046,7 +1103,6 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
     // The host permutation buffer is reused: wait for its copy.
     CVS_HIP(hipStreamSynchronize(st));
   }
-  CVS_HIP(hipMemsetAsync(a.counters, 0, 4 * kSlots * sizeof(unsigned long long), st));
   CVS_HIP(hipStreamSynchronize(st));
   s.seconds_seed = elapsed_s(t_start);
 
@@ -1058,7 +1114,7 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   double join_ms = 0.0;
   uint32_t it = 0;
   double rate = 1.0;
-  unsigned long long prev[4] = {0, 0, 0, 0};
+  std::vector<unsigned long long> partial(4 * kStatGroups);
   for (; it < max_iterations; ++it) {
     CVS_HIP(hipMemsetAsync(a.rev_cnt, 0, size_t(n) * 2 * sizeof(uint32_t), st));
     launch_e<SampleK>(e_slots, wave_grid, st, a);
@@ -1069,22 +1125,23 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
     CVS_HIP(hipEventRecord(ev1, st));
     launch_e<ApplyK>(e_slots, wave_grid, st, a);
     after_launch("apply_kernel");
-    std::vector<unsigned long long> slots(4 * kSlots);
-    CVS_HIP(hipMemcpyAsync(slots.data(), a.counters, slots.size() * sizeof(unsigned long long),
+    hipLaunchKernelGGL(stats_reduce_kernel, dim3(kStatGroups), dim3(256), 0, st,
+                       static_cast<const uint4*>(a.stats), n, d_partial);
+    after_launch("stats_reduce_kernel");
+    CVS_HIP(hipMemcpyAsync(partial.data(), d_partial, partial.size() * sizeof(unsigned long long),
                            hipMemcpyDeviceToHost, st));
     CVS_HIP(hipStreamSynchronize(st));
     unsigned long long cnt[4] = {0, 0, 0, 0};
-    for (int k = 0; k < 4; ++k)
-      for (int i = 0; i < kSlots; ++i) cnt[k] += slots[size_t(k) * kSlots + i];
+    for (int g = 0; g < kStatGroups; ++g)
+      for (int k = 0; k < 4; ++k) cnt[k] += partial[size_t(4 * g + k)];
     float ms = 0.f;
     CVS_HIP(hipEventElapsedTime(&ms, ev0, ev1));
     join_ms += ms;
-    const unsigned long long ins = cnt[0] - prev[0];
-    s.join_members += cnt[1] - prev[1];
-    s.updates_emitted += cnt[2] - prev[2];
-    s.updates_kept += cnt[3] - prev[3];
+    const unsigned long long ins = cnt[2];
+    s.join_members += cnt[0];
+    s.updates_emitted += cnt[1];
+    s.updates_kept += cnt[3];
     s.insertions += ins;
-    for (int i = 0; i < 4; ++i) prev[i] = cnt[i];
     rate = double(ins) / (double(n) * double(kd));
     if (rate < double(termination_threshold)) {
       ++it;
