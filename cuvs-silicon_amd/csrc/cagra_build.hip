@@ -51,6 +51,8 @@
 #include <type_traits>
 #include <vector>
 
+#include <hipcub/hipcub.hpp>
+
 #include "cvs_internal.hpp"
 #include "device_util.hpp"
 
@@ -74,6 +76,12 @@ constexpr int kSample = 32;       // sampled forward/reverse new/old neighbours
 constexpr int kJoinM = 4 * kSample;
 constexpr int kBin = 128;         // update bin capacity per node
 constexpr int kStatGroups = 256;  // workgroups of the per-iteration statistics reduction
+// Locality order of the local join (see label_round_kernel): labels spread
+// over each node's first kLabelK list entries for kLabelRounds rounds, once
+// the lists of iteration kOrderAfter are in place.
+constexpr int kLabelK = 16;
+constexpr int kLabelRounds = 3;
+constexpr int kOrderAfter = 0;
 constexpr int kEmit = 8;          // partners emitted per member and join
 constexpr int kBucket = 256;
 constexpr int kBucketRounds = 4;   // random bucketings merged into the initial lists
@@ -291,6 +299,9 @@ struct BuildArgs {
   // from every XCD, cost the join 4%): [0] join members, [1] updates emitted
   // (join), [2] insertions, [3] bin entries kept (apply).
   uint4* stats;
+  // Node of each join workgroup (workgroup i joins node order[i]), or null
+  // for node i.
+  const uint32_t* order;
 };
 
 // One workgroup per bucket of up to 256 permuted rows.  First round
@@ -425,7 +436,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __shared__ int s_m[2];  // members, new members
   __shared__ unsigned int s_emit;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t u = blockIdx.x;
+  const int64_t u = a.order ? int64_t(a.order[blockIdx.x]) : int64_t(blockIdx.x);
   if (tid < 64) {
     // Lane-parallel member list: new forward, new reverse, old forward, old
     // reverse.  Lanes 0-31 take the new samples, lanes 32-63 the old.  Both
@@ -710,6 +721,36 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
     a.bin_cnt[u] = 0;
     *reinterpret_cast<uint2*>(stat) = make_uint2(uint32_t(inserted), uint32_t(n_keep));
   }
+}
+
+// Locality order of the local join.  A node's sampled neighbourhood is drawn
+// from its list and its list's reverse edges, so nodes close in the graph
+// gather overlapping member rows.  Workgroups are dispatched in order and
+// round-robin over the XCDs, so joining such nodes one after another lets all
+// XCDs share their rows in the last-level cache (on clustered data at N=1M,
+// nodes ordered by cluster made the join 10% faster).  The order: every node
+// starts with its own id as label; each round replaces a node's label by the
+// smallest label among its own and its first kLabelK neighbours'.  After r
+// rounds a node holds the smallest id within r hops, so equal labels form
+// connected regions of the graph around local minima of the ids, and the
+// nodes are sorted by label.  One 16-lane group per node.
+__global__ __launch_bounds__(256) void label_round_kernel(const uint64_t* __restrict__ lists, int kp, int kd,
+                                                          const uint32_t* __restrict__ in,
+                                                          uint32_t* __restrict__ out, int64_t n) {
+  const int64_t u = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 4;
+  const int j = threadIdx.x & 15;
+  if (u >= n) return;  // whole 16-lane groups
+  const uint64_t key = lists[u * kp + min(j, kd - 1)];
+  const uint32_t v = key == kEmpty ? uint32_t(u) : key_id(key);
+  uint32_t m = in ? min(in[u], in[v]) : min(uint32_t(u), v);
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) m = min(m, xor_lanes(m, o));
+  if (j == 0) out[u] = m;
+}
+
+__global__ __launch_bounds__(256) void iota_kernel(uint32_t* __restrict__ out, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = uint32_t(i);
 }
 
 // Sums of the per-node statistics: workgroup g writes its partial sums of the
@@ -1015,6 +1056,32 @@ struct DevMem {
   }
 };
 
+// The join's locality order (see label_round_kernel), in device memory owned
+// by mem.
+uint32_t* join_order(DevMem& mem, hipStream_t st, const BuildArgs& a, int64_t n) {
+  uint32_t* lab[2] = {mem.alloc<uint32_t>(size_t(n)), mem.alloc<uint32_t>(size_t(n))};
+  const dim3 grid(unsigned((n * 16 + 255) / 256));
+  for (int r = 0; r < kLabelRounds; ++r) {
+    hipLaunchKernelGGL(label_round_kernel, grid, dim3(256), 0, st, static_cast<const uint64_t*>(a.lists), a.kp,
+                       a.kd, r == 0 ? static_cast<const uint32_t*>(nullptr) : lab[(r + 1) & 1], lab[r & 1], n);
+    after_launch("label_round_kernel");
+  }
+  const uint32_t* keys = lab[(kLabelRounds - 1) & 1];
+  uint32_t* keys_out = lab[kLabelRounds & 1];
+  uint32_t* ids = mem.alloc<uint32_t>(size_t(n));
+  uint32_t* order = mem.alloc<uint32_t>(size_t(n));
+  hipLaunchKernelGGL(iota_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, ids, n);
+  after_launch("iota_kernel");
+  int bits = 1;
+  while (bits < 32 && (int64_t(1) << bits) < n) ++bits;
+  size_t temp_bytes = 0;
+  CVS_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, keys, keys_out, ids, order, int(n), 0, bits, st));
+  void* temp = mem.alloc<char>(temp_bytes);
+  CVS_HIP(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, keys_out, ids, order, int(n), 0, bits, st));
+  after_launch("radix_sort");
+  return order;
+}
+
 double elapsed_s(std::chrono::steady_clock::time_point t0) {
   return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 }
@@ -1084,6 +1151,7 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   a.bins = mem.alloc<uint64_t>(size_t(n) * kBin);
   a.bin_cnt = mem.alloc<uint32_t>(size_t(n));
   a.stats = mem.alloc<uint4>(size_t(n));
+  a.order = nullptr;
   unsigned long long* d_partial = mem.alloc<unsigned long long>(4 * kStatGroups);
   CVS_HIP(hipMemsetAsync(a.bin_cnt, 0, size_t(n) * sizeof(uint32_t), st));
 
@@ -1147,6 +1215,7 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
       ++it;
       break;
     }
+    if (it == kOrderAfter && !a.order) a.order = join_order(mem, st, a, n);
   }
   (void)hipEventDestroy(ev0);
   (void)hipEventDestroy(ev1);
