@@ -737,14 +737,15 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
 __global__ __launch_bounds__(256) void label_round_kernel(const uint64_t* __restrict__ lists, int kp, int kd,
                                                           const uint32_t* __restrict__ in,
                                                           uint32_t* __restrict__ out, int64_t n) {
-  const int64_t u = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 4;
-  const int j = threadIdx.x & 15;
+  static_assert(kLabelK == 16, "one 16-lane group per node");
+  const int64_t u = (int64_t(blockIdx.x) * 256 + threadIdx.x) / kLabelK;
+  const int j = threadIdx.x % kLabelK;
   if (u >= n) return;  // whole 16-lane groups
   const uint64_t key = lists[u * kp + min(j, kd - 1)];
   const uint32_t v = key == kEmpty ? uint32_t(u) : key_id(key);
   uint32_t m = in ? min(in[u], in[v]) : min(uint32_t(u), v);
 #pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) m = min(m, xor_lanes(m, o));
+  for (int o = kLabelK / 2; o >= 1; o >>= 1) m = min(m, xor_lanes(m, o));
   if (j == 0) out[u] = m;
 }
 
@@ -1060,7 +1061,7 @@ struct DevMem {
 // by mem.
 uint32_t* join_order(DevMem& mem, hipStream_t st, const BuildArgs& a, int64_t n) {
   uint32_t* lab[2] = {mem.alloc<uint32_t>(size_t(n)), mem.alloc<uint32_t>(size_t(n))};
-  const dim3 grid(unsigned((n * 16 + 255) / 256));
+  const dim3 grid(unsigned((n * kLabelK + 255) / 256));
   for (int r = 0; r < kLabelRounds; ++r) {
     hipLaunchKernelGGL(label_round_kernel, grid, dim3(256), 0, st, static_cast<const uint64_t*>(a.lists), a.kp,
                        a.kd, r == 0 ? static_cast<const uint32_t*>(nullptr) : lab[(r + 1) & 1], lab[r & 1], n);
