@@ -70,6 +70,7 @@ constexpr uint32_t kInvalid = 0xffffffffu;
 // (256 and 512 bytes per row per step) measured slower at N=1M D=1024: their
 // registers and LDS cost occupancy, which the join needs more.
 constexpr int kBucketChunkBytes = 128;
+constexpr int kBucketDepth = 1;    // bucket Gram: chunks gathered ahead
 constexpr int kJoinChunkBytes = 128;
 constexpr int kRowAlignDims = 128;  // fp16 row stride: d rounded up to this
 constexpr int kSample = 32;       // sampled forward/reverse new/old neighbours
@@ -307,10 +308,12 @@ struct BuildArgs {
 // One workgroup per bucket of up to 256 permuted rows.  First round
 // (to_bins = 0): each row's list becomes its kd nearest bucket mates.  Later
 // rounds (to_bins = 1): each row's kBucketEmit nearest mates go to its
-// update bin, for the apply kernel to merge into the list.
+// update bin, for the apply kernel to merge into the list.  The Gram matrix
+// is formed 64 rows at a time and its distances sorted 32 rows at a time, so
+// that two workgroups fit a CU's LDS.
 __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t* __restrict__ perm, int to_bins) {
   __shared__ __attribute__((aligned(16))) char s_stage[kBucket * (kBucketChunkBytes + 16)];
-  __shared__ float s_dist[64 * 257];  // one 64-row block of the bucket's distances
+  __shared__ float s_dist[32 * 257];  // one 32-row block of the bucket's distances
   __shared__ uint32_t s_ids[kBucket];
   __shared__ float s_norm[kBucket];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -327,26 +330,31 @@ __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t
     const int rt[4] = {2 * rb, 2 * rb, 2 * rb + 1, 2 * rb + 1};
     const int ct[4] = {2 * wave, 2 * wave + 1, 2 * wave, 2 * wave + 1};
     f32x16 acc[4];
-    gram_tiles<kBucket, 4, 1, kBucketChunkBytes>(a.x16, a.row_bytes, mb, s_ids, s_stage, rt, ct, acc);
+    gram_tiles<kBucket, 4, kBucketDepth, kBucketChunkBytes>(a.x16, a.row_bytes, mb, s_ids, s_stage, rt, ct, acc);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+    const int r0 = 64 * rb + 32 * h;  // first row of this half
+    if (r0 >= mb) break;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      if (rt[t] != 2 * rb + h) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = 32 * rt[t] + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         const int col = 32 * ct[t] + (lane & 31);
-        s_dist[(row - 64 * rb) * 257 + col] = s_norm[row] + s_norm[col] - 2.0f * acc[t][e];
+        s_dist[(row - r0) * 257 + col] = s_norm[row] + s_norm[col] - 2.0f * acc[t][e];
       }
     }
     __syncthreads();
-    for (int i = 0; i < 16; ++i) {
-      const int row = 64 * rb + 16 * wave + i;
+    for (int i = 0; i < 8; ++i) {
+      const int row = r0 + 8 * wave + i;
       if (row >= mb) break;
       uint64_t v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int c = e * 64 + lane;
         v[e] = (c < mb && c != row)
-                   ? (uint64_t(ord_f32(s_dist[(row - 64 * rb) * 257 + c])) << 32) | (uint64_t(s_ids[c]) << 1) | 1ull
+                   ? (uint64_t(ord_f32(s_dist[(row - r0) * 257 + c])) << 32) | (uint64_t(s_ids[c]) << 1) | 1ull
                    : kEmpty;
       }
       wave_sort_e<4>(v);
@@ -364,6 +372,7 @@ __global__ __launch_bounds__(256) void bucket_kernel(BuildArgs a, const uint32_t
       }
     }
     __syncthreads();
+    }
   }
 }
 
