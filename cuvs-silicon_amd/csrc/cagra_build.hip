@@ -437,8 +437,16 @@ __global__ __launch_bounds__(256) void sample_kernel(BuildArgs a) {
 // partners in registers (at least one of the pair new, below the member's
 // current worst key), merges them with the partner lane's, and appends them
 // to its update bin.
+// Transposed Gram tiles of the join's emit: one per pair of row tiles
+// (c, r), c < r <= 3, 32 x 32 distances with rows 33 floats apart.
+constexpr int kTrPitch = 33;
+constexpr int kTrBytes = 6 * 32 * kTrPitch * 4;
+constexpr int kJoinStageBytes = kJoinM * (kJoinChunkBytes + 16);
+__device__ __forceinline__ int tr_pair(int c, int r) { return r * (r - 1) / 2 + c; }
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void join_kernel(BuildArgs a) {
-  __shared__ __attribute__((aligned(16))) char s_stage[kJoinM * (kJoinChunkBytes + 16)];
+  // Gram operand staging, then (after the Gram) the transposed tiles.
+  __shared__ __attribute__((aligned(16))) char s_stage[kJoinStageBytes > kTrBytes ? kJoinStageBytes : kTrBytes];
   __shared__ uint32_t s_ids[kJoinM + 1];  // + a spare slot for unused list entries
   __shared__ float s_norm[kJoinM + 1];
   __shared__ uint64_t s_worst[kJoinM + 1];
@@ -491,18 +499,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     s_norm[member_slot] = nrm;
     s_worst[member_slot] = worst | 1ull;
   };
-  // Row tiles in use: most nodes hold at most 64 members once the lists
-  // settle, and stage only those rows.
-  // The members are ordered new first, and the join uses no pair of two old
-  // members: a wave whose column tile holds no new member multiplies only the
-  // row tiles that do.
+  // Tiles of the Gram matrix.  Row tiles in use: R = ceil(m / 32) (most
+  // nodes hold at most 64 members once the lists settle, and stage only
+  // those rows).  Wave `role` owns column tile `role` (roles rotate with the
+  // workgroup, so that the heavier ones spread over the SIMDs).  The join
+  // uses each pair of members once and no pair of two old members (members
+  // are ordered new first, new_tiles tiles hold the new ones), so the role
+  // multiplies only row tiles r <= role, or r < new_tiles when its own tile
+  // holds no new member: a prefix of `tiles` row tiles.  Tile (r, c) with
+  // r < c serves column c from the registers of role c and, transposed
+  // through LDS, column r.
   f32x16 acc[4];
+  const int role = (wave + int(blockIdx.x)) & 3;
   const int new_tiles = (mnew + 31) / 32;
+  const int row_tiles = (m + 31) / 32;
+  const int tiles = role >= row_tiles ? 0 : role < new_tiles ? role + 1 : new_tiles;
   auto gram = [&](auto r_c) __attribute__((always_inline)) {
     constexpr int R = decltype(r_c)::value;
-    const int tiles = wave >= R ? 0 : 32 * wave < mnew ? R : min(R, new_tiles);
     auto run = [&](auto t_c) __attribute__((always_inline)) {
-      gram_join<R, decltype(t_c)::value, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, wave, acc,
+      gram_join<R, decltype(t_c)::value, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, role, acc,
                                                           member_side);
     };
     if (tiles == R) run(std::integral_constant<int, R>());
@@ -519,12 +534,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   else if (m <= 64) gram(std::integral_constant<int, 2>());
   else if (m <= 96) gram(std::integral_constant<int, 3>());
   else gram(std::integral_constant<int, 4>());
+  __syncthreads();  // the Gram's operand reads are done: s_stage is free
+
+  const int half = lane >> 5;
+  float* s_tr = reinterpret_cast<float*>(s_stage);
+  // Tiles (t, role), t < role, transposed for role t: distance (i, j) of
+  // row i in tile t and column j in tile role at [i * kTrPitch + j].
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    if (t >= tiles || t >= role) continue;
+    float* tr = s_tr + tr_pair(t, role) * 32 * kTrPitch;
+    const float nj = s_norm[32 * role + (lane & 31)];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = 8 * (e >> 2) + 4 * half + (e & 3);
+      tr[i * kTrPitch + (lane & 31)] = s_norm[32 * t + i] + nj - 2.0f * acc[t][e];
+    }
+  }
   __syncthreads();
 
-  const int col = 32 * wave + (lane & 31);
-  const int half = lane >> 5;
+  const int col = 32 * role + (lane & 31);
   unsigned int emitted = 0;
-  if (32 * wave < m) {
+  if (32 * role < m) {
     const bool col_ok = col < m;
     const uint32_t cid = s_ids[col_ok ? col : 0];
     const float cn = s_norm[col_ok ? col : 0];
@@ -536,13 +567,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if (32 * t >= m) break;
+      // Row tile t from this role's registers, or (t > role) transposed from
+      // role t's; past them only pairs of two old members remain.
+      const bool own = t < tiles;
+      const float* tr = s_tr + (t > role ? tr_pair(role, t) : 0) * 32 * kTrPitch + (lane & 31) * kTrPitch;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = 32 * t + 8 * (e >> 2) + 4 * half + (e & 3);
         if (!col_ok || row >= m || !(col_new || row < mnew)) continue;
         const uint32_t rid = s_ids[row];
         if (rid == cid) continue;
-        const float dist = cn + s_norm[row] - 2.0f * acc[t][e];
+        const float dist = own ? cn + s_norm[row] - 2.0f * acc[t][e] : tr[row & 31];
         const uint64_t key = (uint64_t(ord_f32(dist)) << 32) | (uint64_t(rid) << 1) | 1ull;
         if (key < worst && key < best[kEmit - 1]) {
           best[kEmit - 1] = key;
