@@ -833,7 +833,9 @@ template <int E>
 __global__ __launch_bounds__(256) void rescore_kernel(const float* __restrict__ rows, int64_t d, BuildArgs a) {
   __shared__ float s_d[kMaxKd];
   const int tid = threadIdx.x, team = tid >> 4, tp = tid & 15, lane = tid & 63;
-  const int64_t u = blockIdx.x;
+  // In the join's locality order when there is one (neighbour rows of
+  // graph-close nodes then meet in the caches).
+  const int64_t u = a.order ? int64_t(a.order[blockIdx.x]) : int64_t(blockIdx.x);
   uint64_t* lst = a.lists + u * a.kp;
   const float* x = rows + u * d;
   const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
@@ -895,6 +897,7 @@ __global__ __launch_bounds__(256) void list_ids_kernel(const uint64_t* __restric
 // Per node (one wave): detour counts, keep g edges, append reverse edges.
 template <int E>
 __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__ ids, int64_t n, int kd, int g,
+                                                    const uint32_t* __restrict__ order,
                                                     uint32_t* __restrict__ kept, uint32_t* __restrict__ rev,
                                                     uint32_t* __restrict__ rev_cnt) {
   __shared__ uint32_t s_hkey[4][512];
@@ -902,8 +905,11 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
   __shared__ uint32_t s_det[4][kMaxKd];
   __shared__ uint32_t s_nb[4][kMaxKd];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t u = int64_t(blockIdx.x) * 4 + wave;
-  if (u >= n) return;
+  // Nodes in the join's locality order when there is one: graph-close nodes
+  // read overlapping neighbour lists, which then meet in the caches.
+  const int64_t i_node = int64_t(blockIdx.x) * 4 + wave;
+  if (i_node >= n) return;
+  const int64_t u = order ? int64_t(order[i_node]) : i_node;
   uint32_t* hk = s_hkey[wave];
   uint32_t* hv = s_hval[wave];
   for (int i = lane; i < 512; i += 64) hk[i] = kInvalid;
@@ -1294,9 +1300,9 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   uint32_t* rev_cnt = mem.alloc<uint32_t>(size_t(n));
   CVS_HIP(hipMemsetAsync(rev_cnt, 0, size_t(n) * sizeof(uint32_t), st));
   switch (e_slots) {
-    case 1: hipLaunchKernelGGL(prune_kernel<1>, wave_grid, dim3(256), 0, st, ids, n, kd, g, kept, rev, rev_cnt); break;
-    case 2: hipLaunchKernelGGL(prune_kernel<2>, wave_grid, dim3(256), 0, st, ids, n, kd, g, kept, rev, rev_cnt); break;
-    default: hipLaunchKernelGGL(prune_kernel<4>, wave_grid, dim3(256), 0, st, ids, n, kd, g, kept, rev, rev_cnt); break;
+    case 1: hipLaunchKernelGGL(prune_kernel<1>, wave_grid, dim3(256), 0, st, ids, n, kd, g, a.order, kept, rev, rev_cnt); break;
+    case 2: hipLaunchKernelGGL(prune_kernel<2>, wave_grid, dim3(256), 0, st, ids, n, kd, g, a.order, kept, rev, rev_cnt); break;
+    default: hipLaunchKernelGGL(prune_kernel<4>, wave_grid, dim3(256), 0, st, ids, n, kd, g, a.order, kept, rev, rev_cnt); break;
   }
   after_launch("prune_kernel");
   uint32_t* final_graph = graph_on_device ? out_graph : mem.alloc<uint32_t>(size_t(n) * g);
