@@ -65,6 +65,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint64_t kEmpty = ~0ull;
 constexpr uint32_t kInvalid = 0xffffffffu;
+constexpr uint32_t kBinTag = 0x80000000u;  // apply's hash: an id from the bin (ids < 2^31)
 // Bytes of each member row staged per step (64 fp16 dimensions); a staged
 // row is padded by 16 bytes against LDS bank conflicts.  Larger join chunks
 // (256 and 512 bytes per row per step) measured slower at N=1M D=1024: their
@@ -690,6 +691,7 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
       s = (s + 1u) & 511u;
     }
   };
+  // Only the list's own ids (untagged) count as contained.
   auto contains = [&](uint32_t id) -> bool {
     uint32_t s = (id * 0x9E3779B1u) >> 23;
     for (;;) {
@@ -704,28 +706,33 @@ __global__ __launch_bounds__(256) void apply_kernel(BuildArgs a) {
     if (v[e] != kEmpty) insert(key_id(v[e]));
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  // Bin (up to 128 keys, two per lane): keep the closest copy of each id
-  // that is not in the list yet.
-  uint64_t by_id[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int pos = e * 64 + lane;
-    const uint64_t b = pos < c ? bin_raw[e] : kEmpty;
-    by_id[e] = b == kEmpty ? kEmpty : (uint64_t(key_id(b)) << 32) | (b >> 32);
-  }
-  wave_sort_e<2>(by_id);
+  // Bin (up to 128 keys, two per lane): keep one copy of each id that is
+  // not in the list yet.  Copies of an id carry the same key (the distance
+  // of the same pair of rows, formed in the same order), so any copy will
+  // do: each bin id is inserted into the list's hash with the tag bit, and
+  // the lane whose insertion lands first keeps it.  (A 128-key sort by id
+  // did this before, at about twice the apply's VALU time.)
   uint64_t nk[2];
   int n_keep = 0;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    // Both shuffles run on every lane (a shuffle reads only active lanes).
-    const uint64_t up = shfl_u64(by_id[e], lane > 0 ? lane - 1 : 0);
-    const uint64_t tail = e > 0 ? shfl_u64(by_id[e > 0 ? e - 1 : 0], 63) : kEmpty;
-    const uint64_t prev = lane > 0 ? up : tail;
-    const uint32_t bid = uint32_t(by_id[e] >> 32);
-    const bool first = (e == 0 && lane == 0) || uint32_t(prev >> 32) != bid;
-    const bool keep = by_id[e] != kEmpty && first && !contains(bid);
-    nk[e] = keep ? ((by_id[e] & 0xffffffffull) << 32) | (uint64_t(bid) << 1) | 1ull : kEmpty;
+    const int pos = e * 64 + lane;
+    const uint64_t b = pos < c ? bin_raw[e] : kEmpty;
+    bool keep = false;
+    if (b != kEmpty) {
+      const uint32_t id = key_id(b);
+      uint32_t s = (id * 0x9E3779B1u) >> 23;
+      for (;;) {
+        const uint32_t old = atomicCAS(&h[s], kInvalid, id | kBinTag);
+        if (old == kInvalid) {
+          keep = true;
+          break;
+        }
+        if ((old & ~kBinTag) == id) break;
+        s = (s + 1u) & 511u;
+      }
+    }
+    nk[e] = keep ? (b | 1ull) : kEmpty;
     n_keep += popc(__ballot(keep));
   }
   if (n_keep <= 64) {
