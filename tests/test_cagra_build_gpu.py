@@ -74,6 +74,26 @@ def test_neighbour_quality_and_convergence(ctx, oracle):
     assert share > 0.9
 
 
+@pytest.mark.parametrize("iters", [0, 1, 2, 3])
+def test_iteration_limits(ctx, oracle, iters):
+    """The join's locality order is made after the first nn-descent
+    iteration: 0 iterations prune the bucketing lists in node order, 1 makes
+    the order and prunes in it, 2 and more also join in it.  Each graph is
+    valid, and joining improves the lists."""
+    rng = np.random.default_rng(33)
+    n, d = 3000, 48
+    base = clustered(rng, n, d)
+    graph, st = ctx.cagra_build(base, intermediate_degree=64, graph_degree=32, max_iterations=iters,
+                                termination_threshold=0.0)
+    check_graph(graph, n, 32)
+    assert st["iterations"] == iters
+    exact = oracle.knn_graph(base, 10, threads=16)
+    share = np.mean([len(set(exact[i].tolist()) & set(graph[i].tolist())) / 10 for i in range(n)])
+    print(f"iterations {iters}: share of exact 10-NN in the graph {share:.4f}", flush=True)
+    floor = {0: 0.2, 1: 0.95, 2: 0.99, 3: 0.99}[iters]  # measured 0.285, 0.981, 0.9997, 0.9999
+    assert share >= floor
+
+
 @pytest.mark.parametrize("n,d,g,itopk,rescore", [(8000, 128, 32, 64, False), (5000, 1024, 64, 64, False),
                                                  (5000, 1024, 64, 64, True), (6000, 99, 32, 64, True)])
 def test_downstream_recall_at_least_reference(ctx, oracle, n, d, g, itopk, rescore):
