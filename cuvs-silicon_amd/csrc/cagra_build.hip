@@ -179,8 +179,8 @@ __device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t
 
 // Gram columns of the local join: rows s_ids[0..m), 32 < m <= 32*R (or
 // m <= 32 with R = 1), staged CB bytes per row and step.  The calling wave
-// computes column tile `wave` against row tiles 0..T-1 into acc[0..T)
-// (T = 0: it only stages).  Every wave of the workgroup runs the same chunk
+// computes column tile `wave` against row tiles (row0 + t) % R, t < T, into
+// acc[0..T) (T = 0: it only stages).  Every wave of the workgroup runs the same chunk
 // steps and barriers whatever its T, so waves may run different T.  All tile
 // guards are resolved by the template, so each k-step's LDS operand reads
 // (one B tile, T A tiles) sit in one basic block with its T MFMAs and can be
@@ -188,10 +188,13 @@ __device__ __forceinline__ void gram_tiles(const char* __restrict__ x16, int64_t
 // after_issue() runs once the first NS chunks' gathers are issued: loads it
 // makes and waits for overlap them, and registers it holds are free again
 // before the Gram loop.
+constexpr int kJoinAcc = 3;  // accumulator tiles of a join wave (the most row tiles a role multiplies)
+
 template <int R, int T, int CB, class AfterIssue>
 __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t row_bytes, int m,
-                                          const uint32_t* s_ids, char* s_stage, int wave, f32x16 (&acc)[4],
-                                          AfterIssue&& after_issue) {
+                                          const uint32_t* s_ids, char* s_stage, int wave, int row0,
+                                          f32x16 (&acc)[kJoinAcc], AfterIssue&& after_issue) {
+  static_assert(T <= kJoinAcc, "accumulator tiles");
   static_assert(T >= 0 && T <= R, "row tiles");
   constexpr int M = 32 * R;
   constexpr int SEG = CB / 16;
@@ -211,17 +214,21 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
     dst[i] = r * STRIDE + seg * 16;
   }
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < kJoinAcc; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
   const int last = n_chunks - 1;
   const char* a_base = s_stage + (lane & 31) * STRIDE + 16 * (lane >> 5);
   const char* b_base = a_base + 32 * wave * STRIDE;
+  const char* a_tile[T > 0 ? T : 1];
+#pragma unroll
+  for (int t = 0; t < T; ++t) a_tile[t] = a_base + 32 * ((row0 + t) % R) * STRIDE;
   // NS register sets: chunk c + NS is gathered while chunk c is multiplied,
   // so each gather has NS chunks of work to arrive in (four for the small
-  // neighbourhoods that dominate once the lists settle, two for the largest,
-  // whose registers bound the kernel's occupancy).
-  constexpr int NS = R <= 2 ? 4 : 2;
+  // neighbourhoods that dominate once the lists settle, three for the
+  // largest, whose staging registers with the accumulators bound the
+  // kernel's occupancy).
+  constexpr int NS = R <= 2 ? 4 : 3;
   u32x4 reg[NS][LPT];
 #pragma unroll
   for (int k = 0; k < NS; ++k)
@@ -244,7 +251,7 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
         const half8 b = *reinterpret_cast<const half8*>(b_base + s * 32);
         half8 av[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) av[t] = *reinterpret_cast<const half8*>(a_base + 32 * t * STRIDE + s * 32);
+        for (int t = 0; t < T; ++t) av[t] = *reinterpret_cast<const half8*>(a_tile[t] + s * 32);
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], b, acc[t], 0, 0, 0);
       }
@@ -510,25 +517,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   // holds no new member: a prefix of `tiles` row tiles.  Tile (r, c) with
   // r < c serves column c from the registers of role c and, transposed
   // through LDS, column r.
-  f32x16 acc[4];
+  // When every row tile holds new members and there are 3 or 4, all pairs
+  // of tiles are needed, and the roles take circulant windows of row tiles
+  // instead (role c: tiles c, c + 1, and c + 2 for c < 2 when there are 4),
+  // which balances them at 3, 3, 2, 2 (2, 2, 2) tiles: no role multiplies 4,
+  // so kJoinAcc = 3 accumulator tiles serve every case.  Accumulator k holds
+  // row tile (row0 + k) % row_tiles.
+  f32x16 acc[kJoinAcc];
   const int role = (wave + int(blockIdx.x)) & 3;
   const int new_tiles = (mnew + 31) / 32;
   const int row_tiles = (m + 31) / 32;
-  const int tiles = role >= row_tiles ? 0 : role < new_tiles ? role + 1 : new_tiles;
+  const bool circulant = new_tiles == row_tiles && row_tiles >= 3;
+  const int tiles = role >= row_tiles ? 0
+                    : circulant       ? (row_tiles == 4 && role < 2 ? 3 : 2)
+                    : role < new_tiles ? role + 1
+                                       : new_tiles;
+  const int row0 = circulant ? role : 0;
   auto gram = [&](auto r_c) __attribute__((always_inline)) {
     constexpr int R = decltype(r_c)::value;
     auto run = [&](auto t_c) __attribute__((always_inline)) {
-      gram_join<R, decltype(t_c)::value, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, role, acc,
+      gram_join<R, decltype(t_c)::value, kJoinChunkBytes>(a.x16, a.row_bytes, m, s_ids, s_stage, role, row0, acc,
                                                           member_side);
     };
-    if (tiles == R) run(std::integral_constant<int, R>());
-    else if (tiles == 0) run(std::integral_constant<int, 0>());
+    if (tiles == 0) run(std::integral_constant<int, 0>());
+    else if (tiles == 1 || R == 1) run(std::integral_constant<int, 1>());
     else if constexpr (R >= 2) {
-      if (tiles == 1) run(std::integral_constant<int, 1>());
-      else if constexpr (R >= 3) {
-        if (tiles == 2) run(std::integral_constant<int, 2>());
-        else if constexpr (R >= 4) run(std::integral_constant<int, 3>());
-      }
+      if (tiles == 2 || R == 2) run(std::integral_constant<int, 2>());
+      else if constexpr (R >= 3) run(std::integral_constant<int, 3>());
     }
   };
   if (m <= 32) gram(std::integral_constant<int, 1>());
@@ -539,17 +554,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
   const int half = lane >> 5;
   float* s_tr = reinterpret_cast<float*>(s_stage);
-  // Tiles (t, role), t < role, transposed for role t: distance (i, j) of
-  // row i in tile t and column j in tile role at [i * kTrPitch + j].
+  // This role's tiles (t, role), t != role, transposed for role t: distance
+  // (i, j) of row i in tile t and column j in tile role at [i * kTrPitch + j]
+  // of the pair's slot.
 #pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    if (t >= tiles || t >= role) continue;
-    float* tr = s_tr + tr_pair(t, role) * 32 * kTrPitch;
+  for (int k = 0; k < kJoinAcc; ++k) {
+    if (k >= tiles) continue;
+    const int t = (row0 + k) % row_tiles;
+    if (t == role) continue;
+    float* tr = s_tr + tr_pair(min(t, role), max(t, role)) * 32 * kTrPitch;
     const float nj = s_norm[32 * role + (lane & 31)];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int i = 8 * (e >> 2) + 4 * half + (e & 3);
-      tr[i * kTrPitch + (lane & 31)] = s_norm[32 * t + i] + nj - 2.0f * acc[t][e];
+      tr[i * kTrPitch + (lane & 31)] = s_norm[32 * t + i] + nj - 2.0f * acc[k][e];
     }
   }
   __syncthreads();
@@ -565,32 +583,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     uint64_t best[kEmit];
 #pragma unroll
     for (int p = 0; p < kEmit; ++p) best[p] = kEmpty;
+    // A candidate pair (row member, this lane's column member) at distance
+    // dist: kept if it beats the column member's current worst neighbour.
+    auto consider = [&](int row, float dist) __attribute__((always_inline)) {
+      const uint32_t rid = s_ids[row];
+      if (rid == cid) return;
+      const uint64_t key = (uint64_t(ord_f32(dist)) << 32) | (uint64_t(rid) << 1) | 1ull;
+      if (key < worst && key < best[kEmit - 1]) {
+        best[kEmit - 1] = key;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (32 * t >= m) break;
-      // Row tile t from this role's registers, or (t > role) transposed from
-      // role t's; past them only pairs of two old members remain.
-      const bool own = t < tiles;
-      const float* tr = s_tr + (t > role ? tr_pair(role, t) : 0) * 32 * kTrPitch + (lane & 31) * kTrPitch;
+        for (int p = kEmit - 1; p > 0; --p) {
+          if (best[p] < best[p - 1]) {
+            const uint64_t tmp = best[p];
+            best[p] = best[p - 1];
+            best[p - 1] = tmp;
+          }
+        }
+      }
+    };
+    // Row tiles this role multiplied, from its accumulators.
+#pragma unroll
+    for (int k = 0; k < kJoinAcc; ++k) {
+      if (k >= tiles) break;
+      const int t = (row0 + k) % row_tiles;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = 32 * t + 8 * (e >> 2) + 4 * half + (e & 3);
         if (!col_ok || row >= m || !(col_new || row < mnew)) continue;
-        const uint32_t rid = s_ids[row];
-        if (rid == cid) continue;
-        const float dist = own ? cn + s_norm[row] - 2.0f * acc[t][e] : tr[row & 31];
-        const uint64_t key = (uint64_t(ord_f32(dist)) << 32) | (uint64_t(rid) << 1) | 1ull;
-        if (key < worst && key < best[kEmit - 1]) {
-          best[kEmit - 1] = key;
+        consider(row, cn + s_norm[row] - 2.0f * acc[k][e]);
+      }
+    }
+    // Row tiles another role multiplied, transposed through LDS; past them
+    // only pairs of two old members remain (skipped by the test below).
+    for (int t = 0; t < 4; ++t) {
+      if (32 * t >= m) break;
+      if (t == role || (t - row0 + row_tiles) % row_tiles < tiles) continue;
+      const float* tr = s_tr + tr_pair(min(t, role), max(t, role)) * 32 * kTrPitch + (lane & 31) * kTrPitch;
 #pragma unroll
-          for (int p = kEmit - 1; p > 0; --p) {
-            if (best[p] < best[p - 1]) {
-              const uint64_t tmp = best[p];
-              best[p] = best[p - 1];
-              best[p - 1] = tmp;
-            }
-          }
-        }
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * t + 8 * (e >> 2) + 4 * half + (e & 3);
+        if (!col_ok || row >= m || !(col_new || row < mnew)) continue;
+        consider(row, tr[row & 31]);
       }
     }
     // Merge with the partner lane's list (same column, the other 64 rows):
