@@ -828,8 +828,10 @@ __global__ __launch_bounds__(256) void label_round_kernel(const uint64_t* __rest
   const uint64_t key = lists[u * kp + min(j, kd - 1)];
   const uint32_t v = key == kEmpty ? uint32_t(u) : key_id(key);
   uint32_t m = in ? min(in[u], in[v]) : min(uint32_t(u), v);
-#pragma unroll
-  for (int o = kLabelK / 2; o >= 1; o >>= 1) m = min(m, xor_lanes(m, o));
+  m = min(m, xor_lanes<8>(m));
+  m = min(m, xor_lanes<4>(m));
+  m = min(m, xor_lanes<2>(m));
+  m = min(m, xor_lanes<1>(m));
   if (j == 0) out[u] = m;
 }
 
