@@ -82,11 +82,13 @@ struct SearchArgs {
   uint64_t* team_keys;  // teams > 1: (q * teams) x itopk list keys, merged afterwards
 };
 
-// Ascending bitonic sort of one 64-bit key per lane.
+// Ascending bitonic sort of one 64-bit key per lane, within each group of S
+// lanes (S = 64: the whole wave).
+template <int S = 64>
 __device__ __forceinline__ uint64_t wave_sort(uint64_t x) {
   const int lane = __lane_id();
 #pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
+  for (int size = 2; size <= S; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       const uint64_t y = shfl_xor_u64(x, stride);
@@ -316,12 +318,38 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
     }
     __syncthreads();
     if (lead) {
-      const uint64_t key =
+      uint64_t key =
           lane < nf ? (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1) : kEmptyKey;
-      merge_into<E>(top, wave_sort(key));
+      // A key at or above the list's itopk-th key cannot enter the list
+      // (keys are unique; an unfilled list holds the empty key there), so
+      // such candidates are dropped first: no sort at all when none is
+      // left, and a few are compacted into the first lanes (through the
+      // id/distance slots, which every wave has finished reading) and
+      // sorted over 16 or 32 lanes.  The merged list is the same.
+      const int wpos = a.itopk - 1;
+      uint64_t wv = top[0];
 #pragma unroll
-      for (int e = 0; e < E; ++e)
-        if (e * 64 + lane >= a.itopk) top[e] = kEmptyKey;
+      for (int e = 1; e < E; ++e)
+        if (e == (wpos >> 6)) wv = top[e];
+      const uint32_t wlo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(wv)), wpos & 63));
+      const uint32_t whi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(wv >> 32)), wpos & 63));
+      if (key >= ((uint64_t(whi) << 32) | wlo)) key = kEmptyKey;
+      const uint64_t m = __ballot(key != kEmptyKey);
+      const int cnt = popc(m);
+      if (cnt > 0) {
+        if (cnt <= 32) {
+          uint64_t* const s_keys = reinterpret_cast<uint64_t*>(s_ids);
+          if (key != kEmptyKey) s_keys[mbcnt(m)] = key;
+          key = lane < cnt ? s_keys[lane] : kEmptyKey;
+          key = cnt <= 16 ? wave_sort<16>(key) : wave_sort<32>(key);
+        } else {
+          key = wave_sort(key);
+        }
+        merge_into<E>(top, key);
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (e * 64 + lane >= a.itopk) top[e] = kEmptyKey;
+      }
     }
     // With one wave, program order alone separates this chunk's LDS reads
     // from the next chunk's writes; with more, the lead wave writes the next
@@ -597,7 +625,12 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   const int e_slots = itopk <= 64 ? 1 : (itopk <= 128 ? 2 : (itopk <= 256 ? 4 : 8));
   int64_t iters = max_iterations;
   if (iters == 0) iters = std::max<int64_t>(200, 2 * itopk / width);
-  const int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
+  const int waves = waves_per_query(q * teams);
+  // Several waves per query (small batches, at most a few workgroups per CU):
+  // a table four times larger, up to 32 KiB, keeps the lead wave's probe
+  // chains short.
+  int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
+  if (waves > 1) hash_bits = std::max(hash_bits, std::min(hash_bits + 2, 13));
   const size_t lds = (size_t(1) << hash_bits) * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4;
 
   SearchArgs a{};
@@ -636,7 +669,6 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
 
   const TimerSpan t0 = timer_span(ctx, "cagra_search");
   const dim3 grid(static_cast<unsigned>(q * teams));
-  const int waves = waves_per_query(q * teams);
   const bool f16 = idx->traversal_bits == 16;
   // The search kernel starts the span; the team merge (if any) ends it.
   hipEvent_t e1 = teams > 1 ? nullptr : t0.stop;
