@@ -23,8 +23,9 @@
 //    a stride of 256 bytes, so a row is gathered in coalesced 256-byte
 //    segments and one load instruction serves four rows).  The 64 keys are
 //    sorted with a wave bitonic sort and merged into the itopk list with a
-//    bitonic merge.
-//  - waves per query: 1 for large batches; up to 8 when the batch is small
+//    bitonic merge; candidates that cannot enter the list are dropped
+//    before the sort.
+//  - waves per query: 2 for large batches; 4 or 8 when the batch is small
 //    and each query's chain of dependent gathers is the latency (Q = 1).
 //
 // Iteration: pick the first `width` unexpanded entries of the list as
@@ -134,9 +135,10 @@ __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
 // One workgroup of W waves per query.  Wave 0 (the lead wave) owns the
 // itopk list, the hash inserts, the sort and the merge; all 4W 16-lane teams
 // gather candidate rows, so a chunk of 64 candidates costs ceil(64 / 4W)
-// dependent gather rounds instead of 16.  W = 1 for large batches (no
-// barriers between waves are needed), W > 1 when few queries would leave most
-// of the GPU idle and the search is latency-bound.
+// dependent gather rounds instead of 16.  The kernel also runs with W = 1 (no
+// barriers between waves are needed then); the host launches W = 2 for large
+// batches, where the other wave's gathers hide the lead wave's serial work,
+// and W = 4 or 8 when few queries would leave most of the GPU idle.
 template <int E, int W, bool F16>
 __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   extern __shared__ uint32_t s_mem[];
@@ -459,24 +461,23 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   }
 }
 
-// Waves per query: doubled while the grid stays within kWaveBudget waves (8
-// per CU), at most 8 (one query then gathers up to 32 rows per round).
-// Measured at N=100K D=1024 itopk 64 (kernel time, W = 1 / 2 / 4 / 8):
-// Q=1 0.82 / 0.51 / 0.40 / 0.34 ms, Q=100 0.91 / 0.58 / 0.47 / 0.41 ms,
-// Q=1,000 1.27 / 1.18 / 1.32 / 1.68 ms, Q=10,000 11.7 / 11.7 / 11.3 / 16.0 ms.
-constexpr int64_t kWaveBudget = 8 * 256;
-
-int waves_per_query(int64_t q) {
-  int w = 1;
-  while (w < 8 && q * w * 2 <= kWaveBudget) w *= 2;
-  return w;
+// Waves per query (workgroups = queries x teams): 8 up to 128 workgroups, 4
+// up to 512, else 2.  With 2 or more waves the lead wave's serial work (hash,
+// sort, merge) overlaps other queries' gathers on the same SIMD without
+// losing the gathering teams.  Wall time per batch at N=100K D=1024 itopk 64
+// with the visited-hash sizes below (fp16 / fp32 traversal):
+//   W=2: Q=1 0.28 / 0.33, Q=300 0.36 / 0.41, Q=1,000 0.42 / 0.63, Q=10,000 3.21 / 5.78 ms
+//   W=4: Q=1 0.22 / 0.26, Q=300 0.28 / 0.36, Q=1,000 0.57 / 0.76, Q=10,000 3.96 / 5.69 ms
+//   W=8: Q=1 0.23 / 0.26, Q=300 0.49 / 0.59, Q=1,000 1.00 / 1.20, Q=10,000 9.64 / 11.4 ms
+// (one wave per query: Q=10,000 4.62 / 8.45 ms with the smallest table).
+int waves_per_query(int64_t workgroups) {
+  return workgroups <= 128 ? 8 : (workgroups <= 512 ? 4 : 2);
 }
 
 template <int E, bool F16>
 void launch_search(int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a, hipEvent_t e0,
                    hipEvent_t e1) {
   switch (waves) {
-    case 1: hipExtLaunchKernelGGL((cagra_search_kernel<E, 1, F16>), grid, dim3(64), lds, stream, e0, e1, 0, a); break;
     case 2: hipExtLaunchKernelGGL((cagra_search_kernel<E, 2, F16>), grid, dim3(128), lds, stream, e0, e1, 0, a); break;
     case 4: hipExtLaunchKernelGGL((cagra_search_kernel<E, 4, F16>), grid, dim3(256), lds, stream, e0, e1, 0, a); break;
     default: hipExtLaunchKernelGGL((cagra_search_kernel<E, 8, F16>), grid, dim3(512), lds, stream, e0, e1, 0, a); break;
@@ -626,11 +627,14 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   int64_t iters = max_iterations;
   if (iters == 0) iters = std::max<int64_t>(200, 2 * itopk / width);
   const int waves = waves_per_query(q * teams);
-  // Several waves per query (small batches, at most a few workgroups per CU):
-  // a table four times larger, up to 32 KiB, keeps the lead wave's probe
-  // chains short.
+  // The visited hash at twice (W=2) or four times (W=4, 8) the size that
+  // keeps it half empty, up to 2^13 entries (32 KiB): the lead wave's probe
+  // chains stay short, and fewer mid-search clears mean fewer rows evaluated
+  // twice.  W=2 serves the large batches, where a 2^13 table would cost
+  // workgroups per CU (fp16 traversal, Q=10,000: 3.21 ms at 2^12, 3.70 ms at
+  // 2^13, 4.43 ms at 2^11).
   int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
-  if (waves > 1) hash_bits = std::max(hash_bits, std::min(hash_bits + 2, 13));
+  hash_bits = std::max(hash_bits, std::min(hash_bits + (waves >= 4 ? 2 : 1), 13));
   const size_t lds = (size_t(1) << hash_bits) * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4;
 
   SearchArgs a{};
