@@ -9,7 +9,7 @@ the restated reference search (oracle.cagra_reference_search: nearest
 navigation node entry, beam of itopk; shaders/cagra_kernels.metal:28-199) on
 the same graph, navigation nodes and queries, with the paired recall gate of
 tests/search_metrics.py, plus the output invariants:
-- Q = 10,000 in one call: one wave per query (the throughput kernel), fp32
+- Q = 10,000 in one call: two waves per query (the throughput kernel), fp32
   and fp16 traversal, search widths 1 and 4;
 - Q = 1, 100 separate calls: eight waves per query (the latency kernel);
 - 8 teams per query, each with a list of itopk 64, Q = 1,000 and Q = 1.
