@@ -329,13 +329,16 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
       // id/distance slots, which every wave has finished reading) and
       // sorted over 16 or 32 lanes.  The merged list is the same.
       const int wpos = a.itopk - 1;
-      uint64_t wv = top[0];
+      uint64_t worst = kEmptyKey;
 #pragma unroll
-      for (int e = 1; e < E; ++e)
-        if (e == (wpos >> 6)) wv = top[e];
-      const uint32_t wlo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(wv)), wpos & 63));
-      const uint32_t whi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(wv >> 32)), wpos & 63));
-      if (key >= ((uint64_t(whi) << 32) | wlo)) key = kEmptyKey;
+      for (int e = 0; e < E; ++e) {
+        if (e == (wpos >> 6)) {  // uniform: one slot is read
+          const uint32_t wlo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(top[e])), wpos & 63));
+          const uint32_t whi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(top[e] >> 32)), wpos & 63));
+          worst = (uint64_t(whi) << 32) | wlo;
+        }
+      }
+      if (key >= worst) key = kEmptyKey;
       const uint64_t m = __ballot(key != kEmptyKey);
       const int cnt = popc(m);
       if (cnt > 0) {
