@@ -367,6 +367,7 @@ __global__ __launch_bounds__(256) void two_hop_kernel(const float4* __restrict__
   __shared__ uint32_t s_nbr[kMaxG];
   __shared__ uint32_t s_ids[64];
   __shared__ float s_dist[64];
+  __shared__ uint64_t s_keys[32];
   __shared__ uint32_t s_ctl[2];
   const int tid = threadIdx.x, lane = tid & 63;
   const bool lead = __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
@@ -442,11 +443,16 @@ __global__ __launch_bounds__(256) void two_hop_kernel(const float4* __restrict__
     }
     __syncthreads();
     if (lead) {
-      uint64_t v[1] = {lane < nf ? (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1) : kNoKey};
-      wave_sort_e<1>(v);
-      uint64_t l[1] = {list};
-      wave_merge<1>(l, v[0]);
-      list = lane < g ? l[0] : kNoKey;
+      // Candidates at or above the list's g-th key cannot enter it (ids
+      // are unique here): no sort and merge when none is below it.
+      uint64_t key = lane < nf ? (uint64_t(ord_f32(s_dist[lane])) << 32) | (uint64_t(s_ids[lane]) << 1) : kNoKey;
+      const uint32_t glo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(list)), g - 1));
+      const uint32_t ghi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(list >> 32)), g - 1));
+      if (sort_below(key, (uint64_t(ghi) << 32) | glo, kNoKey, s_keys) > 0) {
+        uint64_t l[1] = {list};
+        wave_merge<1>(l, key);
+        list = lane < g ? l[0] : kNoKey;
+      }
     }
   }
   if (lead) {

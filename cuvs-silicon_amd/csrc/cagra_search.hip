@@ -83,24 +83,6 @@ struct SearchArgs {
   uint64_t* team_keys;  // teams > 1: (q * teams) x itopk list keys, merged afterwards
 };
 
-// Ascending bitonic sort of one 64-bit key per lane, within each group of S
-// lanes (S = 64: the whole wave).
-template <int S = 64>
-__device__ __forceinline__ uint64_t wave_sort(uint64_t x) {
-  const int lane = __lane_id();
-#pragma unroll
-  for (int size = 2; size <= S; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint64_t y = shfl_xor_u64(x, stride);
-      const bool lower = (lane & stride) == 0;
-      const bool asc = (lane & size) == 0;
-      x = (lower == asc) ? (x < y ? x : y) : (x < y ? y : x);
-    }
-  }
-  return x;
-}
-
 // Merges 64 sorted keys `c` (one per lane) into the sorted list `top` of
 // 64*E keys, keeping the 64*E smallest.  min(top[i], c'[N-1-i]) with c'
 // = c padded by empty keys is bitonic; half-cleaners then sort it.
@@ -338,18 +320,7 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
           worst = (uint64_t(whi) << 32) | wlo;
         }
       }
-      if (key >= worst) key = kEmptyKey;
-      const uint64_t m = __ballot(key != kEmptyKey);
-      const int cnt = popc(m);
-      if (cnt > 0) {
-        if (cnt <= 32) {
-          uint64_t* const s_keys = reinterpret_cast<uint64_t*>(s_ids);
-          if (key != kEmptyKey) s_keys[mbcnt(m)] = key;
-          key = lane < cnt ? s_keys[lane] : kEmptyKey;
-          key = cnt <= 16 ? wave_sort<16>(key) : wave_sort<32>(key);
-        } else {
-          key = wave_sort(key);
-        }
+      if (sort_below(key, worst, kEmptyKey, reinterpret_cast<uint64_t*>(s_ids)) > 0) {
         merge_into<E>(top, key);
 #pragma unroll
         for (int e = 0; e < E; ++e)

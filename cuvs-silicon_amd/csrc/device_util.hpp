@@ -102,6 +102,48 @@ __device__ __forceinline__ uint64_t shfl_u64(uint64_t x, int src_lane) {
   return (uint64_t(hi) << 32) | lo;
 }
 
+// Ascending bitonic sort of one 64-bit key per lane, within each group of S
+// lanes (S = 64: the whole wave).
+template <int S = 64>
+__device__ __forceinline__ uint64_t wave_sort_lanes(uint64_t x) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int size = 2; size <= S; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t y = shfl_xor_u64(x, stride);
+      const bool lower = (lane & stride) == 0;
+      const bool asc = (lane & size) == 0;
+      x = (lower == asc) ? (x < y ? x : y) : (x < y ? y : x);
+    }
+  }
+  return x;
+}
+
+// Candidate keys (one per lane, `empty` for none) ahead of a merge into a
+// sorted list whose last kept entry is `bound`: keys at or above it cannot
+// enter the list (keys are unique) and become `empty`; the rest are sorted
+// ascending into the first lanes, `empty` after them.  A few survivors are
+// compacted through `scratch` (32 keys of LDS that only this wave uses here)
+// and sorted over 16 or 32 lanes (10 or 15 steps instead of 21).  Returns
+// the survivor count; with none the key is left unsorted and the merge can
+// be skipped.
+__device__ __forceinline__ int sort_below(uint64_t& key, uint64_t bound, uint64_t empty, uint64_t* scratch) {
+  if (key >= bound) key = empty;
+  const uint64_t m = __ballot(key != empty);
+  const int cnt = popc(m);
+  if (cnt == 0) return 0;
+  if (cnt <= 32) {
+    const int lane = __lane_id();
+    if (key != empty) scratch[mbcnt(m)] = key;
+    key = lane < cnt ? scratch[lane] : empty;
+    key = cnt <= 16 ? wave_sort_lanes<16>(key) : wave_sort_lanes<32>(key);
+  } else {
+    key = wave_sort_lanes<64>(key);
+  }
+  return cnt;
+}
+
 // Ascending wave-level bitonic sort of 64*E keys (position i = 64*slot + lane).
 template <int E>
 __device__ __forceinline__ void wave_sort_e(uint64_t (&v)[E]) {
