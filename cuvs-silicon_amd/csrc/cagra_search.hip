@@ -12,11 +12,13 @@
 //        ord(distance) << 32 | id << 1 | expanded
 //    so the order is (distance, id) and marking an entry expanded never
 //    reorders the list.
-//  - visited set: an open-addressing hash of 2^hash_bits ids in LDS, filled to
-//    at most one half.  When the next iteration could overflow that, the
-//    table is cleared and the ids of the itopk list re-inserted: an id that
-//    left the list can be evaluated again, but can never re-enter it (its key
-//    is above the list's current worst), so the list never holds duplicates.
+//  - visited set: a bitmap of n bits in LDS when that is no larger than the
+//    hash below (n <= 131,072 or 262,144); else an open-addressing hash of
+//    2^hash_bits ids, filled to at most one half.  When the next iteration
+//    could overflow the hash, it is cleared and the ids of the itopk list
+//    re-inserted: an id that left the list can be evaluated again, but can
+//    never re-enter it (its key is above the list's current worst), so the
+//    list never holds duplicates and does not depend on which set is used.
 //  - candidates: processed 64 at a time (one id per lane of the lead wave).
 //    New ids pass the hash, are compacted into LDS, and their distances are
 //    computed by the 16-lane teams of all waves (each lane reads 16 bytes at
@@ -79,6 +81,7 @@ struct SearchArgs {
   int width;
   int max_iter;
   int hash_bits;
+  int bitmap_words;     // > 0: the visited set is a bitmap of this many words (n bits, rounded up)
   int teams;            // workgroups per query (block b = query b / teams, team b % teams)
   uint64_t* team_keys;  // teams > 1: (q * teams) x itopk list keys, merged afterwards
 };
@@ -124,9 +127,11 @@ __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
 template <int E, int W, bool F16>
 __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   extern __shared__ uint32_t s_mem[];
-  const int H = 1 << a.hash_bits;
+  const bool bitmap = a.bitmap_words > 0;
+  const int H = bitmap ? a.bitmap_words : 1 << a.hash_bits;  // visited-set words
   const uint32_t hmask = uint32_t(H) - 1u;
-  const int hcap = H / 2;
+  const int hcap = bitmap ? (1 << 30) : H / 2;  // a bitmap is never cleared
+  const uint32_t hempty = bitmap ? 0u : kInvalidId;
   uint32_t* s_hash = s_mem;
   uint32_t* s_ids = s_mem + H;                           // 64 fresh ids
   float* s_dist = reinterpret_cast<float*>(s_ids + 64);  // their distances
@@ -146,7 +151,7 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   const int tm = int(blockIdx.x - qi * a.teams);
   const int team = tid >> 4, tp = lane & 15;
 
-  for (int i = tid; i < H; i += kThreads) s_hash[i] = kInvalidId;
+  for (int i = tid; i < H; i += kThreads) s_hash[i] = hempty;
 
   // Query slice of this lane.  fp32 traversal: float4 columns tp + 16 j of
   // the padded row.  fp16 traversal (and its fp32 re-rank): 8-column pieces
@@ -250,7 +255,12 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   int phase = 0;       // alternates the fresh-count slot
   __syncthreads();
 
+  // Marks id (< n) visited; true if it was not.
   auto hash_insert = [&](uint32_t id) -> bool {
+    if (bitmap) {
+      const uint32_t bit = 1u << (id & 31u);
+      return (atomicOr(&s_hash[id >> 5], bit) & bit) == 0u;
+    }
     uint32_t h = (id * 0x9E3779B1u) >> (32 - a.hash_bits);
     for (;;) {
       const uint32_t old = atomicCAS(&s_hash[h], kInvalidId, id);
@@ -262,7 +272,7 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
 
   auto reset_hash = [&]() {
     __syncthreads();
-    for (int i = tid; i < H; i += kThreads) s_hash[i] = kInvalidId;
+    for (int i = tid; i < H; i += kThreads) s_hash[i] = hempty;
     __syncthreads();
     if (lead) {
       int c = 0;
@@ -609,7 +619,13 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   // 2^13, 4.43 ms at 2^11).
   int hash_bits = std::max(11, ceil_log2(2 * (64 * e_slots + std::max<int64_t>(64, per_iter))));
   hash_bits = std::max(hash_bits, std::min(hash_bits + (waves >= 4 ? 2 : 1), 13));
-  const size_t lds = (size_t(1) << hash_bits) * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4;
+  // A bitmap of the n rows where it takes no more LDS than the hash: one
+  // atomic per id, no probing, never cleared.  Whole 256-byte blocks keep the
+  // words after it 8-byte aligned.
+  const int64_t bitmap_words = (idx->n + 2047) / 2048 * 64;
+  const bool use_bitmap = bitmap_words <= (int64_t(1) << hash_bits);
+  const size_t visit_words = use_bitmap ? size_t(bitmap_words) : (size_t(1) << hash_bits);
+  const size_t lds = visit_words * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4;
 
   SearchArgs a{};
   a.rows = reinterpret_cast<const float4*>(idx->rows);
@@ -638,6 +654,7 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.width = int(width);
   a.max_iter = int(std::min<int64_t>(iters, INT32_MAX));
   a.hash_bits = hash_bits;
+  a.bitmap_words = use_bitmap ? int(bitmap_words) : 0;
   a.teams = teams;
   if (teams > 1) {
     ctx->ws_teams.reserve(size_t(q) * size_t(teams) * size_t(itopk) * sizeof(uint64_t));
