@@ -23,8 +23,9 @@
 
 /* ORACLE_PLANT selects one deliberate mistake for the pinning tests, which
  * build such variants of this file into temporary libraries and check that
- * their known answers reject them (tests/test_oracle_build.py).  0, the
- * default, is the restatement itself. */
+ * their known answers reject them (tests/test_oracle_build.py,
+ * tests/test_oracle_build_stages.py).  0, the default, is the restatement
+ * itself. */
 #ifndef ORACLE_PLANT
 #define ORACLE_PLANT 0
 #endif
@@ -385,12 +386,21 @@ void oracle_ivf_seed(const float* data, int64_t n, int64_t d, uint32_t g, const 
 void oracle_bucketing_perm(int64_t n, uint32_t* perm) {
   for (int64_t i = 0; i < n; ++i) perm[i] = (uint32_t)i;
   uint64_t r = 0xFEDCBA9876543210ULL;
+#if ORACLE_PLANT == 13
+  for (int64_t i = 1; i < n; ++i) {
+#else
   for (int64_t i = n - 1; i > 0; --i) {
+#endif
+#if ORACLE_PLANT != 14
     r = r * 6364136223846793005ULL + 1442695040888963407ULL;
-    const int64_t j = (int64_t)(r >> 33) % (i + 1);
+#endif
+    const int64_t j = (int64_t)(r >> (ORACLE_PLANT == 12 ? 32 : 33)) % (i + 1);
     const uint32_t tmp = perm[i];
     perm[i] = perm[j];
     perm[j] = tmp;
+#if ORACLE_PLANT == 14
+    r = r * 6364136223846793005ULL + 1442695040888963407ULL;
+#endif
   }
 }
 

@@ -159,10 +159,13 @@ void oracle_ivf_seed(const float* data, int64_t n, int64_t d, uint32_t g, const 
                      const uint32_t* nearc, int64_t n_probe, int64_t max_own, const uint8_t* codes,
                      const float* lut, uint32_t* graph, float* gdist, int threads);
 
-/* The bucketing permutation (src/metal_context.mm:802-810).  Pinned: a
- * permutation; its values against a second restatement from the
- * reference's text (parity unpinned beyond that: the reference ships no
- * permutation output). */
+/* The bucketing permutation (src/metal_context.mm:802-810).  Pinned without
+ * re-running the loop: the swap index of every step is recovered from the
+ * output by inverting the Fisher-Yates shuffle and must equal
+ * (x_k >> 33) mod (i + 1), where x_k, the generator's state after k = n - i
+ * steps, is computed in closed form (LCG jump-ahead by repeated squaring);
+ * a shift of 32, ascending i, and the generator advanced after the swap
+ * each fail that check (tests/test_oracle_build_stages.py). */
 void oracle_bucketing_perm(int64_t n, uint32_t* perm);
 
 /* One random-bucketing pass (shaders/cagra_kernels.metal:403-462) over

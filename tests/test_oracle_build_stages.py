@@ -24,8 +24,10 @@ Stages and the mistakes their checks reject:
   set - plants 6 (two probes) and 7 (no cap); with product-quantisation codes
   (:614-681) it equals the exact form on rows built from the quantisation
   prototypes - plant 8 (seven of the eight subspaces summed).
-- bucketing_perm (:802-810): a permutation equal to a second restatement of
-  the reference's LCG from its text.
+- bucketing_perm (:802-810): every swap index, recovered from the output by
+  inverting the Fisher-Yates shuffle, equals (x_k >> 33) mod (i + 1) with the
+  generator state x_k in closed form (jump-ahead) - plants 12 (shift 32), 13
+  (ascending i) and 14 (generator advanced after the swap).
 - bucketing_merge (kernel :403-462): every row gets its min(g, 64) nearest
   bucket mates, and a mate already in the row is inserted again - plant 9
   (duplicates dropped).
@@ -218,23 +220,94 @@ def test_pq_seed_equals_exact_seed_on_prototype_rows(oracle, planted):
 
 # ---- random bucketing --------------------------------------------------------
 
-def lcg_permutation(n):
-    """The reference's bucketing permutation restated from its text
-    (src/metal_context.mm:802-810), in Python integers."""
-    p = list(range(n))
-    r = 0xFEDCBA9876543210
+LCG_A = 6364136223846793005
+LCG_C = 1442695040888963407
+LCG_X0 = 0xFEDCBA9876543210
+M64 = (1 << 64) - 1
+
+
+def lcg_state(k):
+    """State of the reference's generator after k steps (src/metal_context.mm:
+    802-810), in closed form: x_k = a^k x_0 + c (1 + a + ... + a^(k-1)) mod
+    2^64, with a^k and the geometric sum by repeated squaring (the sum over
+    2m terms is the sum over m terms times 1 + a^m), not by stepping."""
+    def power_and_sum(m):
+        if m == 0:
+            return 1, 0
+        p, s = power_and_sum(m // 2)
+        p2, s2 = (p * p) & M64, (s * (1 + p)) & M64
+        if m & 1:
+            p2, s2 = (p2 * LCG_A) & M64, (1 + LCG_A * s2) & M64
+        return p2, s2
+    ak, sk = power_and_sum(k)
+    return (ak * LCG_X0 + LCG_C * sk) & M64
+
+
+def test_lcg_state_closed_form():
+    """The repeated-squaring form against direct stepping for the first
+    steps, and against the geometric sum (a^k - 1) / (a - 1) taken exactly
+    (a^k modulo (a - 1) 2^64, then divided) at large k."""
+    x = LCG_X0
+    for k in range(1, 200):
+        x = (x * LCG_A + LCG_C) & M64
+        assert lcg_state(k) == x
+    for k in (12345, 100_002, 1 << 40):
+        mod = (LCG_A - 1) << 64
+        geo = ((pow(LCG_A, k, mod) - 1) % mod) // (LCG_A - 1)
+        assert lcg_state(k) == (pow(LCG_A, k, 1 << 64) * LCG_X0 + LCG_C * geo) & M64
+
+
+def fisher_yates_swaps(perm):
+    """Swap indices j_i (i = n-1 down to 1) of a descending Fisher-Yates
+    shuffle of the identity that produced `perm`.  Step i swaps positions i
+    and j_i and never touches position i again, so perm[i] is the value at
+    position j_i just before step i: the steps are replayed forward on an
+    index of where each value sits.  Returns None if `perm` is not the output
+    of such a shuffle (a recovered index above i)."""
+    n = len(perm)
+    cur = list(range(n))          # values by position before the next step
+    where = list(range(n))        # position of each value
+    swaps = {}
     for i in range(n - 1, 0, -1):
-        r = (r * 6364136223846793005 + 1442695040888963407) % (1 << 64)
-        j = (r >> 33) % (i + 1)
-        p[i], p[j] = p[j], p[i]
-    return p
+        j = where[perm[i]]
+        if j > i:
+            return None
+        swaps[i] = j
+        vi, vj = cur[i], cur[j]
+        cur[i], cur[j] = vj, vi
+        where[vi], where[vj] = j, i
+    return swaps
 
 
-@pytest.mark.parametrize("n", [1, 2, 10, 1000, 100_003])
-def test_bucketing_perm(oracle, n):
-    perm = oracle.bucketing_perm(n)
-    assert sorted(perm.tolist()) == list(range(n))
-    assert perm.tolist() == lcg_permutation(n)
+def check_bucketing_perm(perm, sample=None, seed=3):
+    """Every recovered swap index (or a sample of them) equals
+    (x_(n-i) >> 33) mod (i + 1) with x_k from the closed form."""
+    n = len(perm)
+    if sorted(perm) != list(range(n)):
+        return False
+    swaps = fisher_yates_swaps(perm)
+    if swaps is None:
+        return False
+    steps = list(range(n - 1, 0, -1))
+    if sample is not None and len(steps) > sample:
+        rng = np.random.default_rng(seed)
+        steps = sorted(set(rng.choice(steps, sample, replace=False).tolist()) | {n - 1, 1})
+    return all(swaps[i] == (lcg_state(n - i) >> 33) % (i + 1) for i in steps)
+
+
+@pytest.mark.parametrize("n,sample", [(1, None), (2, None), (10, None), (1000, None), (100_003, 400)])
+def test_bucketing_perm(oracle, n, sample):
+    assert check_bucketing_perm(oracle.bucketing_perm(n).tolist(), sample)
+
+
+@pytest.mark.parametrize("plant", [12, 13, 14])
+def test_bucketing_perm_rejects_planted_mistakes(oracle, planted, plant):
+    """Plants: 12 shifts by 32, 13 runs i upwards, 14 advances the generator
+    after the swap; each must fail the closed-form check."""
+    with oracle.variant(planted(plant)):
+        for n in (10, 1000):
+            perm = oracle.bucketing_perm(n).tolist()
+            assert not check_bucketing_perm(perm)
 
 
 def bucket_rows(n, seed=9):
