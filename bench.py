@@ -339,7 +339,9 @@ def run_bf(args) -> int:
     # no timestamps; then each kernel's duration from its own dispatch
     # timestamps over K more searches (the timestamps lengthen a step by
     # ~24 us of the four dispatches' bookkeeping, not the kernels).
+    ctx.bf_escalations(reset=True)
     elapsed, kavg = timed_steps(ctx, step, args.steps, families)
+    escalated, rescanned = ctx.bf_escalations(reset=True)
     ms_per_step = 1e3 * elapsed / args.steps
     qps = q * args.steps / elapsed
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step, {qps:.0f} QPS")
@@ -385,6 +387,11 @@ def run_bf(args) -> int:
             "step_frac": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         },
         "kernel_avg_ms": kavg,
+        # Queries (over both passes of timed_steps) whose fp16 candidate
+        # selection was not certified exact and were re-ranked over more
+        # rows: from the candidate lists, or over every row.
+        "uncertified_queries": {"escalated": escalated, "rescanned_all_rows": rescanned,
+                                "of": 2 * args.steps * q},
         "settle": {"ms": args.settle_ms, "steps": settle_steps},
         "reference_published_qps_m3max": REF_M3MAX_QPS,
     }
@@ -496,7 +503,9 @@ def leg_c3(cvs, ctx, ds, base, args) -> dict:
     stepf = lambda: ds.bf_search_async(dq, k, dn, dd)
     for _ in range(2):
         stepf()
+    ctx.bf_escalations(reset=True)
     dt, kt = timed_steps(ctx, stepf, 3, ("bf_prep", "bf_sample", "bf_scan", "bf_merge"))
+    escalated, rescanned = ctx.bf_escalations(reset=True)
     dt /= 3
     nbr = dn.to_host()
     sample = np.random.default_rng(0).choice(q, 100, replace=False)
@@ -507,7 +516,8 @@ def leg_c3(cvs, ctx, ds, base, args) -> dict:
            "scan_tflops": flops / (kt["bf_scan"] * 1e-3) / 1e12,
            "scan_mfma_frac": flops / (kt["bf_scan"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
            "step_mfma_frac": flops / dt / 1e12 / MFMA_F16_PEAK_TFLOPS,
-           "recall_at_100_sampled": recall_at_k(nbr[sample], gt_i, k), "recall_queries": len(sample)}
+           "recall_at_100_sampled": recall_at_k(nbr[sample], gt_i, k), "recall_queries": len(sample),
+           "uncertified_queries": {"escalated": escalated, "rescanned_all_rows": rescanned, "of": 6 * q}}
     if not args.no_cpu_baseline:
         sub = qs[:200]
         t0 = time.perf_counter()

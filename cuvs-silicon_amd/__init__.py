@@ -115,6 +115,7 @@ _SIGNATURES["cvs_cagra_build_ex"] = (c_int, [c_void_p, c_void_p, c_int64, c_int6
 
 _SIGNATURES["cvs_bf_search_noalloc"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p])
 _SIGNATURES["cvs_cagra_nav_nodes"] = (c_int, [c_int64, c_void_p, POINTER(c_int64)])
+_SIGNATURES["cvs_context_bf_escalations"] = (c_int, [c_void_p, POINTER(c_uint64), POINTER(c_uint64), c_int])
 
 # The bucketing permutation seed of the reference (src/metal_context.mm:803).
 DEFAULT_BUILD_SEED = 0xFEDCBA9876543210
@@ -283,6 +284,15 @@ class Context:
         n = c_uint64(0)
         _check(load().cvs_context_kernel_time(self.handle, kernel.encode(), byref(ms), byref(n)))
         return ms.value, int(n.value)
+
+    def bf_escalations(self, reset: bool = False):
+        """(escalated, rescanned): brute-force queries whose fp16 selection
+        was not certified and were re-ranked exactly over more rows, and how
+        many of those over every row (C: cvs_context_bf_escalations)."""
+        esc = c_uint64(0)
+        full = c_uint64(0)
+        _check(load().cvs_context_bf_escalations(self.handle, byref(esc), byref(full), 1 if reset else 0))
+        return int(esc.value), int(full.value)
 
     def dataset(self, rows) -> "Dataset":
         return Dataset(self, rows)

@@ -132,6 +132,8 @@ struct GemmArgs {
   const float* thr0;    // per-query initial threshold
   uint64_t* part;       // [nq][n_lists][CAP] lists
   uint64_t* lmin;       // [nq][n_lists] smallest key of each list
+  float* lcut;          // [nq][n_lists] final threshold of each list (rows it covers and does
+                        // not hold have keys at or above it; +inf for an unused list)
   int n_lists;          // lists per query
 };
 

@@ -414,7 +414,11 @@ void bf_gemm_scan_kernel(GemmArgs a) {
           const uint64_t y = shfl_xor_u64(m, o);
           m = y < m ? y : m;
         }
-        if (lane == 0) a.lmin[int64_t(q) * G + slot] = m;
+        const float cut = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(thr[j]), i));
+        if (lane == 0) {
+          a.lmin[int64_t(q) * G + slot] = m;
+          a.lcut[int64_t(q) * G + slot] = cut;
+        }
       }
     }
   };
@@ -429,7 +433,10 @@ void bf_gemm_scan_kernel(GemmArgs a) {
         uint64_t* lst = a.part + (int64_t(q) * G + sl) * GL::CAP;
 #pragma unroll
         for (int t = 0; t < kKP / 64; ++t) lst[lane + 64 * t] = kSentinel;
-        if (lane == 0) a.lmin[int64_t(q) * G + sl] = kSentinel;
+        if (lane == 0) {
+          a.lmin[int64_t(q) * G + sl] = kSentinel;
+          a.lcut[int64_t(q) * G + sl] = INFINITY;  // covers no rows
+        }
       }
   };
 

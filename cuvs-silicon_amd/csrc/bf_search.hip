@@ -96,6 +96,8 @@ struct ScanArgs {
   int qb_fast;          // 1: linear block id = range * n_qblocks + qblock
   float* sgmin;         // sample: [nq][2 * n_ranges] minima of each lane's sampled rows
   uint64_t* lmin;       // scan: [nq][n_ranges] smallest key of each list (sentinel if empty)
+  float* lcut;          // scan: [nq][n_ranges] final threshold of each list: every row of the
+                        // range that is not in its list has a distance key at or above it
   int64_t s_units;      // sample: number of sampled units
   int64_t s_stride;     // sample: unit stride
 };
@@ -543,7 +545,10 @@ void bf_scan_kernel(ScanArgs a) {
       }
       const uint64_t y = shfl_xor_u64(mn, 32);
       mn = y < mn ? y : mn;
-      if (half == 0 && q < a.nq) a.lmin[int64_t(q) * G + x] = mn;
+      if (half == 0 && q < a.nq) {
+        a.lmin[int64_t(q) * G + x] = mn;
+        a.lcut[int64_t(q) * G + x] = thr;
+      }
       return;
     }
     for (int i = 0; i < 32; ++i) {
@@ -582,20 +587,28 @@ void bf_scan_kernel(ScanArgs a) {
         const uint64_t y = shfl_xor_u64(mn, o);
         mn = y < mn ? y : mn;
       }
-      if (lane == 0) a.lmin[int64_t(q) * G + x] = mn;
+      const float cut = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(thr), i));
+      if (lane == 0) {
+        a.lmin[int64_t(q) * G + x] = mn;
+        a.lcut[int64_t(q) * G + x] = cut;
+      }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Queries fp32 -> fp16 tiles (the dataset's tile layout) + squared norms of
-// the fp16-rounded rows, one wave per query: lane l converts columns
-// [16*l', 16*l'+16) for l' = l, l+64, ...; the norm is a fixed-order wave
-// reduction.  Rows of the last tile beyond q are zero with norm +inf.
+// Queries fp32 -> fp16 tiles of scale * (q - mu) (the dataset's tile layout
+// and centring) + squared norms of the fp16-rounded rows, one wave per
+// query: lane l converts columns [16*l', 16*l'+16) for l' = l, l+64, ...; the
+// norm is a fixed-order wave reduction.  qerr receives the squared rounding
+// error |q~ - scale fl(q - mu)|^2 of each query (for the certificate in the
+// merge).  Rows of the last tile beyond q are zero with norm +inf.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restrict__ queries, int64_t q,
                                                           int64_t d, int ksteps, int64_t q_rows,
-                                                          u32x4* __restrict__ qtiles, float* __restrict__ qnorms) {
+                                                          const float* __restrict__ mu, float scale,
+                                                          u32x4* __restrict__ qtiles, float* __restrict__ qnorms,
+                                                          float* __restrict__ qerr) {
   const int lane = threadIdx.x & 63;
   const int64_t r = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (r >= q_rows) return;
@@ -603,7 +616,7 @@ __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restric
   const float* src = queries + (ok ? r : 0) * d;
   const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0;
   const int64_t t = r >> 5;
-  float acc = 0.f;
+  float acc = 0.f, err = 0.f;
   for (int s = lane; s < ksteps; s += 64) {
 #pragma unroll
     for (int hpart = 0; hpart < 2; ++hpart) {
@@ -618,12 +631,16 @@ __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restric
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = (ok && c0 + j < d) ? src[c0 + j] : 0.f;
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (ok && c0 + j < d) ? (v[j] - mu[c0 + j]) * scale : 0.f;
       _Float16 h[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         h[j] = static_cast<_Float16>(v[j]);
         const float hv = static_cast<float>(h[j]);
         acc += hv * hv;
+        const float e = hv - v[j];
+        err += e * e;
       }
       u32x4 packed;
       __builtin_memcpy(&packed, h, sizeof(packed));
@@ -632,8 +649,14 @@ __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restric
     }
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += xor_lanes_f(acc, o);
-  if (lane == 0) qnorms[r] = ok ? acc : INFINITY;
+  for (int o = 32; o >= 1; o >>= 1) {
+    acc += xor_lanes_f(acc, o);
+    err += xor_lanes_f(err, o);
+  }
+  if (lane == 0) {
+    qnorms[r] = ok ? acc : INFINITY;
+    if (ok) qerr[r] = err;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -673,81 +696,120 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Exact re-rank and output of one query's kp candidates (ids in s_cid,
-// 0xffffffff for none), by the four waves of a workgroup: exact fp32
-// distances from the fp32 rows, 4 candidates per wave at a time, then wave
-// 0 sorts them by (distance, id) and writes k results, padded with
-// UINT32_MAX / +inf (src/cagra.cpp:240-251).  Ends the kernel for waves
-// other than 0.
+// Certificate of the fp16 selection.  A row's key is d~ = |q~|^2 + |x~|^2 -
+// 2 q~.x~ in fp32, with q~, x~ the fp16 copies of s (q - mu), s (x - mu).  For
+// the scaled exact distance D = s^2 |q - x|^2:
+//   |d~ - |q~ - x~|^2| <= A = 2 (d + 16) 2^-24 (|q~| + rmax)^2
+// (fp32 sums of d terms, including an MFMA accumulation that rounds twice
+// per step, and the two final operations), and
+//   | |q~ - x~| - sqrt(D) | <= E = |q~ - s(q - mu)| + dx
+// (triangle inequality; dx bounds every row's rounding, measured when the
+// dataset was made).  Hence D >= lb(d~) = (sqrt(d~ - A) - E)^2 when
+// sqrt(d~ - A) > E, and 0 otherwise: a row whose key is at least T has an
+// exact distance of at least lb(T) / s^2.
+//
+// The merge re-ranks the R smallest keys it holds exactly in fp32.  Every row
+// not re-ranked has a key at or above T = min(key of the R-th candidate, the
+// smallest final list threshold T*) (a list keeps every key of its range
+// below its threshold).  If lb(T) exceeds s^2 d_k (1 + rho), with d_k the
+// k-th exact distance and rho the relative error of the fp32 distances
+// themselves, the result is the exact top k.  Otherwise the query
+// escalates: every row with a key up to T_need = (sqrt(s^2 d_k (1 + rho)) +
+// E)^2 + A (all of them are in the lists when T_need <= T*), or else every
+// row of the dataset, is re-ranked exactly, and the top k of those is the
+// answer.
 // ---------------------------------------------------------------------------
-template <int E>
-__device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s_cd, int kp, const float* rows,
-                                                 int64_t n, int64_t d, const float* qv, int64_t q, int64_t k,
-                                                 uint32_t* out_nbr, float* out_dist) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(qv) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
-  for (int c = 4 * wave; c < kp; c += 4 * kWaves) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    uint32_t id[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      // An id that is not a row (never produced by a scan) counts as empty.
-      id[u] = c + u < kp ? s_cid[c + u] : 0xffffffffu;
-      if (int64_t(id[u]) >= n) id[u] = 0xffffffffu;
-    }
-    if (vec) {
-      // Four 256-column chunks per pass, all loads issued before the first
-      // is used (one HBM round trip per pass for d <= 1024).
-      for (int64_t i0 = int64_t(lane) * 4; i0 < d; i0 += 4 * 256) {
-        float4 a4[4], b4[4][4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int64_t i = i0 + c * 256;
-          a4[c] = i < d ? *reinterpret_cast<const float4*>(qv + i) : float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            b4[c][u] = (i < d && id[u] != 0xffffffffu) ? *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i)
-                                                        : float4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float t0 = a4[c].x - b4[c][u].x, t1 = a4[c].y - b4[c][u].y;
-            const float t2 = a4[c].z - b4[c][u].z, t3 = a4[c].w - b4[c][u].w;
-            acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
-          }
-      }
-    } else {
-      for (int64_t i = lane; i < d; i += 64) {
-        const float a1 = qv[i];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (id[u] == 0xffffffffu) continue;
-          const float t = a1 - rows[int64_t(id[u]) * d + i];
-          acc[u] += t * t;
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc[u] += xor_lanes_f(acc[u], o);
-      if (lane == 0 && c + u < kp) s_cd[c + u] = acc[u];
-    }
-  }
-  __syncthreads();
+struct Cert {
+  float s2;              // scale^2: key units per squared distance unit
+  float rmax;            // every row: |x~| <= rmax (scaled units)
+  float dx;              // every row: |x~ - s (x - mu)| <= dx
+  float a_coef;          // 2 (d + 16) 2^-24
+  float rho;             // 2 (d + 8) 2^-24
+  float qslack;          // sqrt(d) 2^-25 + fp32 error of a query's centring
+  const float* qnorms;   // |q~|^2 per query
+  const float* qerr;     // |q~ - s fl(q - mu)|^2 per query
+  unsigned long long* counters;  // [0] escalated queries, [1] of them re-ranked over every row
+};
 
-  if (wave != 0) return;
-  uint64_t fin[E];
+enum { kCertPass = 0, kCertKeys = 1, kCertAll = 2 };
+
+// Exact squared L2 distances of U rows to the query by the 64 lanes of the
+// calling wave (ids >= n count as none and give 0).  The summation order is
+// fixed: per lane, float4 partial sums over its 4-column pieces of 256-column
+// chunks, then a butterfly, so a row always gets the same value.  All row
+// loads of a 1024-column pass are issued before the first is used.
+template <int U>
+__device__ __forceinline__ void wave_exact(const uint32_t (&id)[U], const float* __restrict__ rows, int64_t n,
+                                           int64_t d, const float* __restrict__ qv, bool vec, float (&out)[U]) {
+  const int lane = threadIdx.x & 63;
+  float acc[U];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int pos = e * 64 + lane;
-    const uint32_t id = pos < kp ? s_cid[pos] : 0xffffffffu;
-    fin[e] = int64_t(id) >= n ? kSentinel : (uint64_t(ord_f32(s_cd[pos])) << 32) | id;
+  for (int u = 0; u < U; ++u) acc[u] = 0.f;
+  if (vec) {
+    for (int64_t i0 = int64_t(lane) * 4; i0 < d; i0 += 4 * 256) {
+      float4 a4[4], b4[4][U];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t i = i0 + c * 256;
+        a4[c] = i < d ? *reinterpret_cast<const float4*>(qv + i) : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          b4[c][u] = (i < d && int64_t(id[u]) < n) ? *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i)
+                                                   : float4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float t0 = a4[c].x - b4[c][u].x, t1 = a4[c].y - b4[c][u].y;
+          const float t2 = a4[c].z - b4[c][u].z, t3 = a4[c].w - b4[c][u].w;
+          acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+        }
+    }
+  } else {
+    for (int64_t i = lane; i < d; i += 64) {
+      const float a1 = qv[i];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (int64_t(id[u]) >= n) continue;
+        const float t = a1 - rows[int64_t(id[u]) * d + i];
+        acc[u] += t * t;
+      }
+    }
   }
-  wave_sort_e<E>(fin);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc[u] += xor_lanes_f(acc[u], o);
+    out[u] = acc[u];
+  }
+}
+
+constexpr int kExactU = 8;  // rows per wave and pass of the exact distances
+
+// Exact keys ord(d) << 32 | id of the ids s_id[0..cnt) (a wave's own list),
+// into s_key[0..cnt), by the calling wave.
+__device__ __forceinline__ void wave_exact_keys(const uint32_t* s_id, int cnt, uint64_t* s_key, const float* rows,
+                                                int64_t n, int64_t d, const float* qv, bool vec) {
+  const int lane = threadIdx.x & 63;
+  for (int c = 0; c < cnt; c += kExactU) {
+    uint32_t id[kExactU];
+#pragma unroll
+    for (int u = 0; u < kExactU; ++u) id[u] = c + u < cnt ? s_id[c + u] : 0xffffffffu;
+    float dd[kExactU];
+    wave_exact<kExactU>(id, rows, n, d, qv, vec, dd);
+#pragma unroll
+    for (int u = 0; u < kExactU; ++u)
+      if (lane == u && c + u < cnt) s_key[c + u] = (uint64_t(ord_f32(dd[u])) << 32) | id[u];
+  }
+}
+
+// Writes k results from a sorted list of exact keys (wave 0), padded with
+// UINT32_MAX / +inf (src/cagra.cpp:240-251).
+template <int E>
+__device__ __forceinline__ void write_results(const uint64_t (&fin)[E], int64_t q, int64_t k, uint32_t* out_nbr,
+                                              float* out_dist) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int64_t pos = e * 64 + lane;
@@ -758,36 +820,171 @@ __device__ __forceinline__ void rerank_and_write(const uint32_t* s_cid, float* s
   }
 }
 
+// Key at position p (uniform) of a sorted 64*E list held by a wave.
+template <int E>
+__device__ __forceinline__ uint64_t key_at(const uint64_t (&v)[E], int p) {
+  uint64_t r = kSentinel;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (e == p / 64) r = shfl_u64(v[e], p % 64);
+  return r;
+}
+
+// Finishes one query from its R candidates (ids in s_cid, sorted by key,
+// 0xffffffff for none) by the four waves of a workgroup: exact re-rank,
+// certificate, and if needed the escalation described above; writes k
+// sorted results.  t_cert: the bound T above (key units); t_star: the
+// smallest list threshold; part / kp / stride: the candidate lists (entry e
+// of the query's lists at part[(e / kp) * stride + e % kp], G * kp entries).
+template <int E>
+__device__ void finish_query(const uint32_t* s_cid, int R, float t_cert, float t_star, const uint64_t* part, int G,
+                             int kp, int stride, const float* __restrict__ rows, int64_t n, int64_t d,
+                             const float* __restrict__ qv, int64_t q, int64_t k, const Cert& cert,
+                             uint32_t* out_nbr, float* out_dist) {
+  __shared__ uint64_t s_key[64 * E > 256 ? 64 * E : 256];  // exact keys: candidates, then per-wave rounds
+  __shared__ uint32_t s_wid[kWaves][64];
+  __shared__ uint64_t s_scr[32];
+  __shared__ int s_mode;
+  __shared__ float s_tneed;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(qv) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
+
+  // 1. Exact distances of the R candidates, kExactU per wave and pass.
+  for (int c = kExactU * wave; c < R; c += kExactU * kWaves) {
+    uint32_t id[kExactU];
+#pragma unroll
+    for (int u = 0; u < kExactU; ++u) id[u] = c + u < R ? s_cid[c + u] : 0xffffffffu;
+    float dd[kExactU];
+    wave_exact<kExactU>(id, rows, n, d, qv, vec, dd);
+#pragma unroll
+    for (int u = 0; u < kExactU; ++u)
+      if (lane == u && c + u < R)
+        s_key[c + u] = int64_t(id[u]) < n ? (uint64_t(ord_f32(dd[u])) << 32) | id[u] : kSentinel;
+  }
+  __syncthreads();
+
+  // 2. Wave 0: sort, certify.
+  uint64_t fin[E];
+  if (wave == 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) fin[e] = e * 64 + lane < R ? s_key[e * 64 + lane] : kSentinel;
+    wave_sort_e<E>(fin);
+    const uint64_t kth = key_at<E>(fin, int(k - 1));
+    if (lane == 0) {
+      const double dk = kth == kSentinel ? INFINITY : double(unord_f32(uint32_t(kth >> 32)));
+      const double qn = double(cert.qnorms[q]);
+      int mode = kCertPass;
+      float tneed = INFINITY;
+      if (!(qn <= 3.0e38) || !(double(cert.rmax) <= 3.0e38)) {
+        mode = kCertAll;  // keys overflowed or rows are not finite: no bound holds
+      } else {
+        const double qt = std::sqrt(qn) * (1.0 + 0x1p-20);
+        const double qe = std::sqrt(double(cert.qerr[q]) * (1.0 + double(d + 8) * 0x1p-24)) * (1.0 + 0x1p-20);
+        const double E_ = qe + qt * 0x1p-23 + double(cert.qslack) + double(cert.dx);
+        const double A = double(cert.a_coef) * (qt + double(cert.rmax)) * (qt + double(cert.rmax));
+        const double V = double(cert.s2) * dk * (1.0 + double(cert.rho));
+        const double T = double(t_cert);
+        bool ok;
+        if (T > 3.0e38) {
+          ok = true;  // every row with a finite key was re-ranked
+        } else {
+          const double r = T > A ? std::sqrt(T - A) : 0.0;
+          const double lb = r > E_ ? (r - E_) * (r - E_) : 0.0;
+          ok = lb * (1.0 - 0x1p-40) > V;
+        }
+        if (!ok) {
+          const double tn = V > 3.0e38 ? INFINITY : ((std::sqrt(V) + E_) * (std::sqrt(V) + E_) + A) * (1.0 + 0x1p-20);
+          mode = tn <= double(t_star) ? kCertKeys : kCertAll;
+          tneed = float(tn);
+        }
+      }
+      s_mode = mode;
+      s_tneed = tneed;
+      if (mode != kCertPass) {
+        atomicAdd(&cert.counters[0], 1ull);
+        if (mode == kCertAll) atomicAdd(&cert.counters[1], 1ull);
+      }
+    }
+  }
+  __syncthreads();
+  const int mode = s_mode;
+  if (mode == kCertPass) {
+    if (wave == 0) write_results<E>(fin, q, k, out_nbr, out_dist);
+    return;
+  }
+
+  // 3. Escalation: exact keys of every row with a key up to T_need (from the
+  // lists) or of every row, 64 per wave and round, merged by wave 0 into its
+  // running exact top-128 (k <= 112 here).
+  const float tneed = s_tneed;
+  const int64_t total = mode == kCertKeys ? int64_t(G) * kp : n;
+  uint64_t run[2] = {kSentinel, kSentinel};
+  for (int64_t base = 0; base < total; base += 64 * kWaves) {
+    const int64_t pos = base + 64 * wave + lane;
+    uint32_t id = 0xffffffffu;
+    bool ok = false;
+    if (mode == kCertKeys) {
+      const uint64_t key = pos < total ? part[(pos / kp) * stride + pos % kp] : kSentinel;
+      ok = key != kSentinel && unord_f32(uint32_t(key >> 32)) <= tneed;
+      id = uint32_t(key);
+    } else {
+      ok = pos < n;
+      id = uint32_t(pos);
+    }
+    const uint64_t m = __ballot(ok);
+    if (ok) s_wid[wave][mbcnt(m)] = id;
+    const int cnt = popc(m);
+    uint64_t* wk = s_key + 64 * wave;
+    wave_exact_keys(s_wid[wave], cnt, wk, rows, n, d, qv, vec);
+    if (lane >= cnt) wk[lane] = kSentinel;
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll 1
+      for (int w = 0; w < kWaves; ++w) {
+        uint64_t ck = s_key[64 * w + lane];
+        if (sort_below(ck, key_at<2>(run, int(k - 1)), kSentinel, s_scr) > 0) wave_merge<2>(run, ck);
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) write_results<2>(run, q, k, out_nbr, out_dist);
+}
+
 // ---------------------------------------------------------------------------
-// Merge + exact re-rank for kp <= 64, one workgroup (4 waves) per query.
-//  1. The kp-th smallest list minimum bounds the kp-th smallest key (kp list
-//     minima are kp distinct keys): only keys at or below it can be among
-//     the kp smallest.  Wave 0 computes it (a 256-key wave sort) while every
-//     wave's first batch of keys is already in flight.
-//  2. A key within the bound comes from one of the kp lists whose minimum is
-//     within it, so at most kp * kp keys pass.  The four waves stream all
+// Merge for kp <= 64, one workgroup (4 waves) per query.
+//  1. The R-th smallest list minimum (R = min(2 kp, 64)) bounds the R-th
+//     smallest key (R list minima are R distinct keys): only keys at or
+//     below it can be among the R smallest.  Wave 0 computes it (a 256-key
+//     wave sort) and the smallest list threshold T* while every wave's first
+//     batch of keys is already in flight.
+//  2. A key within the bound comes from one of the R lists whose minimum is
+//     within it, so at most R * kp keys pass.  The four waves stream all
 //     G * kp keys and append the passing ones to an LDS buffer of that size
 //     (one atomic per wave and batch).
 //  3. Wave 0 sorts the passing keys 64 at a time and merges them into its
-//     running sorted top-64; its first kp ids are re-ranked exactly.
+//     running sorted top-64; its first R ids are finished (re-ranked,
+//     certified) by finish_query.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __restrict__ part,
-                                                              const uint64_t* __restrict__ lmin, int G, int kp,
+                                                              const uint64_t* __restrict__ lmin,
+                                                              const float* __restrict__ lcut, int G, int kp,
                                                               const float* __restrict__ rows, int64_t n, int64_t d,
                                                               const float* __restrict__ queries, int64_t k,
-                                                              uint32_t* __restrict__ out_nbr,
+                                                              Cert cert, uint32_t* __restrict__ out_nbr,
                                                               float* __restrict__ out_dist) {
   constexpr int kBatch = 16;        // keys per thread and batch
-  constexpr int kMaxPass = 64 * 64; // kp * kp for kp <= 64
+  constexpr int kMaxPass = 64 * 64; // R * kp for R, kp <= 64
   __shared__ uint64_t s_pass[kMaxPass];
   __shared__ uint32_t s_npass;
   __shared__ uint64_t s_bound;
+  __shared__ float s_tcert, s_tstar;
   __shared__ uint32_t s_cid[64];
-  __shared__ float s_cd[64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t q = blockIdx.x;
   const uint64_t* src = part + q * int64_t(G) * kp;
   const int total = G * kp;
+  const int R = 2 * kp < 64 ? 2 * kp : 64;
   if (tid == 0) s_npass = 0;
 
   // First batch of keys, requested before the bound is known.
@@ -797,20 +994,24 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
     const int e = r * kThreads + tid;
     key[r] = e < total ? src[e] : kSentinel;
   }
-  // 1. Bound from the list minima (G <= 256), by wave 0.
+  // 1. Bound from the list minima and the smallest list threshold (G <= 256), by wave 0.
   if (wave == 0) {
     uint64_t mins[4];
+    float cut = INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int x = lane + 64 * i;
       mins[i] = x < G ? lmin[q * G + x] : kSentinel;
+      if (x < G) cut = fminf(cut, lcut[q * G + x]);
     }
-    wave_sort_e<4>(mins);
-    uint64_t bound = kSentinel;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i == (kp - 1) / 64) bound = shfl_u64(mins[i], (kp - 1) % 64);
-    if (lane == 0) s_bound = bound;
+    for (int o = 32; o >= 1; o >>= 1) cut = fminf(cut, xor_lanes_f(cut, o));
+    wave_sort_e<4>(mins);
+    const uint64_t bound = key_at<4>(mins, R - 1);
+    if (lane == 0) {
+      s_bound = bound;
+      s_tstar = cut;
+    }
   }
   __syncthreads();
   const uint64_t bound = s_bound;
@@ -838,24 +1039,27 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
   }
   __syncthreads();
 
-  // 3. Wave 0: top-kp of the passing keys.
+  // 3. Wave 0: top-R of the passing keys.
   if (wave == 0) {
-    const int n = s_npass < uint32_t(kMaxPass) ? int(s_npass) : kMaxPass;
+    const int np = s_npass < uint32_t(kMaxPass) ? int(s_npass) : kMaxPass;
     uint64_t run[1] = {kSentinel};
-    for (int r0 = 0; r0 < n; r0 += 64) {
-      uint64_t ck[1] = {r0 + lane < n ? s_pass[r0 + lane] : kSentinel};
+    for (int r0 = 0; r0 < np; r0 += 64) {
+      uint64_t ck[1] = {r0 + lane < np ? s_pass[r0 + lane] : kSentinel};
       wave_sort_e<1>(ck);
       wave_merge<1>(run, ck[0]);
     }
-    s_cid[lane] = (lane < kp && run[0] != kSentinel) ? uint32_t(run[0]) : 0xffffffffu;
+    s_cid[lane] = (lane < R && run[0] != kSentinel) ? uint32_t(run[0]) : 0xffffffffu;
+    const uint64_t kr = key_at<1>(run, R - 1);
+    const float tr = kr == kSentinel ? INFINITY : unord_f32(uint32_t(kr >> 32));
+    if (lane == 0) s_tcert = fminf(tr, s_tstar);
   }
   __syncthreads();
-  rerank_and_write<1>(s_cid, s_cd, kp, rows, n, d, queries + q * d, q, k, out_nbr, out_dist);
+  finish_query<1>(s_cid, R, s_tcert, s_tstar, src, G, kp, kp, rows, n, d, queries + q * d, q, k, cert, out_nbr,
+                  out_dist);
 }
 
 // ---------------------------------------------------------------------------
-// Merge + exact re-rank for kp = 128 (global lists), one workgroup (4 waves)
-// per query.
+// Merge for kp = 128 (global lists), one workgroup (4 waves) per query.
 //  1. The kp-th smallest list minimum bounds the kp-th smallest key (kp list
 //     minima are kp distinct keys): only keys at or below it can be among
 //     the kp smallest.  Each wave computes it (a 256-key wave sort).
@@ -863,38 +1067,37 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
 //     a batch loaded at once; a row holding a key within the bound is sorted
 //     (wave bitonic) and merged into the wave's running sorted top-64*E,
 //     whose kp-th key then tightens the wave's bound.
-//  3. Wave 0 merges the four running lists; the kp candidates are re-ranked
-//     by the four waves with exact fp32 distances from the fp32 rows.
-//  4. Wave 0 sorts them by (distance, id) and writes k results, padded with
-//     UINT32_MAX / +inf (src/cagra.cpp:240-251).
+//  3. Wave 0 merges the four running lists; the kp candidates are finished
+//     (re-ranked, certified) by finish_query.
 // ---------------------------------------------------------------------------
 template <int E>
 __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restrict__ part,
-                                                       const uint64_t* __restrict__ lmin, int G, int kp,
-                                                       int stride, const float* __restrict__ rows, int64_t n,
-                                                       int64_t d,
-                                                       const float* __restrict__ queries, int64_t k,
+                                                       const uint64_t* __restrict__ lmin,
+                                                       const float* __restrict__ lcut, int G, int kp, int stride,
+                                                       const float* __restrict__ rows, int64_t n, int64_t d,
+                                                       const float* __restrict__ queries, int64_t k, Cert cert,
                                                        uint32_t* __restrict__ out_nbr,
                                                        float* __restrict__ out_dist) {
   constexpr int kBatch = 16;
   __shared__ uint64_t s_run[kWaves][64 * E];
   __shared__ uint32_t s_cid[64 * E];
-  __shared__ float s_cd[64 * E];
+  __shared__ float s_tcert;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t q = blockIdx.x;
 
-  // 1. Bound from the list minima (G <= 256).
+  // 1. Bound from the list minima (G <= 256), and the smallest list threshold.
   uint64_t mins[4];
+  float cut = INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int x = lane + 64 * i;
     mins[i] = x < G ? lmin[q * G + x] : kSentinel;
+    if (x < G) cut = fminf(cut, lcut[q * G + x]);
   }
-  wave_sort_e<4>(mins);
-  uint64_t bound = kSentinel;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (i == (kp - 1) / 64) bound = shfl_u64(mins[i], (kp - 1) % 64);
+  for (int o = 32; o >= 1; o >>= 1) cut = fminf(cut, xor_lanes_f(cut, o));
+  wave_sort_e<4>(mins);
+  uint64_t bound = key_at<4>(mins, kp - 1);
 
   // 2. This wave's quarter of the 64-key rows.
   uint64_t run[E];
@@ -918,20 +1121,15 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
       uint64_t ck[1] = {pass ? key[r] : kSentinel};
       wave_sort_e<1>(ck);
       wave_merge<E>(run, ck[0]);
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        if (e == (kp - 1) / 64) {
-          const uint64_t kth = shfl_u64(run[e], (kp - 1) % 64);
-          bound = kth < bound ? kth : bound;
-        }
-      }
+      const uint64_t kth = key_at<E>(run, kp - 1);
+      bound = kth < bound ? kth : bound;
     }
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) s_run[wave][e * 64 + lane] = run[e];
   __syncthreads();
 
-  // 3. Merge the four running lists; re-rank the kp candidates.
+  // 3. Merge the four running lists; finish the kp candidates.
   if (wave == 0) {
 #pragma unroll
     for (int w = 1; w < kWaves; ++w)
@@ -942,9 +1140,13 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
       const int pos = e * 64 + lane;
       s_cid[pos] = (pos < kp && run[e] != kSentinel) ? uint32_t(run[e]) : 0xffffffffu;
     }
+    const uint64_t kr = key_at<E>(run, kp - 1);
+    const float tr = kr == kSentinel ? INFINITY : unord_f32(uint32_t(kr >> 32));
+    if (lane == 0) s_tcert = fminf(tr, cut);
   }
   __syncthreads();
-  rerank_and_write<E>(s_cid, s_cd, kp, rows, n, d, queries + q * d, q, k, out_nbr, out_dist);
+  finish_query<E>(s_cid, kp, s_tcert, cut, src, G, kp, stride, rows, n, d, queries + q * d, q, k, cert, out_nbr,
+                  out_dist);
 }
 
 // ---------------------------------------------------------------------------
@@ -1010,12 +1212,14 @@ struct BfPlan {
   int G = 0;               // candidate lists per query: dataset ranges of the streaming scan
   int stride = 0;          // keys per (query, range) list in the workspace
   int64_t s_units = 0, s_stride = 0;  // threshold sample
+  int sel_rank = 0;        // the initial threshold is this smallest sample minimum
   int Gs = 0;              // dataset ranges of the sample
   int m_min = 0;           // sample minima per query
   int64_t q_tiles = 0;     // 32-query tiles
   // Workspace: query tiles | query norms | thresholds | sample minima |
   // list minima | candidate lists, each 256-byte aligned.
-  size_t off_qnorm = 0, off_thr = 0, off_smin = 0, off_lmin = 0, off_part = 0, total = 0;
+  size_t off_qnorm = 0, off_qerr = 0, off_thr = 0, off_smin = 0, off_lmin = 0, off_lcut = 0, off_part = 0,
+         total = 0;
 };
 
 BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
@@ -1077,16 +1281,50 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   p.Gs = std::min(ctx->compute_units, 256);
   if (int64_t(p.Gs) > p.s_units) p.Gs = int(p.s_units);
   p.m_min = 2 * p.Gs;
+  // The r-th smallest sample minimum (r >= kp: r minima are r distinct rows)
+  // sits near rank r * n / sampled rows of the query's keys.  The merge
+  // certifies its R candidates against the lists' final thresholds, so the
+  // threshold should sit at rank R or beyond: with a sample that covers a
+  // large share of the rows (small n), r is raised towards R; at n = 1M the
+  // rank is ~kp * 61 already and r stays kp.
+  {
+    const int R = p.kp > 64 ? p.kp : std::min(2 * p.kp, 64);
+    const int64_t sampled = p.s_units * rpu;
+    const int64_t want = (int64_t(R) * sampled + ds->n - 1) / ds->n;
+    p.sel_rank = int(std::max<int64_t>(p.kp, std::min<int64_t>(R, want)));
+  }
 
   p.q_tiles = (q + 31) / 32;
   auto align = [](size_t b) { return (b + 255) / 256 * 256; };
   p.off_qnorm = align(size_t(p.q_tiles) * size_t(p.ks) * kStepBytes);
-  p.off_thr = p.off_qnorm + align(size_t(p.q_tiles) * 32 * sizeof(float));
+  p.off_qerr = p.off_qnorm + align(size_t(p.q_tiles) * 32 * sizeof(float));
+  p.off_thr = p.off_qerr + align(size_t(q) * sizeof(float));
   p.off_smin = p.off_thr + align(size_t(q) * sizeof(float));
   p.off_lmin = p.off_smin + align(size_t(q) * size_t(p.m_min) * sizeof(float));
-  p.off_part = p.off_lmin + align(size_t(q) * size_t(G) * sizeof(uint64_t));
+  p.off_lcut = p.off_lmin + align(size_t(q) * size_t(G) * sizeof(uint64_t));
+  p.off_part = p.off_lcut + align(size_t(q) * size_t(G) * sizeof(float));
   p.total = p.off_part + align(size_t(q) * size_t(G) * size_t(p.stride) * sizeof(uint64_t));
   return p;
+}
+
+// Certificate constants of a search over `ds` (see Cert).
+Cert make_cert(cvs_context* ctx, const cvs_dataset* ds, const float* qnorms, const float* qerr) {
+  Cert c{};
+  const double d = double(ds->d);
+  c.s2 = ds->scale * ds->scale;
+  c.rmax = ds->cert_rmax;
+  c.dx = ds->cert_dx;
+  c.a_coef = float(2.0 * (d + 16.0) * 0x1p-24 * (1.0 + 0x1p-20));
+  c.rho = float(2.0 * (d + 8.0) * 0x1p-24 * (1.0 + 0x1p-20));
+  // fp16 subnormal rounding (2^-25 absolute per element) is inside the
+  // measured error; this covers fl(q - mu) against q - mu, which the
+  // measured error does not see: 2^-24 |s (q - mu)| <= 2^-24 (|q~| + err),
+  // added by the merge as |q~| 2^-23, plus the fp32 sum behind err.
+  c.qslack = float(std::sqrt(d) * 0x1p-25);
+  c.qnorms = qnorms;
+  c.qerr = qerr;
+  c.counters = ctx->bf_counters;
+  return c;
 }
 
 // Enqueues the five launches of one search on the context stream, with the
@@ -1097,9 +1335,11 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
                int64_t k, uint32_t* nbr, float* dist, char* ws, bool timed) {
   u32x4* qtiles = reinterpret_cast<u32x4*>(ws);
   float* qnorms = reinterpret_cast<float*>(ws + p.off_qnorm);
+  float* qerr = reinterpret_cast<float*>(ws + p.off_qerr);
   float* thr0 = reinterpret_cast<float*>(ws + p.off_thr);
   float* sgmin = reinterpret_cast<float*>(ws + p.off_smin);
   uint64_t* lmin = reinterpret_cast<uint64_t*>(ws + p.off_lmin);
+  float* lcut = reinterpret_cast<float*>(ws + p.off_lcut);
   uint64_t* part = reinterpret_cast<uint64_t*>(ws + p.off_part);
   const int G = p.G, kp = p.kp;
 
@@ -1116,6 +1356,7 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
   args.part = part;
   args.sgmin = sgmin;
   args.lmin = lmin;
+  args.lcut = lcut;
   args.s_units = p.s_units;
   args.s_stride = p.s_stride;
   args.n_qblocks = int(p.qblocks);
@@ -1124,7 +1365,7 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
   const TimerSpan t0 = timed ? timer_span(ctx, "bf_prep") : TimerSpan{};
   hipExtLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((p.q_tiles * 32 + kWaves - 1) / kWaves)),
                         dim3(kThreads), 0, ctx->stream, t0.start, t0.stop, 0, queries, q, ds->d, p.ks,
-                        p.q_tiles * 32, qtiles, qnorms);
+                        p.q_tiles * 32, static_cast<const float*>(ds->mu), ds->scale, qtiles, qnorms, qerr);
   after_launch("query_tiles_kernel");
 
   const TimerSpan t1 = timed ? timer_span(ctx, "bf_sample") : TimerSpan{};
@@ -1136,7 +1377,7 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
   launch_scan(ctx, p.ks, p.large_batch ? dim3(unsigned(p.Gs) * p.qblocks, 1) : dim3(unsigned(p.Gs), p.qblocks), args,
               kModeSample, t1.start, nullptr);
   hipExtLaunchKernelGGL(bf_select_kernel, dim3(wave_blocks), dim3(kThreads), 0, ctx->stream, nullptr, t1.stop, 0,
-                        static_cast<const float*>(sgmin), p.m_min, kp, int(q), thr0);
+                        static_cast<const float*>(sgmin), p.m_min, p.sel_rank, int(q), thr0);
   after_launch("bf_select_kernel");
 
   const TimerSpan t2 = timed ? timer_span(ctx, "bf_scan") : TimerSpan{};
@@ -1153,6 +1394,7 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
     ga.thr0 = thr0;
     ga.part = part;
     ga.lmin = lmin;
+    ga.lcut = lcut;
     ga.n_lists = G;
     launch_gemm_scan(ctx, ga, p.gemm_wg, t2.start, t2.stop);
   } else {
@@ -1162,15 +1404,18 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
                 kModeScan, t2.start, t2.stop);
   }
 
+  const Cert cert = make_cert(ctx, ds, qnorms, qerr);
   const TimerSpan t3 = timed ? timer_span(ctx, "bf_merge") : TimerSpan{};
   if (kp <= 64)
     hipExtLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
-                          t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp,
-                          static_cast<const float*>(ds->rows), ds->n, ds->d, queries, k, nbr, dist);
+                          t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin),
+                          static_cast<const float*>(lcut), G, kp, static_cast<const float*>(ds->rows), ds->n, ds->d,
+                          queries, k, cert, nbr, dist);
   else
     hipExtLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start, t3.stop,
-                          0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin), G, kp, p.stride,
-                          static_cast<const float*>(ds->rows), ds->n, ds->d, queries, k, nbr, dist);
+                          0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin),
+                          static_cast<const float*>(lcut), G, kp, p.stride, static_cast<const float*>(ds->rows), ds->n,
+                          ds->d, queries, k, cert, nbr, dist);
   after_launch("bf_merge_kernel");
 }
 

@@ -90,6 +90,10 @@ struct cvs_context {
   cvs::DeviceBuffer ws_search;    // brute force: query tiles, thresholds, candidate lists
   cvs::DeviceBuffer ws_io;        // staging of host queries / results
   cvs::DeviceBuffer ws_teams;     // per-team lists of multi-team graph search
+  // Brute-force escalation counters (device, allocated with the context):
+  // [0] queries whose fp16 selection could not be certified and were
+  // re-ranked exactly over more rows, [1] of them over every row.
+  unsigned long long* bf_counters = nullptr;
 };
 
 struct cvs_dataset {
@@ -99,8 +103,22 @@ struct cvs_dataset {
   int64_t dp = 0;         // padded dimensions (32 * power of two)
   int64_t n_tiles = 0;    // 32-row tiles, padded to a multiple of kTilePad
   float* rows = nullptr;          // n x d fp32, row-major
-  uint16_t* tiles = nullptr;      // n_tiles x (dp/16) x 64 lanes x 8 fp16
-  float* norms = nullptr;         // n_tiles*32 squared norms of fp16 rows (+inf pad)
+  uint16_t* tiles = nullptr;      // n_tiles x (dp/16) x 64 lanes x 8 fp16 of scale * (row - mu)
+  float* norms = nullptr;         // n_tiles*32 squared norms of the fp16 rows (+inf pad)
+  // The fp16 copy is centred and scaled: tiles hold fp16(scale * fl(x - mu))
+  // with mu the fp32 column mean (L2 distances are translation invariant,
+  // and the fp16 rounding error then scales with the rows' spread, not their
+  // offset) and scale a power of two that puts the largest centred value in
+  // [128, 256), so that queries up to 256 times farther out stay finite and
+  // small values stay normal.
+  float* mu = nullptr;            // dp fp32 column means, zero-padded (device)
+  float scale = 1.f;
+  // Bounds for the per-query certificate of the fp16 selection, in scaled
+  // units: every row has |x~| <= cert_rmax and |x~ - scale (x - mu)| <= cert_dx
+  // (measured at creation, rounded up).  Infinite when the rows are not
+  // finite, which sends every query to the exact fallback.
+  float cert_rmax = 0.f;
+  float cert_dx = 0.f;
 };
 
 struct cvs_cagra_index {
@@ -168,9 +186,21 @@ inline int64_t padded_dim(int64_t d) {
   return p;
 }
 
-// Launches the fp32 -> fp16-tile conversion (rows may be n x d with row
-// stride d); writes n_tiles tiles and n_tiles*32 norms.
-void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d,
-                     int64_t dp, int64_t n_tiles, uint16_t* tiles, float* norms);
+// Launches the fp32 -> fp16-tile conversion of scale * (row - mu) (rows n x
+// d with row stride d; mu d floats, or null for zero); writes n_tiles tiles
+// and n_tiles*32 norms.  With `stats` (3 floats, zeroed beforehand, read as
+// non-negative bit patterns) it also raises stats[1] to the largest squared
+// norm and stats[2] to the largest squared rounding error |x~ - s (x - mu)|^2
+// of a row.
+void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp, int64_t n_tiles,
+                     uint16_t* tiles, float* norms, const float* mu = nullptr, float scale = 1.f,
+                     uint32_t* stats = nullptr);
+
+// Centring and scaling of an fp16 copy (the brute-force tiles, the graph
+// build's rows, the graph search's traversal copy): computes mu (dp floats,
+// the fp32 column means of the n x d rows, zero past d) on the device and
+// returns the power-of-two scale that puts the largest |x - mu| in
+// [128, 256) (1 if the rows are all equal or not finite).  Synchronizes.
+float centre_rows(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp, float* mu);
 
 }  // namespace cvs

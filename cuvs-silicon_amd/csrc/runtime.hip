@@ -5,6 +5,7 @@
 // with a single HIP stream, explicit dataset handles instead of a cache keyed
 // by host pointer, and a device-side fp32 -> fp16 conversion in place of the
 // host loop at src/metal_context.mm:161-167.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstring>
@@ -88,20 +89,26 @@ TimerSpan timer_span(cvs_context* ctx, const char* kernel) {
 }
 
 // ---------------------------------------------------------------------------
-// fp32 rows -> fp16 32-row tiles + squared norms of the fp16-rounded rows.
-// One 256-thread workgroup per tile; wave w converts k-steps w, w+4, ...
-// Lane l owns row 32t + l%32 and, in k-step s, the 8 columns
-// 16s + 8*(l/32) + [0,8).  Partial norms are combined across the two lanes of
-// a row with one xor-shuffle and across the waves in a fixed order through
-// LDS, so the result does not depend on scheduling.  Rows >= n and columns
-// >= d are written as zeros; padding rows get norm +inf so that no distance
-// involving them can pass a candidate filter.
+// fp32 rows -> fp16 32-row tiles of scale * (row - mu) + squared norms of the
+// fp16-rounded rows.  One 256-thread workgroup per tile; wave w converts
+// k-steps w, w+4, ...  Lane l owns row 32t + l%32 and, in k-step s, the 8
+// columns 16s + 8*(l/32) + [0,8).  Partial norms are combined across the two
+// lanes of a row with one xor-shuffle and across the waves in a fixed order
+// through LDS, so the result does not depend on scheduling.  Rows >= n and
+// columns >= d are written as zeros; padding rows get norm +inf so that no
+// distance involving them can pass a candidate filter.  With `stats`, the
+// largest squared norm and the largest squared rounding error of a row are
+// folded into stats[1] and stats[2] by atomicMax on their bit patterns
+// (non-negative floats order as their bits; the maximum does not depend on
+// the order of the updates).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void to_tiles_kernel(const float* __restrict__ rows,
                                                        int64_t n, int64_t d, int ksteps,
+                                                       const float* __restrict__ mu, float scale,
                                                        uint4* __restrict__ tiles,
-                                                       float* __restrict__ norms) {
-  __shared__ float s_part[4][32];
+                                                       float* __restrict__ norms,
+                                                       uint32_t* __restrict__ stats) {
+  __shared__ float s_part[2][4][32];
   const int64_t t = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -110,7 +117,7 @@ __global__ __launch_bounds__(256) void to_tiles_kernel(const float* __restrict__
   const bool row_ok = r < n;
   const float* src = rows + (row_ok ? r : 0) * d;
   const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(rows) & 15) == 0;
-  float acc = 0.f;
+  float acc = 0.f, err = 0.f;
 #pragma unroll 4
   for (int s = wave; s < ksteps; s += 4) {
     const int64_t c0 = int64_t(s) * kStepCols + cgrp * 8;
@@ -124,34 +131,152 @@ __global__ __launch_bounds__(256) void to_tiles_kernel(const float* __restrict__
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = (row_ok && c0 + i < d) ? src[c0 + i] : 0.f;
     }
+    if (mu) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (c0 + i < d) ? (v[i] - mu[c0 + i]) * scale : 0.f;
+    }
     _Float16 h[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       h[i] = static_cast<_Float16>(v[i]);
       const float hv = static_cast<float>(h[i]);
       acc += hv * hv;
+      const float e = hv - v[i];
+      err += e * e;
     }
     uint4 packed;
     __builtin_memcpy(&packed, h, sizeof(packed));
     tiles[(t * ksteps + s) * 64 + lane] = packed;
   }
   acc += __shfl_xor(acc, 32);
-  if (cgrp == 0) s_part[wave][lane] = acc;
+  err += __shfl_xor(err, 32);
+  if (cgrp == 0) {
+    s_part[0][wave][lane] = acc;
+    s_part[1][wave][lane] = err;
+  }
   __syncthreads();
   if (threadIdx.x < 32) {
-    const float sum = ((s_part[0][threadIdx.x] + s_part[1][threadIdx.x]) + s_part[2][threadIdx.x]) +
-                      s_part[3][threadIdx.x];
-    norms[t * kTileRows + threadIdx.x] = (t * kTileRows + threadIdx.x < n) ? sum : INFINITY;
+    const int i = threadIdx.x;
+    const float sum = ((s_part[0][0][i] + s_part[0][1][i]) + s_part[0][2][i]) + s_part[0][3][i];
+    const float esum = ((s_part[1][0][i] + s_part[1][1][i]) + s_part[1][2][i]) + s_part[1][3][i];
+    const bool ok = t * kTileRows + i < n;
+    norms[t * kTileRows + i] = ok ? sum : INFINITY;
+    if (stats && ok) {
+      // NaN maps above +inf, so a non-finite row shows up as a non-finite bound.
+      atomicMax(&stats[1], __float_as_uint(sum));
+      atomicMax(&stats[2], __float_as_uint(esum));
+    }
   }
 }
 
-void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp,
-                     int64_t n_tiles, uint16_t* tiles, float* norms) {
+void launch_to_tiles(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp, int64_t n_tiles,
+                     uint16_t* tiles, float* norms, const float* mu, float scale, uint32_t* stats) {
   if (n_tiles <= 0) return;
   hipLaunchKernelGGL(to_tiles_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0,
-                     ctx->stream, rows, n, d, static_cast<int>(dp / kStepCols),
-                     reinterpret_cast<uint4*>(tiles), norms);
+                     ctx->stream, rows, n, d, static_cast<int>(dp / kStepCols), mu, scale,
+                     reinterpret_cast<uint4*>(tiles), norms, stats);
   after_launch("to_tiles_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Column means for the centring of fp16 copies.  column_sum_kernel: block
+// (chunk, column group) sums rows [chunk * rows_per_chunk, ...) of 256
+// consecutive columns in fp64 (each row segment read as one coalesced
+// 1 KiB access); column_mean_kernel adds the chunks in chunk order and
+// divides by n, so the means do not depend on scheduling.  maxabs_kernel
+// folds the largest |fl(x - mu)| into stats[0] by atomicMax on bit patterns.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ rows, int64_t n, int64_t d,
+                                                         int64_t rows_per_chunk, double* __restrict__ partial) {
+  const int64_t c = int64_t(blockIdx.y) * 256 + threadIdx.x;
+  if (c >= d) return;
+  const int64_t r0 = int64_t(blockIdx.x) * rows_per_chunk;
+  const int64_t r1 = r0 + rows_per_chunk < n ? r0 + rows_per_chunk : n;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  int64_t r = r0;
+  for (; r + 4 <= r1; r += 4) {
+    s0 += rows[(r + 0) * d + c];
+    s1 += rows[(r + 1) * d + c];
+    s2 += rows[(r + 2) * d + c];
+    s3 += rows[(r + 3) * d + c];
+  }
+  for (; r < r1; ++r) s0 += rows[r * d + c];
+  partial[int64_t(blockIdx.x) * d + c] = (s0 + s1) + (s2 + s3);
+}
+
+__global__ __launch_bounds__(256) void column_mean_kernel(const double* __restrict__ partial, int chunks,
+                                                          int64_t n, int64_t d, int64_t dp, float* __restrict__ mu) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= dp) return;
+  if (c >= d) {
+    mu[c] = 0.f;
+    return;
+  }
+  double s = 0.0;
+  for (int i = 0; i < chunks; ++i) s += partial[int64_t(i) * d + c];
+  mu[c] = float(s / double(n));
+}
+
+__global__ __launch_bounds__(256) void maxabs_kernel(const float* __restrict__ rows, int64_t n, int64_t d,
+                                                     int64_t rows_per_chunk, const float* __restrict__ mu,
+                                                     uint32_t* __restrict__ stats) {
+  const int64_t c = int64_t(blockIdx.y) * 256 + threadIdx.x;
+  float m = 0.f;
+  if (c < d) {
+    const float mc = mu[c];
+    const int64_t r0 = int64_t(blockIdx.x) * rows_per_chunk;
+    const int64_t r1 = r0 + rows_per_chunk < n ? r0 + rows_per_chunk : n;
+    for (int64_t r = r0; r < r1; ++r) {
+      const float v = fabsf(rows[r * d + c] - mc);
+      m = (v > m || v != v) ? v : m;  // keeps a NaN
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float y = __shfl_xor(m, o);
+    m = (y > m || y != y) ? y : m;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(&stats[0], __float_as_uint(m));
+}
+
+float centre_rows(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int64_t dp, float* mu) {
+  const int64_t rows_per_chunk = std::max<int64_t>(64, (n + 255) / 256);
+  const int chunks = int((n + rows_per_chunk - 1) / rows_per_chunk);
+  double* partial = nullptr;
+  uint32_t* stats = nullptr;
+  CVS_HIP(hipMalloc(&partial, size_t(chunks) * size_t(d) * sizeof(double)));
+  float scale = 1.f;
+  try {
+    CVS_HIP(hipMalloc(&stats, sizeof(uint32_t)));
+    CVS_HIP(hipMemsetAsync(stats, 0, sizeof(uint32_t), ctx->stream));
+    hipLaunchKernelGGL(column_sum_kernel, dim3(unsigned(chunks), unsigned((d + 255) / 256)), dim3(256), 0,
+                       ctx->stream, rows, n, d, rows_per_chunk, partial);
+    after_launch("column_sum_kernel");
+    hipLaunchKernelGGL(column_mean_kernel, dim3(unsigned((dp + 255) / 256)), dim3(256), 0, ctx->stream,
+                       static_cast<const double*>(partial), chunks, n, d, dp, mu);
+    after_launch("column_mean_kernel");
+    hipLaunchKernelGGL(maxabs_kernel, dim3(unsigned(chunks), unsigned((d + 255) / 256)), dim3(256), 0, ctx->stream,
+                       rows, n, d, rows_per_chunk, static_cast<const float*>(mu), stats);
+    after_launch("maxabs_kernel");
+    uint32_t bits = 0;
+    CVS_HIP(hipMemcpyAsync(&bits, stats, sizeof(bits), hipMemcpyDeviceToHost, ctx->stream));
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+    float m;
+    std::memcpy(&m, &bits, sizeof(m));
+    if (std::isfinite(m) && m > 0.f) {
+      // m = f * 2^x with f in [0.5, 1), so m * 2^(8 - x) lies in [128, 256).
+      int x = 0;
+      (void)std::frexp(m, &x);
+      scale = std::ldexp(1.f, std::max(-120, std::min(120, 8 - x)));
+    }
+  } catch (...) {
+    (void)hipFree(partial);
+    if (stats) (void)hipFree(stats);
+    throw;
+  }
+  (void)hipFree(partial);
+  (void)hipFree(stats);
+  return scale;
 }
 
 // ---------------------------------------------------------------------------
@@ -240,7 +365,12 @@ int cvs_context_create(int device, cvs_context** out_ctx) {
     try {
       CVS_HIP(hipSetDevice(device));
       CVS_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+      CVS_HIP(hipMalloc(&ctx->bf_counters, 2 * sizeof(unsigned long long)));
+      CVS_HIP(hipMemsetAsync(ctx->bf_counters, 0, 2 * sizeof(unsigned long long), ctx->stream));
+      CVS_HIP(hipStreamSynchronize(ctx->stream));
     } catch (...) {
+      if (ctx->bf_counters) (void)hipFree(ctx->bf_counters);
+      if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
       delete ctx;
       throw;
     }
@@ -266,6 +396,7 @@ int cvs_context_destroy(cvs_context* ctx) {
     ctx->ws_search.release();
     ctx->ws_io.release();
     ctx->ws_teams.release();
+    if (ctx->bf_counters) (void)hipFree(ctx->bf_counters);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
   });
@@ -320,6 +451,18 @@ int cvs_context_kernel_time(cvs_context* ctx, const char* kernel, double* total_
     }
     *total_ms = sum;
     *launches = cnt;
+  });
+}
+
+int cvs_context_bf_escalations(cvs_context* ctx, uint64_t* escalated, uint64_t* rescanned, int reset) {
+  return guarded([&] {
+    bind(ctx);
+    unsigned long long host[2] = {0, 0};
+    CVS_HIP(hipMemcpyAsync(host, ctx->bf_counters, sizeof(host), hipMemcpyDeviceToHost, ctx->stream));
+    if (reset) CVS_HIP(hipMemsetAsync(ctx->bf_counters, 0, sizeof(host), ctx->stream));
+    CVS_HIP(hipStreamSynchronize(ctx->stream));
+    if (escalated) *escalated = host[0];
+    if (rescanned) *rescanned = host[1];
   });
 }
 
@@ -424,23 +567,47 @@ int cvs_dataset_create(cvs_context* ctx, const float* rows, int64_t n, int64_t d
     ds->dp = padded_dim(d);
     const int64_t tiles = (n + kTileRows - 1) / kTileRows;
     ds->n_tiles = (tiles + kTilePad - 1) / kTilePad * kTilePad;  // no ragged stage loads
+    uint32_t* stats = nullptr;
     try {
       const size_t row_bytes = size_t(n) * size_t(d) * sizeof(float);
       CVS_HIP(hipMalloc(&ds->rows, row_bytes));
       CVS_HIP(hipMalloc(&ds->tiles, size_t(ds->n_tiles) * size_t(ds->dp / kStepCols) * kStepBytes));
       // + kNormSlack: stage copies read whole 64-float windows past the last tile.
       CVS_HIP(hipMalloc(&ds->norms, (size_t(ds->n_tiles) * kTileRows + kNormSlack) * sizeof(float)));
+      CVS_HIP(hipMalloc(&ds->mu, size_t(ds->dp) * sizeof(float)));
+      CVS_HIP(hipMalloc(&stats, 4 * sizeof(uint32_t)));
+      CVS_HIP(hipMemsetAsync(stats, 0, 4 * sizeof(uint32_t), ctx->stream));
       CVS_HIP(hipMemsetAsync(ds->norms, 0, (size_t(ds->n_tiles) * kTileRows + kNormSlack) * sizeof(float),
                              ctx->stream));
       CVS_HIP(hipMemcpyAsync(ds->rows, rows, row_bytes,
                              rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                              ctx->stream));
-      launch_to_tiles(ctx, ds->rows, n, d, ds->dp, ds->n_tiles, ds->tiles, ds->norms);
+      ds->scale = centre_rows(ctx, ds->rows, n, d, ds->dp, ds->mu);
+      launch_to_tiles(ctx, ds->rows, n, d, ds->dp, ds->n_tiles, ds->tiles, ds->norms, ds->mu, ds->scale, stats);
+      uint32_t host[4] = {0, 0, 0, 0};
+      CVS_HIP(hipMemcpyAsync(host, stats, sizeof(host), hipMemcpyDeviceToHost, ctx->stream));
       CVS_HIP(hipStreamSynchronize(ctx->stream));
+      (void)hipFree(stats);
+      stats = nullptr;
+      float nmax, emax;
+      std::memcpy(&nmax, &host[1], sizeof(float));
+      std::memcpy(&emax, &host[2], sizeof(float));
+      // Rounded up: the fp32 sums behind nmax and emax carry a relative error
+      // below (d + 8) 2^-24; fl(x - mu) is within 2^-24 |x - mu| per element
+      // of x - mu; an fp16 subnormal result is within 2^-25 absolute.
+      const double rel = 1.0 + double(d + 8) * 0x1p-24;
+      const double rmax = std::sqrt(double(nmax) * rel) * (1.0 + 0x1p-20);
+      const double dx = std::sqrt(double(emax) * rel) * (1.0 + 0x1p-20) + rmax * 0x1p-23 +
+                        std::sqrt(double(d)) * 0x1p-25;
+      const bool finite = std::isfinite(nmax) && std::isfinite(emax);
+      ds->cert_rmax = finite ? float(rmax * (1.0 + 0x1p-20)) : INFINITY;
+      ds->cert_dx = finite ? float(dx * (1.0 + 0x1p-20)) : INFINITY;
     } catch (...) {
+      if (stats) (void)hipFree(stats);
       if (ds->rows) (void)hipFree(ds->rows);
       if (ds->tiles) (void)hipFree(ds->tiles);
       if (ds->norms) (void)hipFree(ds->norms);
+      if (ds->mu) (void)hipFree(ds->mu);
       delete ds;
       throw;
     }
@@ -457,6 +624,7 @@ int cvs_dataset_destroy(cvs_dataset* ds) {
     (void)hipFree(ds->rows);
     (void)hipFree(ds->tiles);
     (void)hipFree(ds->norms);
+    (void)hipFree(ds->mu);
     --ds->ctx->live_children;
     delete ds;
   });

@@ -96,6 +96,15 @@ int cvs_context_set_timing(cvs_context* ctx, int enable);
 int cvs_context_kernel_time(cvs_context* ctx, const char* kernel,
                             double* total_ms, uint64_t* launches);
 
+/* Brute-force escalations since the context was made (or last reset): the
+ * number of queries whose fp16 candidate selection could not be certified
+ * exact and that were re-ranked exactly over every row with a key up to
+ * the bound (see cvs_bf_search), and how many of those over every row of
+ * the dataset.  Synchronizes; reset = 1 clears them afterwards.  No
+ * counterpart in the reference, whose GPU path does not check its fp16
+ * selection (src/metal_context.mm:203-246). */
+int cvs_context_bf_escalations(cvs_context* ctx, uint64_t* escalated, uint64_t* rescanned, int reset);
+
 /* Device calibration; no counterpart in the reference (its roofline figures
  * are nominal).  Streams `bytes` of device memory, rounded down to whole
  * 32 KiB steps per workgroup, with `workgroups` workgroups of 256 threads,
@@ -132,10 +141,16 @@ int cvs_dataset_rows(const cvs_dataset* ds, const float** out_rows);
 
 /* Exact squared-L2 k-NN of q queries against the dataset.  Replaces
  * MetalContext::search_brute_force (metal_context.hpp:35-40;
- * src/metal_context.mm:139-255: MPS fp16 GEMM + l2_topk_from_cross).
- * Fused: fp16 MFMA cross terms over LDS-staged tiles with a per-query
- * candidate filter, then an exact fp32 re-rank.  Requires 1 <= k,
- * k <= CVS_BF_MAX_K, d <= CVS_BF_MAX_DIM.  Host pointers, blocking. */
+ * src/metal_context.mm:139-255: MPS fp16 GEMM + l2_topk_from_cross) and
+ * returns what the reference's CPU loop returns (src/cagra.cpp:211-252).
+ * Fused: fp16 MFMA cross terms of the centred, scaled rows and queries over
+ * LDS-staged tiles select candidates, which are re-ranked in fp32.  Each
+ * query is certified: with a bound on the fp16 arithmetic's error, no row
+ * outside the re-ranked candidates can be nearer than the k-th result; a
+ * query that fails is re-ranked exactly over every row that could be (in
+ * the worst case every row), so results are exact on any finite input.
+ * Requires 1 <= k, k <= CVS_BF_MAX_K, d <= CVS_BF_MAX_DIM.  Host pointers,
+ * blocking. */
 int cvs_bf_search(cvs_context* ctx, const cvs_dataset* ds,
                   const float* queries, int64_t q, int64_t k,
                   uint32_t* out_neighbors, float* out_distances);
