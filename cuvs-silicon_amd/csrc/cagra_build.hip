@@ -6,8 +6,9 @@
 // (:334-395) that recomputes full 2-hop distance sets per node.  Here every
 // phase runs on the GPU and no update is lost to a race:
 //
-//  1. convert   fp32 rows -> fp16 rows (row stride dp = d rounded up to 128)
-//               + fp32 squared norms of the fp16-rounded rows.
+//  1. convert   fp32 rows -> fp16 rows of scale * (row - mean) (row stride dp
+//               = d rounded up to 128) + fp32 squared norms of the
+//               fp16-rounded rows.
 //  2. bucket    rows are split into buckets of 256 consecutive entries of a
 //               random permutation (the reference's LCG Fisher-Yates,
 //               src/metal_context.mm:802-810).  One workgroup per bucket forms
@@ -42,7 +43,8 @@
 //
 // Lists are sorted 64-bit keys ord(distance) << 32 | id << 1 | new, so the
 // order is (distance, id) and the new flag never reorders a list.  Distances
-// in the build are fp16-input expanded-form estimates; they only rank
+// in the build are fp16-input expanded-form estimates of the centred, scaled
+// rows (scale^2 times the squared distance, up to rounding); they only rank
 // candidates (the search computes exact fp32 distances).
 #include <algorithm>
 #include <chrono>
@@ -267,11 +269,14 @@ __device__ __forceinline__ void gram_join(const char* __restrict__ x16, int64_t 
     if (c + k < n_chunks) step(reg[k], c + k);
 }
 
-// fp32 rows -> fp16 rows (stride dp) + squared norms of the fp16-rounded rows.
-// One wave per row.
+// fp32 rows -> fp16 rows of scale * (row - mu) (stride dp) + squared norms of
+// the fp16-rounded rows.  Centring (mu: the column means) keeps the fp16
+// rounding proportional to the rows' spread instead of their offset from the
+// origin; every distance the build compares is between rows, so the shift
+// and the power-of-two scale change no ranking.  One wave per row.
 __global__ __launch_bounds__(256) void to_half_rows_kernel(const float* __restrict__ rows, int64_t n, int64_t d,
-                                                           int64_t dp, _Float16* __restrict__ out,
-                                                           float* __restrict__ norms) {
+                                                           int64_t dp, const float* __restrict__ mu, float scale,
+                                                           _Float16* __restrict__ out, float* __restrict__ norms) {
   const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= n) return;
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(256) void to_half_rows_kernel(const float* __restri
   _Float16* dst = out + r * dp;
   float acc = 0.f;
   for (int64_t c = lane; c < dp; c += 64) {
-    const _Float16 h = static_cast<_Float16>(c < d ? src[c] : 0.f);
+    const _Float16 h = static_cast<_Float16>(c < d ? (src[c] - mu[c]) * scale : 0.f);
     dst[c] = h;
     const float hv = static_cast<float>(h);
     acc += hv * hv;
@@ -1212,8 +1217,10 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
     CVS_HIP(hipMemcpyAsync(tmp, rows, size_t(n) * d * sizeof(float), hipMemcpyHostToDevice, st));
     rows32 = tmp;
   }
-  hipLaunchKernelGGL(to_half_rows_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, rows32, n, d, dp, x16,
-                     norms);
+  float* mu = mem.alloc<float>(size_t(dp));
+  const float scale = centre_rows(ctx, rows32, n, d, dp, mu);
+  hipLaunchKernelGGL(to_half_rows_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, rows32, n, d, dp,
+                     static_cast<const float*>(mu), scale, x16, norms);
   after_launch("to_half_rows_kernel");
   // Random permutations: the reference's LCG Fisher-Yates
   // (src/metal_context.mm:802-810); later rounds continue the sequence.

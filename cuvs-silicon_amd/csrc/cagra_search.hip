@@ -60,7 +60,9 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
 struct SearchArgs {
   const float4* rows;     // n rows of dq float4, zero-padded
-  const uint4* rows16;    // n rows of dq8 x 8 fp16 (traversal copy), zero-padded
+  const uint4* rows16;    // n rows of dq8 x 8 fp16 of scale * (row - mu) (traversal copy), zero-padded
+  const float* mu;        // dpad column means subtracted in the traversal copy (zero-padded)
+  float scale;            // power of two applied after centring
   const uint32_t* graph;  // n x g
   const uint32_t* seeds;  // n_seeds seed ids, or null
   const float* queries;   // q x d fp32
@@ -174,12 +176,14 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
       qv[j] = t;
     }
   } else {
+    // Centred and scaled as the traversal copy is (distances in the
+    // traversal are scale^2 times the squared distance).
 #pragma unroll
     for (int j = 0; j < kMaxDv8; ++j)
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int64_t c = int64_t(tp + 16 * j) * 8 + t;
-        qh[j][t] = (j < a.dv8 && c < a.d) ? qsrc[c] : 0.f;
+        qh[j][t] = (j < a.dv8 && c < a.d) ? (qsrc[c] - a.mu[c]) * a.scale : 0.f;
       }
   }
 
@@ -221,6 +225,8 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
         }
       }
     } else {
+      // Exact: the fp32 rows against the query as given (read again; this
+      // runs once per list entry at the end of the search).
       const float4* row = a.rows + int64_t(rid) * a.dq + 2 * tp;
       float4 x[2 * kMaxDv8];
 #pragma unroll
@@ -233,9 +239,15 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
 #pragma unroll
       for (int j = 0; j < kMaxDv8; ++j) {
         if (j < a.dv8) {
+          float qr[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int64_t c = int64_t(tp + 16 * j) * 8 + t;
+            qr[t] = c < a.d ? qsrc[c] : 0.f;
+          }
           const float4 lo = x[2 * j], hi = x[2 * j + 1];
-          const float d0 = qh[j][0] - lo.x, d1 = qh[j][1] - lo.y, d2 = qh[j][2] - lo.z, d3 = qh[j][3] - lo.w;
-          const float d4 = qh[j][4] - hi.x, d5 = qh[j][5] - hi.y, d6 = qh[j][6] - hi.z, d7 = qh[j][7] - hi.w;
+          const float d0 = qr[0] - lo.x, d1 = qr[1] - lo.y, d2 = qr[2] - lo.z, d3 = qr[3] - lo.w;
+          const float d4 = qr[4] - hi.x, d5 = qr[5] - hi.y, d6 = qr[6] - hi.z, d7 = qr[7] - hi.w;
           acc += ((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3)) + ((d4 * d4 + d5 * d5) + (d6 * d6 + d7 * d7));
         }
       }
@@ -523,21 +535,26 @@ __global__ __launch_bounds__(64) void team_merge_kernel(const uint64_t* __restri
   }
 }
 
-// fp32 rows -> the fp16 traversal copy (round to nearest even), 8 values per
-// thread.
-__global__ void rows_to_half_kernel(const float4* __restrict__ src, size_t pieces, uint4* __restrict__ dst) {
+// fp32 rows (n x dpad) -> the fp16 traversal copy of scale * (row - mu)
+// (round to nearest even), 8 values per thread.  Centring keeps the fp16
+// rounding proportional to the rows' spread, not their offset from the
+// origin; the query is centred and scaled the same way in the search.
+__global__ void rows_to_half_kernel(const float4* __restrict__ src, size_t pieces, int dpad8,
+                                    const float4* __restrict__ mu, float scale, uint4* __restrict__ dst) {
   const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= pieces) return;
+  const size_t c = (i % size_t(dpad8)) * 2;  // float4 column of the piece
   const float4 lo = src[2 * i], hi = src[2 * i + 1];
+  const float4 ml = mu[c], mh = mu[c + 1];
   half8_t h;
-  h[0] = _Float16(lo.x);
-  h[1] = _Float16(lo.y);
-  h[2] = _Float16(lo.z);
-  h[3] = _Float16(lo.w);
-  h[4] = _Float16(hi.x);
-  h[5] = _Float16(hi.y);
-  h[6] = _Float16(hi.z);
-  h[7] = _Float16(hi.w);
+  h[0] = _Float16((lo.x - ml.x) * scale);
+  h[1] = _Float16((lo.y - ml.y) * scale);
+  h[2] = _Float16((lo.z - ml.z) * scale);
+  h[3] = _Float16((lo.w - ml.w) * scale);
+  h[4] = _Float16((hi.x - mh.x) * scale);
+  h[5] = _Float16((hi.y - mh.y) * scale);
+  h[6] = _Float16((hi.z - mh.z) * scale);
+  h[7] = _Float16((hi.w - mh.w) * scale);
   dst[i] = __builtin_bit_cast(uint4, h);
 }
 
@@ -639,6 +656,8 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.n = uint32_t(idx->n);
   a.g = int(idx->degree);
   a.rows16 = reinterpret_cast<const uint4*>(idx->rows16);
+  a.mu = idx->mu;
+  a.scale = idx->scale;
   a.dq = int(idx->dpad / 4);
   a.dv = int(idx->dpad / 64);
   a.dq8 = int(idx->dpad / 8);
@@ -745,8 +764,11 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
       if (ix->dpad != d) CVS_HIP(hipMemsetAsync(ix->rows, 0, row_bytes, ctx->stream));
       upload_rows(ctx, ix->rows, ix->dpad, rows, n, d, rows_on_device);
       CVS_HIP(hipMalloc(&ix->rows16, size_t(n) * size_t(ix->dpad) * 2));
+      CVS_HIP(hipMalloc(&ix->mu, size_t(ix->dpad) * sizeof(float)));
+      ix->scale = centre_rows(ctx, ix->rows, n, ix->dpad, ix->dpad, ix->mu);
       hipLaunchKernelGGL(rows_to_half_kernel, dim3(unsigned((size_t(n) * size_t(ix->dpad) / 8 + 255) / 256)), dim3(256),
                          0, ctx->stream, reinterpret_cast<const float4*>(ix->rows), size_t(n) * size_t(ix->dpad) / 8,
+                         int(ix->dpad / 8), reinterpret_cast<const float4*>(ix->mu), ix->scale,
                          reinterpret_cast<uint4*>(ix->rows16));
       after_launch("rows_to_half_kernel");
       CVS_HIP(hipMemcpyAsync(ix->graph, graph, size_t(n) * degree * sizeof(uint32_t),
@@ -758,6 +780,7 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
     } catch (...) {
       if (ix->rows) (void)hipFree(ix->rows);
       if (ix->rows16) (void)hipFree(ix->rows16);
+      if (ix->mu) (void)hipFree(ix->mu);
       if (ix->graph) (void)hipFree(ix->graph);
       if (ix->seeds) (void)hipFree(ix->seeds);
       delete ix;
@@ -775,6 +798,7 @@ int cvs_cagra_index_destroy(cvs_cagra_index* index) {
     (void)hipStreamSynchronize(index->ctx->stream);
     (void)hipFree(index->rows);
     (void)hipFree(index->rows16);
+    (void)hipFree(index->mu);
     (void)hipFree(index->graph);
     if (index->seeds) (void)hipFree(index->seeds);
     --index->ctx->live_children;

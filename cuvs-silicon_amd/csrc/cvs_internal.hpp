@@ -130,7 +130,9 @@ struct cvs_cagra_index {
   uint32_t n_seeds = 0;
   int traversal_bits = 16;   // 16: traverse rows16, re-rank the list from rows; 32: rows only
   float* rows = nullptr;     // n x dpad fp32, zero-padded
-  void* rows16 = nullptr;    // n x dpad fp16 copy of rows, zero-padded
+  void* rows16 = nullptr;    // n x dpad fp16 copy of scale * (rows - mu), zero-padded
+  float* mu = nullptr;       // dpad column means (zero-padded)
+  float scale = 1.f;         // power of two of the fp16 copy (see cvs_dataset)
   uint32_t* graph = nullptr; // n x degree
   uint32_t* seeds = nullptr; // n_seeds ids
 };

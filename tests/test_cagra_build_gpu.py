@@ -74,6 +74,27 @@ def test_neighbour_quality_and_convergence(ctx, oracle):
     assert share > 0.9
 
 
+@pytest.mark.parametrize("offset_norm", [0.0, 300.0])
+def test_neighbour_quality_on_offset_data(ctx, oracle, offset_norm):
+    """Unit-norm clustered rows shifted by a common offset: the build's fp16
+    copy is centred, so the share of exact neighbours in the lists is the
+    same as without the offset (uncentred fp16 rows at offset 300 carry a
+    rounding error of ~0.15 per coordinate, far above the neighbour gaps)."""
+    rng = np.random.default_rng(77)
+    n, d = 6000, 256
+    c = rng.standard_normal((32, d)).astype(np.float32)
+    x = c[rng.integers(0, 32, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
+    base = x / np.linalg.norm(x, axis=1, keepdims=True)
+    off = rng.standard_normal(d)
+    base = (base + off * (offset_norm / np.linalg.norm(off))).astype(np.float32)
+    graph, _ = ctx.cagra_build(base, intermediate_degree=64, graph_degree=32, max_iterations=30)
+    check_graph(graph, n, 32)
+    exact = oracle.knn_graph(base, 10, threads=16)
+    share = np.mean([len(set(exact[i].tolist()) & set(graph[i].tolist())) / 10 for i in range(n)])
+    print(f"offset {offset_norm}: share of exact 10-NN in the built lists: {share:.4f}")
+    assert share > 0.9
+
+
 @pytest.mark.parametrize("iters", [0, 1, 2, 3])
 def test_iteration_limits(ctx, oracle, iters):
     """The join's locality order is made after the first nn-descent

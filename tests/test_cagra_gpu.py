@@ -116,6 +116,36 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width, bits):
     assert recall(nbr, gt, k) > 0.8
 
 
+@pytest.mark.parametrize("offset_norm", [100.0, 300.0])
+def test_fp16_traversal_on_offset_data(ctx, oracle, offset_norm):
+    """Rows and queries shifted by a common offset: the fp16 traversal copy
+    is centred, so fp16 traversal keeps fp32 traversal's recall, and both at
+    least the restated reference search's on the same graph."""
+    rng = np.random.default_rng(int(offset_norm))
+    n, d, g, itopk = 4000, 256, 32, 64
+    centers = rng.standard_normal((16, d)).astype(np.float32)
+    x = centers[rng.integers(0, 16, n)] + 0.4 * rng.standard_normal((n, d)).astype(np.float32)
+    y = centers[rng.integers(0, 16, 150)] + 0.4 * rng.standard_normal((150, d)).astype(np.float32)
+    off = rng.standard_normal(d)
+    off = (off * (offset_norm / np.linalg.norm(off))).astype(np.float32)
+    base = (x / np.linalg.norm(x, axis=1, keepdims=True) + off).astype(np.float32)
+    qs = (y / np.linalg.norm(y, axis=1, keepdims=True) + off).astype(np.float32)
+    graph = oracle.knn_graph(base, g, threads=16)
+    nav = oracle.cagra_nav_nodes(n)
+    k = 10
+    gt, _ = oracle.bf_exact(base, qs, k, threads=16)
+    ref_nbr, _ = oracle.cagra_reference_search(base, graph, nav, qs, k, itopk_size=itopk, threads=16)
+    out = {}
+    for bits in (32, 16):
+        idx = ctx.cagra_index(base, graph, nav, traversal_bits=bits)
+        nbr, dist = idx.search(qs, k, itopk_size=itopk)
+        idx.close()
+        check_invariants(base, qs, nbr, dist, rtol=1e-4)
+        assert_recall_not_below(nbr, ref_nbr, gt, k, f"offset {offset_norm} {bits}-bit")
+        out[bits] = recall(nbr, gt, k)
+    assert out[16] >= out[32] - 0.02, out
+
+
 @pytest.mark.parametrize("bits", [32, 16])
 def test_itopk_512_on_complete_graph_is_exact(ctx, oracle, bits):
     """itopk 512 (8 list slots per lane) and k up to 512: on a complete graph
