@@ -30,8 +30,8 @@ CVS_ERR_NO_DEVICE = 3
 CVS_ERR_OUT_OF_MEMORY = 4
 CVS_ERR_UNSUPPORTED = 5
 
-BF_MAX_DIM = 1024
-BF_MAX_K = 112
+BF_MAX_DIM = 16384
+BF_MAX_K = 1024
 CAGRA_MAX_DIM = 1024
 CAGRA_MAX_ITOPK = 512
 CAGRA_MAX_WIDTH = 16

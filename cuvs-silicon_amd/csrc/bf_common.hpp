@@ -117,6 +117,132 @@ __device__ __forceinline__ uint32_t compact_query(uint64_t* list, int half, uint
   return cnt > uint32_t(kp) ? kth_hi : 0xffffffffu;
 }
 
+// ---------------------------------------------------------------------------
+// Certificate of the fp16 selection.  A row's key is d~ = |q~|^2 + |x~|^2 -
+// 2 q~.x~ in fp32, with q~, x~ the fp16 copies of s (q - mu), s (x - mu).  For
+// the scaled exact distance D = s^2 |q - x|^2:
+//   |d~ - |q~ - x~|^2| <= A = 2 (d + 16) 2^-24 (|q~| + rmax)^2
+// (fp32 sums of d terms, including an MFMA accumulation that rounds twice
+// per step, and the two final operations), and
+//   | |q~ - x~| - sqrt(D) | <= E = |q~ - s(q - mu)| + dx
+// (triangle inequality; dx bounds every row's rounding, measured when the
+// dataset was made).  Hence D >= lb(d~) = (sqrt(d~ - A) - E)^2 when
+// sqrt(d~ - A) > E, and 0 otherwise: a row whose key is at least T has an
+// exact distance of at least lb(T) / s^2.
+//
+// The merge re-ranks the R smallest keys it holds exactly in fp32.  Every row
+// not re-ranked has a key at or above T = min(key of the R-th candidate, the
+// smallest final list threshold T*) (a list keeps every key of its range
+// below its threshold).  If lb(T) exceeds s^2 d_k (1 + rho), with d_k the
+// k-th exact distance and rho the relative error of the fp32 distances
+// themselves, the result is the exact top k.  Otherwise the query
+// escalates: every row with a key up to T_need = (sqrt(s^2 d_k (1 + rho)) +
+// E)^2 + A (all of them are in the lists when T_need <= T*), or else every
+// row of the dataset, is re-ranked exactly, and the top k of those is the
+// answer.
+// ---------------------------------------------------------------------------
+struct Cert {
+  float s2;              // scale^2: key units per squared distance unit
+  float rmax;            // every row: |x~| <= rmax (scaled units)
+  float dx;              // every row: |x~ - s (x - mu)| <= dx
+  float a_coef;          // 2 (d + 16) 2^-24
+  float rho;             // 2 (d + 8) 2^-24
+  float qslack;          // sqrt(d) 2^-25 + fp32 error of a query's centring
+  const float* qnorms;   // |q~|^2 per query
+  const float* qerr;     // |q~ - s fl(q - mu)|^2 per query
+  unsigned long long* counters;  // [0] escalated queries, [1] of them re-ranked over every row
+};
+
+enum { kCertPass = 0, kCertKeys = 1, kCertAll = 2 };
+
+// Exact squared L2 distances of U rows to the query by the 64 lanes of the
+// calling wave (ids >= n count as none and give 0).  The summation order is
+// fixed: per lane, float4 partial sums over its 4-column pieces of 256-column
+// chunks, then a butterfly, so a row always gets the same value.  All row
+// loads of a 1024-column pass are issued before the first is used.
+template <int U>
+__device__ __forceinline__ void wave_exact(const uint32_t (&id)[U], const float* __restrict__ rows, int64_t n,
+                                           int64_t d, const float* __restrict__ qv, bool vec, float (&out)[U]) {
+  const int lane = threadIdx.x & 63;
+  float acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = 0.f;
+  if (vec) {
+    for (int64_t i0 = int64_t(lane) * 4; i0 < d; i0 += 4 * 256) {
+      float4 a4[4], b4[4][U];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t i = i0 + c * 256;
+        a4[c] = i < d ? *reinterpret_cast<const float4*>(qv + i) : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          b4[c][u] = (i < d && int64_t(id[u]) < n) ? *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i)
+                                                   : float4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float t0 = a4[c].x - b4[c][u].x, t1 = a4[c].y - b4[c][u].y;
+          const float t2 = a4[c].z - b4[c][u].z, t3 = a4[c].w - b4[c][u].w;
+          acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
+        }
+    }
+  } else {
+    for (int64_t i = lane; i < d; i += 64) {
+      const float a1 = qv[i];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (int64_t(id[u]) >= n) continue;
+        const float t = a1 - rows[int64_t(id[u]) * d + i];
+        acc[u] += t * t;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc[u] += xor_lanes_f(acc[u], o);
+    out[u] = acc[u];
+  }
+}
+
+constexpr int kExactU = 8;  // rows per wave and pass of the exact distances
+
+// Exact keys ord(d) << 32 | id of the ids s_id[0..cnt) (a wave's own list),
+// into s_key[0..cnt), by the calling wave.
+__device__ __forceinline__ void wave_exact_keys(const uint32_t* s_id, int cnt, uint64_t* s_key, const float* rows,
+                                                int64_t n, int64_t d, const float* qv, bool vec) {
+  const int lane = threadIdx.x & 63;
+  for (int c = 0; c < cnt; c += kExactU) {
+    uint32_t id[kExactU];
+#pragma unroll
+    for (int u = 0; u < kExactU; ++u) id[u] = c + u < cnt ? s_id[c + u] : 0xffffffffu;
+    float dd[kExactU];
+    wave_exact<kExactU>(id, rows, n, d, qv, vec, dd);
+#pragma unroll
+    for (int u = 0; u < kExactU; ++u)
+      if (lane == u && c + u < cnt) s_key[c + u] = (uint64_t(ord_f32(dd[u])) << 32) | id[u];
+  }
+}
+
+// Certificate constants of a search over `ds` (defined in bf_search.hip).
+Cert make_cert(cvs_context* ctx, const cvs_dataset* ds, const float* qnorms, const float* qerr);
+
+// Converts q queries (device, q x d fp32) into q_rows / 32 query tiles of
+// the dataset's layout and centring, their norms (q_rows, +inf past q) and
+// squared rounding errors (q), on the context stream (bf_search.hip).
+void launch_query_tiles(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t q_rows,
+                        u32x4* qtiles, float* qnorms, float* qerr, hipEvent_t e0, hipEvent_t e1);
+
+// Exact k-NN outside the fused scan's limits (d > 1024 or k > 112): fp16
+// MFMA keys of a query chunk against every row, a radix select and the
+// certified exact re-rank (bf_wide.hip).  Device pointers, context stream.
+void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
+                    uint32_t* nbr, float* dist);
+constexpr int64_t kFusedMaxDim = 1024;  // the fused scan holds a query tile's operands for d <= 1024
+constexpr int64_t kFusedMaxK = 112;     // and keeps up to 128 candidates per query
+
 // Arguments of the register-blocked large-batch scan (bf_gemm.hip).  The
 // candidate lists and their minima have the streaming scan's global-list
 // layout: part[q][list][Lists<128, kModeScan>::CAP], first kp valid.

@@ -695,115 +695,6 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
   if (lane == 0) thr0[q] = pre == 0xffffffffu ? INFINITY : unord_f32(pre);
 }
 
-// ---------------------------------------------------------------------------
-// Certificate of the fp16 selection.  A row's key is d~ = |q~|^2 + |x~|^2 -
-// 2 q~.x~ in fp32, with q~, x~ the fp16 copies of s (q - mu), s (x - mu).  For
-// the scaled exact distance D = s^2 |q - x|^2:
-//   |d~ - |q~ - x~|^2| <= A = 2 (d + 16) 2^-24 (|q~| + rmax)^2
-// (fp32 sums of d terms, including an MFMA accumulation that rounds twice
-// per step, and the two final operations), and
-//   | |q~ - x~| - sqrt(D) | <= E = |q~ - s(q - mu)| + dx
-// (triangle inequality; dx bounds every row's rounding, measured when the
-// dataset was made).  Hence D >= lb(d~) = (sqrt(d~ - A) - E)^2 when
-// sqrt(d~ - A) > E, and 0 otherwise: a row whose key is at least T has an
-// exact distance of at least lb(T) / s^2.
-//
-// The merge re-ranks the R smallest keys it holds exactly in fp32.  Every row
-// not re-ranked has a key at or above T = min(key of the R-th candidate, the
-// smallest final list threshold T*) (a list keeps every key of its range
-// below its threshold).  If lb(T) exceeds s^2 d_k (1 + rho), with d_k the
-// k-th exact distance and rho the relative error of the fp32 distances
-// themselves, the result is the exact top k.  Otherwise the query
-// escalates: every row with a key up to T_need = (sqrt(s^2 d_k (1 + rho)) +
-// E)^2 + A (all of them are in the lists when T_need <= T*), or else every
-// row of the dataset, is re-ranked exactly, and the top k of those is the
-// answer.
-// ---------------------------------------------------------------------------
-struct Cert {
-  float s2;              // scale^2: key units per squared distance unit
-  float rmax;            // every row: |x~| <= rmax (scaled units)
-  float dx;              // every row: |x~ - s (x - mu)| <= dx
-  float a_coef;          // 2 (d + 16) 2^-24
-  float rho;             // 2 (d + 8) 2^-24
-  float qslack;          // sqrt(d) 2^-25 + fp32 error of a query's centring
-  const float* qnorms;   // |q~|^2 per query
-  const float* qerr;     // |q~ - s fl(q - mu)|^2 per query
-  unsigned long long* counters;  // [0] escalated queries, [1] of them re-ranked over every row
-};
-
-enum { kCertPass = 0, kCertKeys = 1, kCertAll = 2 };
-
-// Exact squared L2 distances of U rows to the query by the 64 lanes of the
-// calling wave (ids >= n count as none and give 0).  The summation order is
-// fixed: per lane, float4 partial sums over its 4-column pieces of 256-column
-// chunks, then a butterfly, so a row always gets the same value.  All row
-// loads of a 1024-column pass are issued before the first is used.
-template <int U>
-__device__ __forceinline__ void wave_exact(const uint32_t (&id)[U], const float* __restrict__ rows, int64_t n,
-                                           int64_t d, const float* __restrict__ qv, bool vec, float (&out)[U]) {
-  const int lane = threadIdx.x & 63;
-  float acc[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) acc[u] = 0.f;
-  if (vec) {
-    for (int64_t i0 = int64_t(lane) * 4; i0 < d; i0 += 4 * 256) {
-      float4 a4[4], b4[4][U];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int64_t i = i0 + c * 256;
-        a4[c] = i < d ? *reinterpret_cast<const float4*>(qv + i) : float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          b4[c][u] = (i < d && int64_t(id[u]) < n) ? *reinterpret_cast<const float4*>(rows + int64_t(id[u]) * d + i)
-                                                   : float4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const float t0 = a4[c].x - b4[c][u].x, t1 = a4[c].y - b4[c][u].y;
-          const float t2 = a4[c].z - b4[c][u].z, t3 = a4[c].w - b4[c][u].w;
-          acc[u] += (t0 * t0 + t1 * t1) + (t2 * t2 + t3 * t3);
-        }
-    }
-  } else {
-    for (int64_t i = lane; i < d; i += 64) {
-      const float a1 = qv[i];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (int64_t(id[u]) >= n) continue;
-        const float t = a1 - rows[int64_t(id[u]) * d + i];
-        acc[u] += t * t;
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc[u] += xor_lanes_f(acc[u], o);
-    out[u] = acc[u];
-  }
-}
-
-constexpr int kExactU = 8;  // rows per wave and pass of the exact distances
-
-// Exact keys ord(d) << 32 | id of the ids s_id[0..cnt) (a wave's own list),
-// into s_key[0..cnt), by the calling wave.
-__device__ __forceinline__ void wave_exact_keys(const uint32_t* s_id, int cnt, uint64_t* s_key, const float* rows,
-                                                int64_t n, int64_t d, const float* qv, bool vec) {
-  const int lane = threadIdx.x & 63;
-  for (int c = 0; c < cnt; c += kExactU) {
-    uint32_t id[kExactU];
-#pragma unroll
-    for (int u = 0; u < kExactU; ++u) id[u] = c + u < cnt ? s_id[c + u] : 0xffffffffu;
-    float dd[kExactU];
-    wave_exact<kExactU>(id, rows, n, d, qv, vec, dd);
-#pragma unroll
-    for (int u = 0; u < kExactU; ++u)
-      if (lane == u && c + u < cnt) s_key[c + u] = (uint64_t(ord_f32(dd[u])) << 32) | id[u];
-  }
-}
-
 // Writes k results from a sorted list of exact keys (wave 0), padded with
 // UINT32_MAX / +inf (src/cagra.cpp:240-251).
 template <int E>
@@ -1222,16 +1113,24 @@ struct BfPlan {
          total = 0;
 };
 
-BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
-               const uint32_t* nbr, const float* dist) {
+void validate_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
+                 const uint32_t* nbr, const float* dist) {
   if (!ds || ds->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "dataset does not belong to context");
   if (!queries || !nbr || !dist) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
   if (q <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count must be positive");
   if (k <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "k must be positive");
-  if (k > CVS_BF_MAX_K) fail(CVS_ERR_UNSUPPORTED, "k exceeds CVS_BF_MAX_K for the fused kernel");
-  if (ds->d > CVS_BF_MAX_DIM)
-    fail(CVS_ERR_UNSUPPORTED, "dimension exceeds CVS_BF_MAX_DIM for the fused kernel");
+  if (k > CVS_BF_MAX_K) fail(CVS_ERR_UNSUPPORTED, "k exceeds CVS_BF_MAX_K");
+  if (ds->d > CVS_BF_MAX_DIM) fail(CVS_ERR_UNSUPPORTED, "dimension exceeds CVS_BF_MAX_DIM");
   if (q > (int64_t(1) << 24)) fail(CVS_ERR_UNSUPPORTED, "too many queries in one call");
+}
+
+// True when the call runs the fused scan (else the wide path, bf_wide.hip).
+bool fused_shape(const cvs_dataset* ds, int64_t k) { return ds->d <= kFusedMaxDim && k <= kFusedMaxK; }
+
+BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
+               const uint32_t* nbr, const float* dist) {
+  validate_bf(ctx, ds, queries, q, k, nbr, dist);
+  if (!fused_shape(ds, k)) fail(CVS_ERR_UNSUPPORTED, "shape outside the fused scan (d <= 1024, k <= 112)");
 
   BfPlan p;
   p.ks = int(ds->dp / kStepCols);
@@ -1305,26 +1204,6 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   p.off_part = p.off_lcut + align(size_t(q) * size_t(G) * sizeof(float));
   p.total = p.off_part + align(size_t(q) * size_t(G) * size_t(p.stride) * sizeof(uint64_t));
   return p;
-}
-
-// Certificate constants of a search over `ds` (see Cert).
-Cert make_cert(cvs_context* ctx, const cvs_dataset* ds, const float* qnorms, const float* qerr) {
-  Cert c{};
-  const double d = double(ds->d);
-  c.s2 = ds->scale * ds->scale;
-  c.rmax = ds->cert_rmax;
-  c.dx = ds->cert_dx;
-  c.a_coef = float(2.0 * (d + 16.0) * 0x1p-24 * (1.0 + 0x1p-20));
-  c.rho = float(2.0 * (d + 8.0) * 0x1p-24 * (1.0 + 0x1p-20));
-  // fp16 subnormal rounding (2^-25 absolute per element) is inside the
-  // measured error; this covers fl(q - mu) against q - mu, which the
-  // measured error does not see: 2^-24 |s (q - mu)| <= 2^-24 (|q~| + err),
-  // added by the merge as |q~| 2^-23, plus the fp32 sum behind err.
-  c.qslack = float(std::sqrt(d) * 0x1p-25);
-  c.qnorms = qnorms;
-  c.qerr = qerr;
-  c.counters = ctx->bf_counters;
-  return c;
 }
 
 // Enqueues the five launches of one search on the context stream, with the
@@ -1421,6 +1300,11 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
 
 void bf_search_device(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q,
                       int64_t k, uint32_t* nbr, float* dist) {
+  validate_bf(ctx, ds, queries, q, k, nbr, dist);
+  if (!fused_shape(ds, k)) {
+    bf_wide_search(ctx, ds, queries, q, k, nbr, dist);
+    return;
+  }
   const BfPlan p = plan_bf(ctx, ds, queries, q, k, nbr, dist);
   ctx->ws_search.reserve(p.total);
   bf_launch(ctx, ds, p, queries, q, k, nbr, dist, ctx->ws_search.as<char>(), true);
@@ -1453,6 +1337,37 @@ char* scratch_on(int device) {
 }
 
 }  // namespace
+
+namespace bf {
+void launch_query_tiles(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t q_rows,
+                        u32x4* qtiles, float* qnorms, float* qerr, hipEvent_t e0, hipEvent_t e1) {
+  hipExtLaunchKernelGGL(query_tiles_kernel, dim3(unsigned((q_rows + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                        ctx->stream, e0, e1, 0, queries, q, ds->d, int(ds->dp / kStepCols), q_rows,
+                        static_cast<const float*>(ds->mu), ds->scale, qtiles, qnorms, qerr);
+  after_launch("query_tiles_kernel");
+}
+
+// Certificate constants of a search over `ds` (see Cert).
+Cert make_cert(cvs_context* ctx, const cvs_dataset* ds, const float* qnorms, const float* qerr) {
+  Cert c{};
+  const double d = double(ds->d);
+  c.s2 = ds->scale * ds->scale;
+  c.rmax = ds->cert_rmax;
+  c.dx = ds->cert_dx;
+  c.a_coef = float(2.0 * (d + 16.0) * 0x1p-24 * (1.0 + 0x1p-20));
+  c.rho = float(2.0 * (d + 8.0) * 0x1p-24 * (1.0 + 0x1p-20));
+  // fp16 subnormal rounding (2^-25 absolute per element) is inside the
+  // measured error; this covers fl(q - mu) against q - mu, which the
+  // measured error does not see: 2^-24 |s (q - mu)| <= 2^-24 (|q~| + err),
+  // added by the merge as |q~| 2^-23, plus the fp32 sum behind err.
+  c.qslack = float(std::sqrt(d) * 0x1p-25);
+  c.qnorms = qnorms;
+  c.qerr = qerr;
+  c.counters = ctx->bf_counters;
+  return c;
+}
+
+}  // namespace bf
 }  // namespace cvs
 
 using namespace cvs;
@@ -1472,6 +1387,9 @@ int cvs_bf_search_noalloc(cvs_context* ctx, const cvs_dataset* ds, const float* 
                           int64_t k, uint32_t* out_neighbors_dev, float* out_distances_dev) {
   return guarded([&] {
     bind(ctx);
+    validate_bf(ctx, ds, queries_dev, q, k, out_neighbors_dev, out_distances_dev);
+    if (!fused_shape(ds, k))
+      fail(CVS_ERR_UNSUPPORTED, "cvs_bf_search_noalloc runs the fused scan only: d <= 1024 and k <= 112");
     const BfPlan p = plan_bf(ctx, ds, queries_dev, q, k, out_neighbors_dev, out_distances_dev);
     if (p.total > kScratchBytes)
       fail(CVS_ERR_UNSUPPORTED, "cvs_bf_search_noalloc: this call needs " + std::to_string(p.total) +

@@ -1,0 +1,415 @@
+// Exact brute-force k-NN beyond the fused scan's limits: d > 1024 (the scan
+// keeps a query tile's fp16 operands for the whole dimension in registers)
+// or k > 112 (the scan keeps at most 128 candidates per query).  The
+// reference's CPU loop has neither limit (src/cagra.cpp:211-252); this path
+// returns the same answers for d up to CVS_BF_MAX_DIM and k up to
+// CVS_BF_MAX_K.
+//
+// Per chunk of up to 512 queries (keys of the chunk within ~2 GiB):
+//  keys    fp16 MFMA keys d~ = |q~|^2 + |x~|^2 - 2 q~.x~ of the centred,
+//          scaled copies (the dataset's tiles and the queries converted the
+//          same way) for every (query, row), written to a chunk x N fp32
+//          matrix.  One wave per (32-row dataset tile, 4 query tiles): each
+//          k-step is one 16-byte load per lane of each operand (the tile
+//          layout is the MFMA operand layout) and four
+//          v_mfma_f32_32x32x16_f16, the loads of the next two k-steps in
+//          flight while the current ones multiply.
+//  select  one workgroup per query: a three-pass radix select (12 + 12 + 8
+//          bits of the keys' order image) finds the R-th smallest key
+//          (R = k + max(32, k / 4)); every row at or below it is re-ranked
+//          exactly in fp32 into a running top k kept in LDS (block bitonic
+//          sort of up to 2,048 keys).  The certificate of the fused path
+//          (Cert, bf_common.hpp) then bounds the exact distance of every row
+//          above the R-th key; if it does not clear the k-th exact distance,
+//          every row with a key up to the bound T_need is re-ranked too.
+//          Every key exists here, so no row outside the matrix is ever
+//          needed; a query whose fp16 copy is not finite re-ranks every
+//          row.
+//
+// Bytes per chunk: N * dp * 2 (tiles) + chunk * N * 4 (keys, written and
+// read three times by the select) + the re-ranked rows.
+#include <algorithm>
+#include <cmath>
+
+#include "bf_common.hpp"
+#include "cvs_internal.hpp"
+#include "device_util.hpp"
+
+namespace cvs {
+namespace bf {
+namespace {
+
+constexpr int kWT = 256;           // threads per workgroup (4 waves)
+constexpr int kChunkQ = 512;       // queries per chunk at most
+constexpr int kAccCap = 2048;      // exact keys held by the select's accumulator
+constexpr int kIdsCap = 4096;      // candidate ids per streaming step (16 keys per thread)
+
+struct KeysArgs {
+  const u32x4* tiles;   // dataset tiles
+  const float* norms;   // dataset norms (+inf past n)
+  int ks;               // k-steps per tile
+  const u32x4* qtiles;  // query tiles of the call (a multiple of 4 tiles)
+  const float* qnorms;  // their norms (+inf past q)
+  int qt0;              // first query tile of the chunk
+  int nq;               // queries of the chunk
+  float* keys;          // [nq][ldk]
+  int64_t ldk;          // padded rows (n_tiles * 32)
+};
+
+// Block (dataset tile group bx, query block by): wave w multiplies dataset
+// tile 4 bx + w with the query tiles qt0 + 4 by + j, j = 0..3.  Lane l holds,
+// for query tile j, query 32 (qt0 + 4 by + j) + l % 32 against rows
+// 32 t + 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
+__global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t t = int64_t(blockIdx.x) * 4 + wave;
+  const int qtb = a.qt0 + int(blockIdx.y) * 4;
+  const int64_t tstep = int64_t(a.ks) * 64;  // u32x4 per tile
+  const u32x4* A = a.tiles + t * tstep + lane;
+  const u32x4* B = a.qtiles + int64_t(qtb) * tstep + lane;
+  f32x16 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+
+  // Two k-steps per group; group g + 1 is loaded before group g multiplies.
+  u32x4 ra[2][2], rb[2][2][4];
+  auto load = [&](int buf, int s0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int s = s0 + u;
+      ra[buf][u] = A[int64_t(s) * 64];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rb[buf][u][j] = B[int64_t(j) * tstep + int64_t(s) * 64];
+    }
+  };
+  auto mult = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const half8 av = __builtin_bit_cast(half8, ra[buf][u]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, __builtin_bit_cast(half8, rb[buf][u][j]), acc[j], 0, 0,
+                                                        0);
+    }
+  };
+  // ks is a power of two >= 2 (the padded dimension is 32 * 2^j).
+  load(0, 0);
+  for (int s = 0; s < a.ks; s += 4) {
+    if (s + 2 < a.ks) load(1, s + 2);
+    mult(0);
+    if (s + 4 < a.ks) load(0, s + 4);
+    if (s + 2 < a.ks) mult(1);
+  }
+
+  const int half = lane >> 5;
+  const int64_t row0 = t * 32;
+  f32x4 xn[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) xn[g] = *reinterpret_cast<const f32x4*>(a.norms + row0 + 8 * g + 4 * half);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int ql = (qtb + j) * 32 + (lane & 31) - a.qt0 * 32;  // query of the chunk
+    if (ql >= a.nq) continue;
+    const float qn = a.qnorms[a.qt0 * 32 + ql];
+    float* dst = a.keys + int64_t(ql) * a.ldk + row0 + 4 * half;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = qn + xn[g][e] - 2.0f * acc[j][4 * g + e];
+      *reinterpret_cast<f32x4*>(dst + 8 * g) = v;
+    }
+  }
+}
+
+// Ascending bitonic sort of s[0..p) (p a power of two, <= kAccCap) by the
+// whole workgroup.
+__device__ __forceinline__ void block_sort(uint64_t* s, int p) {
+  for (int size = 2; size <= p; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < p / 2; i += kWT) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const uint64_t x = s[lo], y = s[hi];
+        if (asc ? y < x : x < y) {
+          s[lo] = y;
+          s[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+}
+
+struct SelectArgs {
+  const float* keys;     // [nq][ldk] of the chunk
+  int64_t ldk;
+  int64_t n;
+  int64_t d;
+  int q0;                // first query of the chunk
+  int R;                 // rank of the radix select
+  int64_t k;
+  const float* rows;     // fp32 rows
+  const float* queries;  // fp32 queries of the call
+  uint32_t* out_nbr;
+  float* out_dist;
+};
+
+__global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cert) {
+  __shared__ uint32_t s_hist[4096];
+  __shared__ uint64_t s_acc[kAccCap];
+  __shared__ uint32_t s_ids[kIdsCap];
+  __shared__ uint32_t s_wsum[4];
+  __shared__ uint32_t s_sel[4];  // bin, keys below it
+  __shared__ int s_mode;
+  __shared__ float s_tneed;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t ql = blockIdx.x;          // query of the chunk
+  const int64_t q = a.q0 + ql;            // query of the call
+  const float* kr = a.keys + ql * a.ldk;
+  const float* qv = a.queries + q * a.d;
+  const bool vec = (a.d & 3) == 0 && (reinterpret_cast<uintptr_t>(qv) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.rows) & 15) == 0;
+  const int64_t n = a.n, k = a.k;
+
+  // Finite inputs?  Otherwise no key means anything: every row is re-ranked.
+  const float qn = cert.qnorms[q];
+  const bool finite = qn <= 3.0e38f && cert.rmax <= 3.0e38f;
+
+  // 1. Radix select of the R-th smallest order image among the n keys.
+  uint32_t tau = 0xffffffffu, below = 0, eq = uint32_t(n);
+  if (finite) {
+    uint32_t prefix = 0;
+    int need = a.R;
+    below = 0;
+    const int shifts[3] = {20, 8, 0}, widths[3] = {12, 12, 8};
+#pragma unroll 1
+    for (int p = 0; p < 3; ++p) {
+      const int sh = shifts[p], w = widths[p], nb = 1 << w;
+      for (int i = tid; i < nb; i += kWT) s_hist[i] = 0;
+      __syncthreads();
+      const int hs = sh + w;  // bits above this pass must equal the prefix
+      for (int64_t i = tid; i < n; i += kWT) {
+        const uint32_t o = ord_f32(kr[i]);
+        if (hs >= 32 || (o >> hs) == prefix) atomicAdd(&s_hist[(o >> sh) & uint32_t(nb - 1)], 1u);
+      }
+      __syncthreads();
+      // Bin holding the need-th key: each thread sums nb / 256 bins, a block
+      // scan of those sums, then the owning thread walks its bins.
+      const int per = nb / kWT;
+      uint32_t mine = 0;
+      for (int b = 0; b < per; ++b) mine += s_hist[tid * per + b];
+      uint32_t incl = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+        if (lane >= o) incl += y;
+      }
+      if (lane == 63) s_wsum[wave] = incl;
+      __syncthreads();
+      uint32_t off = 0;
+      for (int w2 = 0; w2 < wave; ++w2) off += s_wsum[w2];
+      const uint32_t excl = off + incl - mine;
+      if (excl < uint32_t(need) && uint32_t(need) <= excl + mine) {
+        uint32_t c = excl;
+        for (int b = 0; b < per; ++b) {
+          const uint32_t h = s_hist[tid * per + b];
+          if (uint32_t(need) <= c + h) {
+            s_sel[0] = uint32_t(tid * per + b);
+            s_sel[1] = c;
+            s_sel[2] = h;
+            break;
+          }
+          c += h;
+        }
+      }
+      __syncthreads();
+      prefix = (prefix << w) | s_sel[0];
+      below += s_sel[1];
+      need -= int(s_sel[1]);
+      eq = s_sel[2];
+      __syncthreads();
+    }
+    tau = prefix;
+  }
+
+  // Running exact top k in s_acc[0..fill): after a flush, the first min(k,
+  // fill) entries are the best so far, sorted.
+  int fill = 0;
+  auto flush = [&]() {
+    int p = 1;
+    while (p < fill) p <<= 1;
+    for (int i = fill + tid; i < p; i += kWT) s_acc[i] = kSentinel;
+    __syncthreads();
+    block_sort(s_acc, p);
+    fill = fill < int(k) ? fill : int(k);
+  };
+  // Streams every row whose key passes `take` (by its order image) into the
+  // running top k: 16 keys per thread and step, compacted into s_ids, then
+  // re-ranked exactly by the four waves (8 rows per wave and pass).
+  auto stream = [&](auto take) {
+    for (int64_t base = 0; base < n; base += int64_t(kWT) * 16) {
+      uint32_t bits = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int64_t i = base + int64_t(j) * kWT + tid;
+        if (i < n && take(ord_f32(kr[i]))) bits |= 1u << j;
+      }
+      const uint32_t mine = uint32_t(__builtin_popcount(bits));
+      uint32_t incl = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+        if (lane >= o) incl += y;
+      }
+      if (lane == 63) s_wsum[wave] = incl;
+      __syncthreads();
+      uint32_t off = 0, total = 0;
+      for (int w2 = 0; w2 < 4; ++w2) {
+        if (w2 < wave) off += s_wsum[w2];
+        total += s_wsum[w2];
+      }
+      uint32_t pos = off + incl - mine;
+      while (bits) {
+        const int j = __builtin_ctz(bits);
+        bits &= bits - 1;
+        s_ids[pos++] = uint32_t(base + int64_t(j) * kWT + tid);
+      }
+      __syncthreads();
+      for (uint32_t done = 0; done < total;) {
+        const int m = int(std::min<uint32_t>(total - done, uint32_t(kAccCap - fill)));
+        for (int c = kExactU * wave; c < m; c += kExactU * 4) {
+          uint32_t id[kExactU];
+#pragma unroll
+          for (int u = 0; u < kExactU; ++u) id[u] = c + u < m ? s_ids[done + c + u] : 0xffffffffu;
+          float dd[kExactU];
+          wave_exact<kExactU>(id, a.rows, n, a.d, qv, vec, dd);
+#pragma unroll
+          for (int u = 0; u < kExactU; ++u)
+            if (lane == u && c + u < m) s_acc[fill + c + u] = (uint64_t(ord_f32(dd[u])) << 32) | id[u];
+        }
+        fill += m;
+        done += uint32_t(m);
+        __syncthreads();
+        if (fill == kAccCap) flush();
+      }
+    }
+  };
+
+  if (finite) {
+    stream([&](uint32_t o) { return o <= tau; });
+  } else {
+    stream([](uint32_t) { return true; });
+  }
+  flush();
+
+  // 2. Certificate (see Cert): every row not re-ranked has a key of at least
+  // unord(tau).
+  if (tid == 0) {
+    int mode = kCertPass;
+    float tneed = INFINITY;
+    const uint64_t kth = k <= fill ? s_acc[k - 1] : kSentinel;
+    if (!finite) {
+      atomicAdd(&cert.counters[0], 1ull);
+      atomicAdd(&cert.counters[1], 1ull);
+    }
+    if (finite && uint64_t(below) + eq < uint64_t(n)) {
+      const double dk = kth == kSentinel ? INFINITY : double(unord_f32(uint32_t(kth >> 32)));
+      const double qt = std::sqrt(double(qn)) * (1.0 + 0x1p-20);
+      const double qe = std::sqrt(double(cert.qerr[q]) * (1.0 + double(a.d + 8) * 0x1p-24)) * (1.0 + 0x1p-20);
+      const double E_ = qe + qt * 0x1p-23 + double(cert.qslack) + double(cert.dx);
+      const double A = double(cert.a_coef) * (qt + double(cert.rmax)) * (qt + double(cert.rmax));
+      const double V = double(cert.s2) * dk * (1.0 + double(cert.rho));
+      const double T = double(unord_f32(tau));
+      const double r = T > A ? std::sqrt(T - A) : 0.0;
+      const double lb = r > E_ ? (r - E_) * (r - E_) : 0.0;
+      if (!(lb * (1.0 - 0x1p-40) > V)) {
+        mode = kCertKeys;
+        tneed = V > 3.0e38 ? INFINITY
+                           : float(((std::sqrt(V) + E_) * (std::sqrt(V) + E_) + A) * (1.0 + 0x1p-20));
+        atomicAdd(&cert.counters[0], 1ull);
+      }
+    }
+    s_mode = mode;
+    s_tneed = tneed;
+  }
+  __syncthreads();
+  if (s_mode != kCertPass) {
+    const uint32_t hi = ord_f32(s_tneed);
+    stream([&](uint32_t o) { return o > tau && o <= hi; });
+    flush();
+  }
+
+  // 3. Output: k results by (distance, id), padded with UINT32_MAX / +inf.
+  for (int64_t i = tid; i < k; i += kWT) {
+    const uint64_t key = i < fill ? s_acc[i] : kSentinel;
+    a.out_nbr[q * k + i] = key == kSentinel ? 0xffffffffu : uint32_t(key);
+    a.out_dist[q * k + i] = key == kSentinel ? INFINITY : unord_f32(uint32_t(key >> 32));
+  }
+}
+
+}  // namespace
+
+void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
+                    uint32_t* nbr, float* dist) {
+  const int ks = int(ds->dp / kStepCols);
+  const int64_t q_tiles4 = ((q + 31) / 32 + 3) / 4 * 4;
+  const int64_t ldk = ds->n_tiles * kTileRows;
+  // Queries per chunk: a multiple of 128, at most 512, keys within ~2 GiB.
+  int64_t qc = kChunkQ;
+  while (qc > 128 && qc * ldk * 4 > (int64_t(2) << 30)) qc -= 128;
+  qc = std::min<int64_t>(qc, (q + 127) / 128 * 128);
+  auto align = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t off_qn = align(size_t(q_tiles4) * size_t(ks) * kStepBytes);
+  const size_t off_qe = off_qn + align(size_t(q_tiles4) * 32 * sizeof(float));
+  const size_t off_keys = off_qe + align(size_t(q) * sizeof(float));
+  const size_t total = off_keys + align(size_t(qc) * size_t(ldk) * sizeof(float));
+  ctx->ws_search.reserve(total);
+  char* ws = ctx->ws_search.as<char>();
+  u32x4* qtiles = reinterpret_cast<u32x4*>(ws);
+  float* qnorms = reinterpret_cast<float*>(ws + off_qn);
+  float* qerr = reinterpret_cast<float*>(ws + off_qe);
+  float* keys = reinterpret_cast<float*>(ws + off_keys);
+
+  const TimerSpan t0 = timer_span(ctx, "bf_prep");
+  launch_query_tiles(ctx, ds, queries, q, q_tiles4 * 32, qtiles, qnorms, qerr, t0.start, t0.stop);
+  const Cert cert = make_cert(ctx, ds, qnorms, qerr);
+  const int R = int(std::min<int64_t>(ds->n, k + std::max<int64_t>(32, k / 4)));
+  for (int64_t c0 = 0; c0 < q; c0 += qc) {
+    const int64_t nq = std::min(qc, q - c0);
+    KeysArgs ka{};
+    ka.tiles = reinterpret_cast<const u32x4*>(ds->tiles);
+    ka.norms = ds->norms;
+    ka.ks = ks;
+    ka.qtiles = qtiles;
+    ka.qnorms = qnorms;
+    ka.qt0 = int(c0 / 32);
+    ka.nq = int(nq);
+    ka.keys = keys;
+    ka.ldk = ldk;
+    const TimerSpan t1 = timer_span(ctx, "bf_scan");
+    hipExtLaunchKernelGGL(wide_keys_kernel, dim3(unsigned(ds->n_tiles / 4), unsigned((nq + 127) / 128)), dim3(kWT),
+                          0, ctx->stream, t1.start, t1.stop, 0, ka);
+    after_launch("wide_keys_kernel");
+    SelectArgs sa{};
+    sa.keys = keys;
+    sa.ldk = ldk;
+    sa.n = ds->n;
+    sa.d = ds->d;
+    sa.q0 = int(c0);
+    sa.R = R;
+    sa.k = k;
+    sa.rows = ds->rows;
+    sa.queries = queries;
+    sa.out_nbr = nbr;
+    sa.out_dist = dist;
+    const TimerSpan t2 = timer_span(ctx, "bf_merge");
+    hipExtLaunchKernelGGL(wide_select_kernel, dim3(unsigned(nq)), dim3(kWT), 0, ctx->stream, t2.start, t2.stop, 0, sa,
+                          cert);
+    after_launch("wide_select_kernel");
+  }
+}
+
+}  // namespace bf
+}  // namespace cvs

@@ -47,9 +47,12 @@ typedef struct cvs_context cvs_context; /* one device + one HIP stream */
 typedef struct cvs_dataset cvs_dataset; /* device-resident dataset (fp32 rows, fp16 tiles, norms) */
 typedef struct cvs_cagra_index cvs_cagra_index; /* device-resident graph index (rows, graph, seeds) */
 
-/* Limits of the fused brute-force kernel (checked by cvs_bf_search*). */
-#define CVS_BF_MAX_DIM 1024
-#define CVS_BF_MAX_K 112
+/* Limits of the brute force (checked by cvs_bf_search*).  Calls with
+ * d <= 1024 and k <= 112 run the fused streaming scan; larger d or k run a
+ * keys-matrix path with the same exact results (the reference's CPU loop,
+ * src/cagra.cpp:211-252, has no limit on either). */
+#define CVS_BF_MAX_DIM 16384
+#define CVS_BF_MAX_K 1024
 
 /* Limits of the graph search kernel (checked by cvs_cagra_search*). */
 #define CVS_CAGRA_MAX_DIM 1024
@@ -149,8 +152,10 @@ int cvs_dataset_rows(const cvs_dataset* ds, const float** out_rows);
  * outside the re-ranked candidates can be nearer than the k-th result; a
  * query that fails is re-ranked exactly over every row that could be (in
  * the worst case every row), so results are exact on any finite input.
- * Requires 1 <= k, k <= CVS_BF_MAX_K, d <= CVS_BF_MAX_DIM.  Host pointers,
- * blocking. */
+ * Requires 1 <= k <= CVS_BF_MAX_K and d <= CVS_BF_MAX_DIM; d > 1024 or
+ * k > 112 run a second path (fp16 MFMA keys of a query chunk against every
+ * row, a radix select, the same certificate and exact re-rank).  Host
+ * pointers, blocking. */
 int cvs_bf_search(cvs_context* ctx, const cvs_dataset* ds,
                   const float* queries, int64_t q, int64_t k,
                   uint32_t* out_neighbors, float* out_distances);
@@ -160,8 +165,8 @@ int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds,
                         const float* queries_dev, int64_t q, int64_t k,
                         uint32_t* out_neighbors_dev, float* out_distances_dev);
 
-/* cvs_bf_search_async without any allocation: no counterpart in the
- * reference.  For callers that cannot allocate device memory (code under HIP
+/* cvs_bf_search_async without any allocation, for d <= 1024 and k <= 112
+ * (the fused scan): no counterpart in the reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * workspace (query tiles, thresholds, sample minima, candidate lists) lives in
  * a 64 MiB array that the library holds on each device it runs on until the

@@ -189,11 +189,11 @@ def test_argument_errors(ctx):
     with pytest.raises(ValueError):
         ds.bf_search(np.ones((2, 4), np.float32), 0)
     with pytest.raises(ValueError):
-        ds.bf_search(np.ones((2, 4), np.float32), 113)
+        ds.bf_search(np.ones((2, 4), np.float32), 1025)
     with pytest.raises(ValueError):
         ds.bf_search(np.ones((2, 5), np.float32), 3)
     with pytest.raises(ValueError):
-        ctx.dataset(np.ones((10, 1025), np.float32)).bf_search(np.ones((1, 1025), np.float32), 3)
+        ctx.dataset(np.ones((10, 16385), np.float32)).bf_search(np.ones((1, 16385), np.float32), 3)
     with pytest.raises(ValueError):
         ctx.dataset(np.ones((0, 4), np.float32))
 
