@@ -698,7 +698,7 @@ def run_cagra_search(args) -> int:
     nav = cvs.cagra_nav_nodes(n)
     idx = ctx.cagra_index(base, graph, nav)
     gt = exact_ground_truth(base, qs, k)[0]
-    own_idx = ctx.cagra_index(base, own_graph, nav)
+    own_idx = ctx.cagra_index(base, own_graph, nav, traversal_bits=16)
     own_nbr, _ = own_idx.search(qs, k, itopk_size=args.itopk)
     own_idx.close()
     dq = cvs.DeviceArray.from_host(ctx, qs)

@@ -32,7 +32,7 @@ CVS_ERR_UNSUPPORTED = 5
 
 BF_MAX_DIM = 16384
 BF_MAX_K = 1024
-CAGRA_MAX_DIM = 1024
+CAGRA_MAX_DIM = 8192
 CAGRA_MAX_ITOPK = 512
 CAGRA_MAX_WIDTH = 16
 
@@ -115,6 +115,12 @@ _SIGNATURES["cvs_cagra_build_ex"] = (c_int, [c_void_p, c_void_p, c_int64, c_int6
 
 _SIGNATURES["cvs_bf_search_noalloc"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p])
 _SIGNATURES["cvs_cagra_nav_nodes"] = (c_int, [c_int64, c_void_p, POINTER(c_int64)])
+_SIGNATURES["cvs_cagra_entry_points"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p])
+_SIGNATURES["cvs_cagra_entry_points_async"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p])
+_SIGNATURES["cvs_cagra_search_reference"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32,
+                                                     c_uint32, c_void_p, c_void_p, c_void_p])
+_SIGNATURES["cvs_cagra_search_reference_async"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32,
+                                                           c_uint32, c_void_p, c_void_p, c_void_p])
 _SIGNATURES["cvs_context_bf_escalations"] = (c_int, [c_void_p, POINTER(c_uint64), POINTER(c_uint64), c_int])
 
 # The bucketing permutation seed of the reference (src/metal_context.mm:803).
@@ -297,7 +303,7 @@ class Context:
     def dataset(self, rows) -> "Dataset":
         return Dataset(self, rows)
 
-    def cagra_index(self, rows, graph, seeds=None, traversal_bits: int = 16) -> "CagraIndex":
+    def cagra_index(self, rows, graph, seeds=None, traversal_bits: int = 32) -> "CagraIndex":
         return CagraIndex(self, rows, graph, seeds, traversal_bits)
 
     def cagra_build_reference(self, rows, graph_degree: int = 64, exact_limit: int = None, pq_limit: int = None):
@@ -414,7 +420,7 @@ class CagraIndex:
     """Device-resident graph index (C: cvs_cagra_index): rows, neighbour lists
     and seed (navigation) node ids."""
 
-    def __init__(self, ctx: Context, rows, graph, seeds=None, traversal_bits: int = 16):
+    def __init__(self, ctx: Context, rows, graph, seeds=None, traversal_bits: int = 32):
         self.ctx = ctx
         h = c_void_p()
         graph_dev = isinstance(graph, DeviceArray)
@@ -460,6 +466,45 @@ class CagraIndex:
         _check(load().cvs_cagra_index_edge_distances(self.ctx.handle, self.handle,
                                                      host.ctypes.data_as(c_void_p), 0))
         return host
+
+    def entry_points(self, queries) -> np.ndarray:
+        """Per-query entry node: the nearest seed (navigation) node, as the
+        reference picks it (C: cvs_cagra_entry_points)."""
+        queries = _f32(queries)
+        out = np.empty(queries.shape[0], np.uint32)
+        _check(load().cvs_cagra_entry_points(self.ctx.handle, self.handle, queries.ctypes.data_as(c_void_p),
+                                             queries.shape[0], out.ctypes.data_as(c_void_p)))
+        return out
+
+    def search_reference(self, queries, k: int, beam_size: int, max_iter: int, entry_nodes=None):
+        """The reference's own beam search (C: cvs_cagra_search_reference):
+        one entry node per query (None: the hashed fallback), beam and
+        iteration cap as given."""
+        queries = _f32(queries)
+        q = queries.shape[0]
+        ent = None
+        if entry_nodes is not None:
+            ent = np.ascontiguousarray(entry_nodes, np.uint32)
+            if ent.shape != (q,):
+                raise ValueError("entry_nodes must hold one id per query")
+        nbr = np.empty((q, k), np.uint32)
+        dist = np.empty((q, k), np.float32)
+        _check(load().cvs_cagra_search_reference(self.ctx.handle, self.handle, queries.ctypes.data_as(c_void_p), q,
+                                                 int(k), int(beam_size), int(max_iter),
+                                                 None if ent is None else ent.ctypes.data_as(c_void_p),
+                                                 nbr.ctypes.data_as(c_void_p), dist.ctypes.data_as(c_void_p)))
+        return nbr, dist
+
+    def search_reference_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray,
+                               beam_size: int, max_iter: int, entry_nodes: DeviceArray = None) -> None:
+        _check(load().cvs_cagra_search_reference_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0],
+                                                       int(k), int(beam_size), int(max_iter),
+                                                       None if entry_nodes is None else entry_nodes.ptr, nbr.ptr,
+                                                       dist.ptr))
+
+    def entry_points_async(self, queries: DeviceArray, out: DeviceArray) -> None:
+        _check(load().cvs_cagra_entry_points_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0],
+                                                   out.ptr))
 
     def set_traversal(self, bits: int) -> None:
         """16: candidates evaluated on the fp16 copy, final list re-ranked in

@@ -53,8 +53,12 @@ namespace {
 
 constexpr uint32_t kInvalidId = 0xffffffffu;
 constexpr uint64_t kEmptyKey = ~0ull;
-constexpr int kMaxDv = CVS_CAGRA_MAX_DIM / 64;   // float4 per lane and row (fp32 traversal)
-constexpr int kMaxDv8 = CVS_CAGRA_MAX_DIM / 128; // 8-column pieces per lane and row (fp16 traversal)
+// Rows of up to kBigDim columns keep the query slice in registers; wider
+// rows (up to CVS_CAGRA_MAX_DIM) keep it in LDS and are gathered in chunks
+// of kBigDim columns.
+constexpr int kBigDim = 1024;
+constexpr int kMaxDv = kBigDim / 64;   // float4 per lane and row (fp32 traversal)
+constexpr int kMaxDv8 = kBigDim / 128; // 8-column pieces per lane and row (fp16 traversal)
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
@@ -126,7 +130,7 @@ __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
 // barriers between waves are needed then); the host launches W = 2 for large
 // batches, where the other wave's gathers hide the lead wave's serial work,
 // and W = 4 or 8 when few queries would leave most of the GPU idle.
-template <int E, int W, bool F16>
+template <int E, int W, bool F16, bool BIG>
 __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   extern __shared__ uint32_t s_mem[];
   const bool bitmap = a.bitmap_words > 0;
@@ -143,6 +147,11 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   // reset, [3, 4] parent count (alternating per iteration).  Alternating slots
   // keep a write for the next step from racing a slow wave's read.
   uint32_t* s_ctl = s_par + CVS_CAGRA_MAX_WIDTH;
+  // d > 1024 (BIG): the query stays in LDS, as given (s_q) and, for fp16
+  // traversal, centred and scaled (s_qc); dpad floats each, after the
+  // control words.
+  float* s_q = reinterpret_cast<float*>(s_ctl + 8);
+  float* s_qc = s_q + (BIG ? a.dq * 4 : 0);
 
   constexpr int kThreads = 64 * W;
   constexpr int kTeams = 4 * W;
@@ -154,15 +163,24 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   const int team = tid >> 4, tp = lane & 15;
 
   for (int i = tid; i < H; i += kThreads) s_hash[i] = hempty;
+  if constexpr (BIG) {
+    const float* qg = a.queries + qi * a.d;
+    for (int i = tid; i < 4 * a.dq; i += kThreads) {
+      const float v = i < a.d ? qg[i] : 0.f;
+      s_q[i] = v;
+      if (F16) s_qc[i] = i < a.d ? (v - a.mu[i]) * a.scale : 0.f;
+    }
+  }
 
-  // Query slice of this lane.  fp32 traversal: float4 columns tp + 16 j of
+  // Query slice of this lane (d <= 1024).  fp32 traversal: float4 columns tp + 16 j of
   // the padded row.  fp16 traversal (and its fp32 re-rank): 8-column pieces
   // tp + 16 j, so that a 16-lane team reads 256 contiguous bytes of an fp16
   // row (512 of an fp32 row) per piece.
   const float* qsrc = a.queries + qi * a.d;
-  float4 qv[F16 ? 1 : kMaxDv];
-  float qh[F16 ? kMaxDv8 : 1][8];
-  if constexpr (!F16) {
+  float4 qv[F16 || BIG ? 1 : kMaxDv];
+  float qh[F16 && !BIG ? kMaxDv8 : 1][8];
+  if constexpr (BIG) {
+  } else if constexpr (!F16) {
 #pragma unroll
     for (int j = 0; j < kMaxDv; ++j) {
       float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -191,7 +209,56 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
   // this lane's team: from the traversal copy, or (exact) from the fp32 rows.
   auto team_dist = [&](uint32_t rid, bool exact) -> float {
     float acc = 0.f;
-    if constexpr (!F16) {
+    if constexpr (BIG) {
+      // Chunks of 1,024 columns: the row's pieces tp + 16 j of the chunk,
+      // all loads of a chunk issued before the first is used; the query from
+      // LDS.
+      if (!F16 || exact) {
+        // fp32 rows: float4 columns (F16: 8-column pieces as two float4).
+        const float4* row = a.rows + int64_t(rid) * a.dq;
+        const float4* qq = reinterpret_cast<const float4*>(s_q);
+        for (int c0 = 0; c0 < a.dq; c0 += 256) {
+          const int nj = (a.dq - c0) / 16 < 16 ? (a.dq - c0) / 16 : 16;
+          float4 x[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (j < nj) x[j] = row[c0 + tp + 16 * j];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            if (j < nj) {
+              const float4 qj = qq[c0 + tp + 16 * j];
+              const float dx = qj.x - x[j].x, dy = qj.y - x[j].y;
+              const float dz = qj.z - x[j].z, dw = qj.w - x[j].w;
+              acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+            }
+          }
+        }
+      } else {
+        // fp16 traversal copy: 8-column pieces against the centred query.
+        const uint4* row = a.rows16 + int64_t(rid) * a.dq8;
+        for (int c0 = 0; c0 < a.dq8; c0 += 128) {
+          const int nj = (a.dq8 - c0) / 16 < 8 ? (a.dq8 - c0) / 16 : 8;
+          uint4 x[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (j < nj) x[j] = row[c0 + tp + 16 * j];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            if (j < nj) {
+              const half8_t h = __builtin_bit_cast(half8_t, x[j]);
+              const float* qc = s_qc + 8 * (c0 + tp + 16 * j);
+              float p[8];
+#pragma unroll
+              for (int t = 0; t < 8; ++t) {
+                const float dt = qc[t] - float(h[t]);
+                p[t] = dt * dt;
+              }
+              acc += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            }
+          }
+        }
+      }
+    } else if constexpr (!F16) {
       const float4* row = a.rows + int64_t(rid) * a.dq + tp;
       float4 x[kMaxDv];
 #pragma unroll
@@ -471,22 +538,26 @@ int waves_per_query(int64_t workgroups) {
 }
 
 template <int E, bool F16>
-void launch_search(int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a, hipEvent_t e0,
-                   hipEvent_t e1) {
+void launch_search(int waves, bool big, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a,
+                   hipEvent_t e0, hipEvent_t e1) {
+  if (big) {  // d > 1024: four waves per query at any batch size
+    hipExtLaunchKernelGGL((cagra_search_kernel<E, 4, F16, true>), grid, dim3(256), lds, stream, e0, e1, 0, a);
+    return;
+  }
   switch (waves) {
-    case 2: hipExtLaunchKernelGGL((cagra_search_kernel<E, 2, F16>), grid, dim3(128), lds, stream, e0, e1, 0, a); break;
-    case 4: hipExtLaunchKernelGGL((cagra_search_kernel<E, 4, F16>), grid, dim3(256), lds, stream, e0, e1, 0, a); break;
-    default: hipExtLaunchKernelGGL((cagra_search_kernel<E, 8, F16>), grid, dim3(512), lds, stream, e0, e1, 0, a); break;
+    case 2: hipExtLaunchKernelGGL((cagra_search_kernel<E, 2, F16, false>), grid, dim3(128), lds, stream, e0, e1, 0, a); break;
+    case 4: hipExtLaunchKernelGGL((cagra_search_kernel<E, 4, F16, false>), grid, dim3(256), lds, stream, e0, e1, 0, a); break;
+    default: hipExtLaunchKernelGGL((cagra_search_kernel<E, 8, F16, false>), grid, dim3(512), lds, stream, e0, e1, 0, a); break;
   }
 }
 
 template <int E>
-void launch_search(bool f16, int waves, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a,
+void launch_search(bool f16, int waves, bool big, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a,
                    hipEvent_t e0, hipEvent_t e1) {
   if (f16)
-    launch_search<E, true>(waves, grid, lds, stream, a, e0, e1);
+    launch_search<E, true>(waves, big, grid, lds, stream, a, e0, e1);
   else
-    launch_search<E, false>(waves, grid, lds, stream, a, e0, e1);
+    launch_search<E, false>(waves, big, grid, lds, stream, a, e0, e1);
 }
 
 // Merge of the teams' lists of one query (one wave per query): the teams x
@@ -562,8 +633,11 @@ __global__ void rows_to_half_kernel(const float4* __restrict__ src, size_t piece
 // recompute_graph_distances, shaders/cagra_kernels.metal:658-681).  One
 // workgroup per node: the node's row stays in registers (float4 columns
 // tp + 16 j per lane of each 16-lane team) and the 16 teams gather the
-// neighbour rows, 256 contiguous bytes per load instruction and team.
-// Entries that are not row ids (UINT32_MAX, or >= n) get +inf.
+// neighbour rows, 256 contiguous bytes per load instruction and team.  Rows
+// wider than 1,024 columns (BIG) go in chunks of 1,024, the node's piece of
+// each chunk loaded again (from the caches).  Entries that are not row ids
+// (UINT32_MAX, or >= n) get +inf.
+template <bool BIG>
 __global__ __launch_bounds__(256) void edge_distances_kernel(const float4* __restrict__ rows, int dq, int dv,
                                                              const uint32_t* __restrict__ graph, int g, uint32_t n,
                                                              float* __restrict__ out) {
@@ -571,24 +645,34 @@ __global__ __launch_bounds__(256) void edge_distances_kernel(const float4* __res
   const int tid = threadIdx.x, team = tid >> 4, tp = tid & 15;
   float4 xv[kMaxDv];
   const float4* self = rows + node * dq + tp;
+  if constexpr (!BIG) {
 #pragma unroll
-  for (int j = 0; j < kMaxDv; ++j)
-    if (j < dv) xv[j] = self[16 * j];
+    for (int j = 0; j < kMaxDv; ++j)
+      if (j < dv) xv[j] = self[16 * j];
+  }
   for (int e = team; e < g; e += 16) {
     const uint32_t nb = graph[node * g + e];
     const bool valid = nb < n;
     const float4* row = rows + int64_t(valid ? nb : uint32_t(node)) * dq + tp;
-    float4 x[kMaxDv];
-#pragma unroll
-    for (int j = 0; j < kMaxDv; ++j)
-      if (j < dv) x[j] = row[16 * j];
     float acc = 0.f;
+    for (int c0 = 0; c0 < (BIG ? dq : 1); c0 += 256) {
+      const int nj = BIG ? ((dq - c0) / 16 < kMaxDv ? (dq - c0) / 16 : kMaxDv) : dv;
+      if constexpr (BIG) {
 #pragma unroll
-    for (int j = 0; j < kMaxDv; ++j) {
-      if (j < dv) {
-        const float dx = xv[j].x - x[j].x, dy = xv[j].y - x[j].y;
-        const float dz = xv[j].z - x[j].z, dw = xv[j].w - x[j].w;
-        acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        for (int j = 0; j < kMaxDv; ++j)
+          if (j < nj) xv[j] = self[c0 + 16 * j];
+      }
+      float4 x[kMaxDv];
+#pragma unroll
+      for (int j = 0; j < kMaxDv; ++j)
+        if (j < nj) x[j] = row[c0 + 16 * j];
+#pragma unroll
+      for (int j = 0; j < kMaxDv; ++j) {
+        if (j < nj) {
+          const float dx = xv[j].x - x[j].x, dy = xv[j].y - x[j].y;
+          const float dz = xv[j].z - x[j].z, dw = xv[j].w - x[j].w;
+          acc += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        }
       }
     }
     acc += xor_lanes_f(acc, 8);
@@ -627,7 +711,8 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   const int e_slots = itopk <= 64 ? 1 : (itopk <= 128 ? 2 : (itopk <= 256 ? 4 : 8));
   int64_t iters = max_iterations;
   if (iters == 0) iters = std::max<int64_t>(200, 2 * itopk / width);
-  const int waves = waves_per_query(q * teams);
+  const bool big = idx->d > kBigDim;
+  const int waves = big ? 4 : waves_per_query(q * teams);
   // The visited hash at twice (W=2) or four times (W=4, 8) the size that
   // keeps it half empty, up to 2^13 entries (32 KiB): the lead wave's probe
   // chains stay short, and fewer mid-search clears mean fewer rows evaluated
@@ -642,7 +727,8 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   const int64_t bitmap_words = (idx->n + 2047) / 2048 * 64;
   const bool use_bitmap = bitmap_words <= (int64_t(1) << hash_bits);
   const size_t visit_words = use_bitmap ? size_t(bitmap_words) : (size_t(1) << hash_bits);
-  const size_t lds = visit_words * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4;
+  const size_t lds = visit_words * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4 +
+                     (big ? size_t(idx->dpad) * 4 * (idx->traversal_bits == 16 ? 2 : 1) : 0);
 
   SearchArgs a{};
   a.rows = reinterpret_cast<const float4*>(idx->rows);
@@ -687,10 +773,10 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   // The search kernel starts the span; the team merge (if any) ends it.
   hipEvent_t e1 = teams > 1 ? nullptr : t0.stop;
   switch (e_slots) {
-    case 1: launch_search<1>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
-    case 2: launch_search<2>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
-    case 4: launch_search<4>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
-    default: launch_search<8>(f16, waves, grid, lds, ctx->stream, a, t0.start, e1); break;
+    case 1: launch_search<1>(f16, waves, big, grid, lds, ctx->stream, a, t0.start, e1); break;
+    case 2: launch_search<2>(f16, waves, big, grid, lds, ctx->stream, a, t0.start, e1); break;
+    case 4: launch_search<4>(f16, waves, big, grid, lds, ctx->stream, a, t0.start, e1); break;
+    default: launch_search<8>(f16, waves, big, grid, lds, ctx->stream, a, t0.start, e1); break;
   }
   after_launch("cagra_search_kernel");
   if (teams > 1) {
@@ -819,7 +905,8 @@ int cvs_cagra_index_edge_distances(cvs_context* ctx, const cvs_cagra_index* inde
       dst = ctx->ws_io.as<float>();
     }
     const TimerSpan t0 = timer_span(ctx, "cagra_edge_distances");
-    hipExtLaunchKernelGGL(edge_distances_kernel, dim3(unsigned(index->n)), dim3(256), 0, ctx->stream, t0.start,
+    auto kern = index->d > kBigDim ? edge_distances_kernel<true> : edge_distances_kernel<false>;
+    hipExtLaunchKernelGGL(kern, dim3(unsigned(index->n)), dim3(256), 0, ctx->stream, t0.start,
                           t0.stop, 0, reinterpret_cast<const float4*>(index->rows), int(index->dpad / 4),
                           int(index->dpad / 64), static_cast<const uint32_t*>(index->graph), int(index->degree),
                           uint32_t(index->n), dst);

@@ -128,7 +128,7 @@ struct cvs_cagra_index {
   int64_t dpad = 0;        // row stride in elements (d rounded up to 128)
   uint32_t degree = 0;
   uint32_t n_seeds = 0;
-  int traversal_bits = 16;   // 16: traverse rows16, re-rank the list from rows; 32: rows only
+  int traversal_bits = 32;   // 32: rows only; 16: traverse rows16, re-rank the list from rows
   float* rows = nullptr;     // n x dpad fp32, zero-padded
   void* rows16 = nullptr;    // n x dpad fp16 copy of scale * (rows - mu), zero-padded
   float* mu = nullptr;       // dpad column means (zero-padded)

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <limits>
 #include <stdexcept>
+#include <vector>
 
 #include "backend.hpp"
 
@@ -171,12 +172,38 @@ void search<float, std::uint32_t, std::int64_t>(
   detail::device_state& dev = device_state_of(index, has_graph);
   cvs_context* ctx = Backend::instance().ctx();
   if (has_graph) {
-    // itopk_size 0 -> 128 and max_iterations 0 -> the kernel's cap follow
-    // src/cagra.cpp:182-185.  The reference's clamp of the beam to 32 for
-    // q <= 4 (:186-189) is not applied: it only lowers recall.
     auto clamp32 = [](std::uint64_t v) {
       return static_cast<std::uint32_t>(std::min<std::uint64_t>(v, 0xffffffffu));
     };
+    if (params.reference_beam) {
+      // The reference's route (src/cagra.cpp:128-196): each query's entry
+      // node is its nearest navigation node (on the GPU), beam = itopk_size
+      // (0 -> 128), iterations = max_iterations (0 -> 200), and q <= 4
+      // clamps the beam to 32.
+      std::uint32_t beam = clamp32(params.itopk_size > 0 ? params.itopk_size : 128);
+      std::uint32_t iters = clamp32(params.max_iterations > 0 ? params.max_iterations : 200);
+      if (q <= 4) {
+        beam = std::min<std::uint32_t>(beam, 32u);
+        iters = std::min<std::uint32_t>(iters, 200u);
+      }
+      std::vector<std::uint32_t> entry;
+      if (!index.nav_nodes().empty()) {
+        entry.resize(static_cast<std::size_t>(q));
+        counted([&] {
+          return cvs_cagra_entry_points(ctx, dev.graph_index->ix, queries.data_handle(), q, entry.data());
+        });
+      }
+      counted([&] {
+        return cvs_cagra_search_reference(ctx, dev.graph_index->ix, queries.data_handle(), q, k, beam, iters,
+                                          entry.empty() ? nullptr : entry.data(), neighbors.data_handle(),
+                                          distances.data_handle());
+      });
+      return;
+    }
+    // itopk_size 0 -> 128 and max_iterations 0 -> the kernel's cap follow
+    // src/cagra.cpp:182-185.  The reference's clamp of the beam to 32 for
+    // q <= 4 (:186-189) is not applied here: it only lowers recall.
+    check(cvs_cagra_index_set_traversal(dev.graph_index->ix, params.fp16_traversal ? 16 : 32));
     if (params.algo == search_algo::MULTI_CTA) {
       // Teams of workgroups per query with 32-entry lists (k if larger), as
       // many teams as cuVS's multi-CTA mode uses CTAs: max(search_width,

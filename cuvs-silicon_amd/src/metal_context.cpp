@@ -24,13 +24,11 @@ struct MetalContext::Impl {
   const float* bf_ptr = nullptr;
   int64_t bf_n = 0, bf_d = 0;
   cvs_dataset* bf_ds = nullptr;
-  // Device copy of the last graph index, keyed by (dataset, graph, N, D, G,
-  // entry set).
+  // Device copy of the last graph index, keyed by (dataset, graph, N, D, G).
   const float* gi_rows = nullptr;
   const uint32_t* gi_graph = nullptr;
   int64_t gi_n = 0, gi_d = 0;
   uint32_t gi_degree = 0;
-  std::vector<uint32_t> gi_seeds;
   cvs_cagra_index* gi = nullptr;
 
   void drop_dataset() {
@@ -117,31 +115,23 @@ uint64_t MetalContext::search_cagra(const float* dataset, int64_t N, int64_t D, 
                                     uint32_t* out_neighbors, float* out_distances, int64_t K, uint32_t beam_size,
                                     uint32_t max_iter, const uint32_t* entry_nodes) {
   cvs_context* ctx = require(impl_->ctx);
-  std::vector<uint32_t> seeds;
-  if (entry_nodes) {
-    seeds.assign(entry_nodes, entry_nodes + Q);
-    std::sort(seeds.begin(), seeds.end());
-    seeds.erase(std::unique(seeds.begin(), seeds.end()), seeds.end());
-    seeds.erase(std::remove_if(seeds.begin(), seeds.end(), [&](uint32_t s) { return int64_t(s) >= N; }),
-                seeds.end());
-  }
   Impl& m = *impl_;
   if (m.gi == nullptr || m.gi_rows != dataset || m.gi_graph != knn_graph || m.gi_n != N || m.gi_d != D ||
-      m.gi_degree != graph_degree || m.gi_seeds != seeds) {
+      m.gi_degree != graph_degree) {
     m.drop_index();
-    check(cvs_cagra_index_create(ctx, dataset, N, D, 0, knn_graph, graph_degree, 0,
-                                 seeds.empty() ? nullptr : seeds.data(), static_cast<uint32_t>(seeds.size()),
-                                 &m.gi));
-    check(cvs_cagra_index_set_traversal(m.gi, 32));  // the reference traverses in fp32
+    check(cvs_cagra_index_create(ctx, dataset, N, D, 0, knn_graph, graph_degree, 0, nullptr, 0, &m.gi));
     m.gi_rows = dataset;
     m.gi_graph = knn_graph;
     m.gi_n = N;
     m.gi_d = D;
     m.gi_degree = graph_degree;
-    m.gi_seeds = std::move(seeds);
   }
+  // The reference kernel itself: query q starts from entry_nodes[q] (or the
+  // hashed fallback), with the caller's beam and iteration cap
+  // (src/metal_context.mm:1041-1110).
   const uint64_t before = cvs_dispatch_count();
-  check(cvs_cagra_search(ctx, m.gi, queries, Q, K, beam_size, 1, max_iter, out_neighbors, out_distances));
+  check(cvs_cagra_search_reference(ctx, m.gi, queries, Q, K, beam_size, max_iter, entry_nodes, out_neighbors,
+                                   out_distances));
   return cvs_dispatch_count() - before;
 }
 

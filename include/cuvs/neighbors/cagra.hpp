@@ -69,6 +69,17 @@ struct search_params {
   float hashmap_max_fill_rate = 0.5F;
   std::uint32_t num_random_samplings = 1;
   std::uint64_t rand_xor_mask = 0x128394;
+  // Added after the reference's fields:
+  // - fp16_traversal: evaluate candidates on an fp16 copy of the rows (the
+  //   final list is re-ranked in fp32, so distances stay exact); off: every
+  //   evaluation in fp32, as the reference traverses.
+  // - reference_beam: run the reference's own beam search (one entry node
+  //   per query, the nearest navigation node; an unsorted beam of itopk_size
+  //   with replace-worst insertion; the beam clamped to 32 for q <= 4), which
+  //   returns what the reference returns query by query; off: the
+  //   register-list search seeded from every navigation node.
+  bool fp16_traversal = false;
+  bool reference_beam = false;
 };
 
 namespace detail {

@@ -54,8 +54,9 @@ typedef struct cvs_cagra_index cvs_cagra_index; /* device-resident graph index (
 #define CVS_BF_MAX_DIM 16384
 #define CVS_BF_MAX_K 1024
 
-/* Limits of the graph search kernel (checked by cvs_cagra_search*). */
-#define CVS_CAGRA_MAX_DIM 1024
+/* Limits of the graph search kernel (checked by cvs_cagra_search*).  Rows
+ * of up to 1024 columns keep the query in registers, wider ones in LDS. */
+#define CVS_CAGRA_MAX_DIM 8192
 #define CVS_CAGRA_MAX_ITOPK 512
 #define CVS_CAGRA_MAX_WIDTH 16
 #define CVS_CAGRA_MAX_TEAMS 64
@@ -202,13 +203,13 @@ int cvs_cagra_index_create(cvs_context* ctx, const float* rows, int64_t n, int64
                            cvs_cagra_index** out_index);
 int cvs_cagra_index_destroy(cvs_cagra_index* index);
 
-/* Precision of the graph traversal: 16 (the default) evaluates candidates on
- * an fp16 copy of the rows made at index creation, then recomputes the
- * distances of the final itopk list from the fp32 rows and re-sorts it, so
- * that output distances are exact fp32; 32 evaluates every candidate on the
- * fp32 rows, as the reference's beam search does
- * (shaders/cagra_kernels.metal:117-132).  No counterpart in the reference:
- * the fp16 copy halves the bytes each distance evaluation reads. */
+/* Precision of the graph traversal: 32 (the default) evaluates every
+ * candidate on the fp32 rows, as the reference's beam search does
+ * (shaders/cagra_kernels.metal:117-132); 16 evaluates candidates on an fp16
+ * copy of the centred, scaled rows made at index creation, then recomputes
+ * the distances of the final itopk list from the fp32 rows and re-sorts it,
+ * so that output distances are exact fp32.  No counterpart in the
+ * reference: the fp16 copy halves the bytes each distance evaluation reads. */
 int cvs_cagra_index_set_traversal(cvs_cagra_index* index, int bits);
 
 /* Exact squared L2 length of every edge of the index's graph: out[i*degree
@@ -260,6 +261,38 @@ int cvs_cagra_search_async(cvs_context* ctx, const cvs_cagra_index* index, const
                            int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
                            uint32_t max_iterations, uint32_t* out_neighbors_dev,
                            float* out_distances_dev, uint32_t* out_stats_dev);
+
+/* Per-query entry node of the reference's search route (src/cagra.cpp:
+ * 128-178): among the index's seed nodes (the navigation nodes), the one
+ * that minimises |q|^2 - 2 q.v + |v|^2 in fp32, the first on ties, computed
+ * on the GPU.  The index must have seed nodes.  Host pointers, blocking; the
+ * _async form takes device pointers. */
+int cvs_cagra_entry_points(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
+                           uint32_t* out_entry);
+int cvs_cagra_entry_points_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                                 int64_t q, uint32_t* out_entry_dev);
+
+/* The reference's own beam search (shaders/cagra_kernels.metal:28-199, host
+ * src/metal_context.mm:1041-1110), for query-by-query parity with it:
+ * query i starts from entry_nodes[i] when that is < n, else (or with
+ * entry_nodes null) from (i * 2654435761) mod n; an unsorted beam of
+ * beam_size entries (1 to CVS_CAGRA_MAX_ITOPK, used as given: the
+ * reference's defaults and its q <= 4 clamp, src/cagra.cpp:182-189, are the
+ * caller's); each iteration expands the first unexpanded entry of smallest
+ * distance and offers its neighbours in graph order, an unvisited one
+ * replacing the first entry of largest distance if strictly closer; at most
+ * max_iter iterations; fp32 distances over the fp32 rows.  Results sorted by
+ * (distance, id), padded with UINT32_MAX / +inf.  Replaces
+ * MetalContext::search_cagra (metal_context.hpp:58-67).  Host pointers,
+ * blocking (entry_nodes: q host ids or null); the _async form takes device
+ * pointers (entry_nodes_dev: q device ids or null). */
+int cvs_cagra_search_reference(cvs_context* ctx, const cvs_cagra_index* index, const float* queries, int64_t q,
+                               int64_t k, uint32_t beam_size, uint32_t max_iter, const uint32_t* entry_nodes,
+                               uint32_t* out_neighbors, float* out_distances);
+int cvs_cagra_search_reference_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                                     int64_t q, int64_t k, uint32_t beam_size, uint32_t max_iter,
+                                     const uint32_t* entry_nodes_dev, uint32_t* out_neighbors_dev,
+                                     float* out_distances_dev);
 
 /* ---- CAGRA graph build --------------------------------------------------- */
 

@@ -9,9 +9,16 @@
 //  - graph_degree = 0 (exact route, src/cagra.cpp:197-202) and the
 //    brute_force namespace (uint32 and int64 ids);
 //  - build -> save_index -> load_index -> search on random data against exact
-//    search.
+//    search;
+//  - the default graph search traverses in fp32 (fp16 traversal is opt-in);
+//  - MetalContext::search_brute_force and search_cagra (the reference's
+//    backend interface) against the C ABI, with a distinct entry node per
+//    query, and the reference_beam search mode of cagra::search.
 #include <cuvs/neighbors/brute_force.hpp>
 #include <cuvs/neighbors/cagra.hpp>
+#include <cuvs_silicon/metal_context.hpp>
+
+#include "cvs_hip.h"
 
 #include <algorithm>
 #include <cmath>
@@ -268,6 +275,136 @@ void nav_change_reseeds() {
   CHECK(nbr[0] == B);
 }
 
+// Rows 1, 2 and 3 differ by less than the fp16 copy resolves after
+// centring (their centred values 49.99, 50.00, 50.01 all round to 50), so
+// an fp16 traversal with a one-entry list keeps the lowest id of the tie
+// (row 1) while the fp32 traversal keeps the exact nearest, row 3.
+void default_search_is_fp32() {
+  const std::int64_t N = 4, D = 4;
+  std::vector<float> base(N * D, 0.f);
+  base[0] = -200.f;
+  base[1 * D] = 0.f;
+  base[2 * D] = 0.01f;
+  base[3 * D] = 0.02f;
+  cagra::index<float, std::uint32_t> idx{base, N, D};
+  std::vector<std::uint32_t> g;
+  for (std::uint32_t i = 0; i < N; ++i)
+    for (std::uint32_t j = 0; j < N; ++j)
+      if (j != i) g.push_back(j);
+  idx.set_knn_graph(g, N - 1);
+  idx.set_nav_nodes({0});
+  idx.set_nav_vectors(std::vector<float>(base.begin(), base.begin() + D));
+  std::vector<float> q(D, 0.f);
+  q[0] = 0.02f;
+  raft::resources res;
+  std::vector<std::uint32_t> nbr(1);
+  std::vector<float> dist(1);
+  auto run = [&](const cagra::search_params& sp) {
+    cagra::search(res, sp, idx, raft::make_device_matrix_view<const float, std::int64_t>(q.data(), 1, D),
+                  raft::make_device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), 1, 1),
+                  raft::make_device_matrix_view<float, std::int64_t>(dist.data(), 1, 1));
+    return nbr[0];
+  };
+  cagra::search_params sp;
+  sp.itopk_size = 1;
+  CHECK(!sp.fp16_traversal && !sp.reference_beam);
+  CHECK(run(sp) == 3u);
+  CHECK(dist[0] == 0.f);
+  sp.fp16_traversal = true;
+  CHECK(run(sp) == 1u);  // the opt-in fp16 copy cannot tell rows 1-3 apart
+  sp.fp16_traversal = false;
+  CHECK(run(sp) == 3u);
+}
+
+// MetalContext (the reference's backend class) against the C ABI.
+void metal_context_matches_c_abi() {
+  auto& mc = cuvs_silicon::MetalContext::instance();
+  CHECK(mc.is_available());
+  const std::int64_t N = 3000, D = 48, Q = 40, K = 8;
+  std::mt19937 rng(17);
+  std::uniform_int_distribution<int> u(-4, 4);  // integer data: every sum exact
+  std::vector<float> base(N * D), qs(Q * D);
+  for (auto& v : base) v = float(u(rng));
+  for (auto& v : qs) v = float(u(rng));
+
+  cvs_context* ctx = nullptr;
+  CHECK(cvs_context_create(0, &ctx) == CVS_OK);
+
+  // Exact search.
+  std::vector<std::uint32_t> n1(Q * K), n2(Q * K);
+  std::vector<float> d1(Q * K), d2(Q * K);
+  CHECK(mc.search_brute_force(base.data(), N, D, qs.data(), Q, n1.data(), d1.data(), K) > 0);
+  cvs_dataset* ds = nullptr;
+  CHECK(cvs_dataset_create(ctx, base.data(), N, D, 0, &ds) == CVS_OK);
+  CHECK(cvs_bf_search(ctx, ds, qs.data(), Q, K, n2.data(), d2.data()) == CVS_OK);
+  CHECK(n1 == n2 && d1 == d2);
+  cvs_dataset_destroy(ds);
+
+  // Graph search with a distinct entry node per query.
+  const std::uint32_t G = 16;
+  std::vector<std::uint32_t> graph(N * G);
+  cvs_build_stats st{};
+  CHECK(cvs_cagra_build(ctx, base.data(), N, D, 0, 32, G, 10, 0.001f, 0xFEDCBA9876543210ULL, graph.data(), 0,
+                        &st) == CVS_OK);
+  std::vector<std::uint32_t> entry(Q);
+  for (std::int64_t i = 0; i < Q; ++i) entry[i] = std::uint32_t((i * 977) % N);
+  CHECK(mc.search_cagra(base.data(), N, D, graph.data(), G, qs.data(), Q, n1.data(), d1.data(), K, 32, 100,
+                        entry.data()) > 0);
+  cvs_cagra_index* ix = nullptr;
+  CHECK(cvs_cagra_index_create(ctx, base.data(), N, D, 0, graph.data(), G, 0, nullptr, 0, &ix) == CVS_OK);
+  CHECK(cvs_cagra_search_reference(ctx, ix, qs.data(), Q, K, 32, 100, entry.data(), n2.data(), d2.data()) ==
+        CVS_OK);
+  CHECK(n1 == n2 && d1 == d2);
+  cvs_cagra_index_destroy(ix);
+
+  // With no edges each query can only return its own entry node.
+  std::vector<std::uint32_t> empty(N * G, kNone);
+  CHECK(mc.search_cagra(base.data(), N, D, empty.data(), G, qs.data(), Q, n1.data(), d1.data(), K, 32, 100,
+                        entry.data()) > 0);
+  for (std::int64_t i = 0; i < Q; ++i) {
+    CHECK(n1[i * K] == entry[i]);
+    CHECK(n1[i * K + 1] == kNone && std::isinf(d1[i * K + 1]));
+  }
+  cvs_context_destroy(ctx);
+}
+
+// cagra::search with reference_beam: entry nodes from the navigation
+// nodes, the beam clamped to 32 for q <= 4, the reference kernel.
+void reference_beam_mode() {
+  const std::int64_t N = 2500, D = 24, K = 5;
+  std::mt19937 rng(23);
+  std::uniform_int_distribution<int> u(-5, 5);
+  std::vector<float> base(N * D), qs(3 * D);
+  for (auto& v : base) v = float(u(rng));
+  for (auto& v : qs) v = float(u(rng));
+  raft::resources res;
+  cagra::index_params ip;
+  ip.graph_degree = 16;
+  ip.intermediate_graph_degree = 32;
+  auto idx = cagra::build(res, ip, raft::make_device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  cagra::search_params sp;
+  sp.reference_beam = true;
+  sp.itopk_size = 64;
+  std::vector<std::uint32_t> nbr(3 * K), n2(3 * K);
+  std::vector<float> dist(3 * K), d2(3 * K);
+  cagra::search(res, sp, idx, raft::make_device_matrix_view<const float, std::int64_t>(qs.data(), 3, D),
+                raft::make_device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), 3, K),
+                raft::make_device_matrix_view<float, std::int64_t>(dist.data(), 3, K));
+  // The same through the C ABI: entry points, beam 32 (q = 3 <= 4), 200 iterations.
+  cvs_context* ctx = nullptr;
+  CHECK(cvs_context_create(0, &ctx) == CVS_OK);
+  cvs_cagra_index* ix = nullptr;
+  const auto& nav = idx.nav_nodes();
+  CHECK(cvs_cagra_index_create(ctx, base.data(), N, D, 0, idx.knn_graph().data(), idx.graph_degree(), 0, nav.data(),
+                               std::uint32_t(nav.size()), &ix) == CVS_OK);
+  std::vector<std::uint32_t> entry(3);
+  CHECK(cvs_cagra_entry_points(ctx, ix, qs.data(), 3, entry.data()) == CVS_OK);
+  CHECK(cvs_cagra_search_reference(ctx, ix, qs.data(), 3, K, 32, 200, entry.data(), n2.data(), d2.data()) == CVS_OK);
+  CHECK(nbr == n2 && dist == d2);
+  cvs_cagra_index_destroy(ix);
+  cvs_context_destroy(ctx);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -276,5 +413,8 @@ int main(int argc, char** argv) {
   dispatch_test();
   build_save_load_search(scratch);
   nav_change_reseeds();
+  default_search_is_fp32();
+  metal_context_matches_c_abi();
+  reference_beam_mode();
   return apitest::finish("test_api_gpu");
 }

@@ -220,7 +220,7 @@ def test_argument_errors(ctx, oracle):
     with pytest.raises(ValueError):
         idx.search(np.ones((2, 5), np.float32), 3)
     with pytest.raises(ValueError):
-        ctx.cagra_index(np.ones((10, 1025), np.float32), g)
+        ctx.cagra_index(np.ones((10, 8193), np.float32), g)
     with pytest.raises(ValueError):
         ctx.cagra_index(base, g, np.array([10], np.uint32))
     with pytest.raises(ValueError):
