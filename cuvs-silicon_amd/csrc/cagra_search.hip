@@ -541,6 +541,9 @@ template <int E, bool F16>
 void launch_search(int waves, bool big, dim3 grid, size_t lds, hipStream_t stream, const SearchArgs& a,
                    hipEvent_t e0, hipEvent_t e1) {
   if (big) {  // d > 1024: four waves per query at any batch size
+    if (lds > 64 * 1024)
+      CVS_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(cagra_search_kernel<E, 4, F16, true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
     hipExtLaunchKernelGGL((cagra_search_kernel<E, 4, F16, true>), grid, dim3(256), lds, stream, e0, e1, 0, a);
     return;
   }

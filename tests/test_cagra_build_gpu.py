@@ -95,6 +95,20 @@ def test_neighbour_quality_on_offset_data(ctx, oracle, offset_norm):
     assert share > 0.9
 
 
+def test_build_wide_rows(ctx, oracle):
+    """d = 1536: the build's fp16 rows, Gram tiles and joins over more than
+    1,024 columns."""
+    rng = np.random.default_rng(15)
+    n, d = 4000, 1536
+    base = clustered(rng, n, d)
+    graph, _ = ctx.cagra_build(base, intermediate_degree=64, graph_degree=32, max_iterations=20)
+    check_graph(graph, n, 32)
+    exact = oracle.knn_graph(base, 10, threads=16)
+    share = np.mean([len(set(exact[i].tolist()) & set(graph[i].tolist())) / 10 for i in range(n)])
+    print(f"d=1536: share of exact 10-NN in the built lists: {share:.4f}")
+    assert share > 0.9
+
+
 @pytest.mark.parametrize("iters", [0, 1, 2, 3])
 def test_iteration_limits(ctx, oracle, iters):
     """The join's locality order is made after the first nn-descent

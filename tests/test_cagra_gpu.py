@@ -116,6 +116,52 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width, bits):
     assert recall(nbr, gt, k) > 0.8
 
 
+@pytest.mark.parametrize("d,bits,width", [(1536, 32, 1), (1536, 16, 1), (3072, 32, 4), (3072, 16, 1), (8192, 16, 1)])
+def test_wide_rows(ctx, oracle, d, bits, width):
+    """Rows wider than 1,024 columns: the query slice lives in LDS and rows
+    are gathered in chunks of 1,024 columns (the reference's search takes any
+    d, shaders/cagra_kernels.metal:117-132)."""
+    rng = np.random.default_rng(d + bits)
+    n, g, itopk = 3000, 32, 64
+    centers = rng.standard_normal((16, d)).astype(np.float32)
+    base = centers[rng.integers(0, 16, n)] + 0.5 * rng.standard_normal((n, d)).astype(np.float32)
+    qs = centers[rng.integers(0, 16, 100)] + 0.5 * rng.standard_normal((100, d)).astype(np.float32)
+    graph = oracle.knn_graph(base, g, threads=16)
+    nav = oracle.cagra_nav_nodes(n)
+    k = 10
+    gt, _ = oracle.bf_exact(base, qs, k, threads=16)
+    ref_nbr, _ = oracle.cagra_reference_search(base, graph, nav, qs, k, itopk_size=itopk, threads=16)
+    idx = ctx.cagra_index(base, graph, nav, traversal_bits=bits)
+    nbr, dist = idx.search(qs, k, itopk_size=itopk, search_width=width)
+    check_invariants(base, qs, nbr, dist, rtol=1e-4)
+    assert_recall_not_below(nbr, ref_nbr, gt, k, f"d={d} {bits}-bit width {width}")
+    tn, td = idx.search_teams(qs, k, teams=4, itopk_size=32)
+    check_invariants(base, qs, tn, td, rtol=1e-4)
+    if d == 1536:
+        e = idx.edge_distances()
+        np.testing.assert_allclose(e, oracle.edge_distances(base, graph, threads=16), rtol=1e-4)
+    idx.close()
+
+
+def test_wide_rows_reference_mode_equals_oracle(ctx, oracle):
+    """The reference's beam search at d = 2048 on integer rows: equal to the
+    oracle query by query."""
+    rng = np.random.default_rng(8)
+    n, d, g = 4000, 2048, 24
+    base = rng.integers(-3, 4, (n, d)).astype(np.float32)
+    qs = rng.integers(-3, 4, (60, d)).astype(np.float32)
+    graph = rng.integers(0, n, (n, g)).astype(np.uint32)
+    nav = oracle.cagra_nav_nodes(n)
+    idx = ctx.cagra_index(base, graph, nav)
+    entry = idx.entry_points(qs)
+    np.testing.assert_array_equal(entry, oracle.cagra_entry_points(qs, nav, base[nav]))
+    gn, gd = idx.search_reference(qs, 10, 64, 100, entry)
+    idx.close()
+    rn, rd = oracle.cagra_search(base, graph, qs, 10, 64, 100, entry, threads=16)
+    np.testing.assert_array_equal(gn, rn)
+    np.testing.assert_array_equal(gd, rd)
+
+
 @pytest.mark.parametrize("offset_norm", [100.0, 300.0])
 def test_fp16_traversal_on_offset_data(ctx, oracle, offset_norm):
     """Rows and queries shifted by a common offset: the fp16 traversal copy
