@@ -554,6 +554,8 @@ def leg_c4(cvs, ctx, args) -> dict:
     dn = cvs.DeviceArray(ctx, (q, k), np.uint32)
     dd = cvs.DeviceArray(ctx, (q, k), np.float32)
     st = cvs.DeviceArray(ctx, (q, 2), np.uint32)
+    cap = 8192
+    rec = cvs.DeviceArray(ctx, (q, cap), np.uint32)
     widths = []
     for width in (1, 4):
         stepf = lambda: idx.search_async(dq, k, dn, dd, itopk_size=itopk, search_width=width)
@@ -564,19 +566,36 @@ def leg_c4(cvs, ctx, args) -> dict:
         nbr = dn.to_host()
         if width == 1:
             nbr_w1 = nbr
-        idx.search_async(dq, k, dn, dd, itopk_size=itopk, search_width=width, stats=st)
+        # The same search once more, recording every query's evaluated rows,
+        # then those row gathers replayed alone: the time the search's data
+        # movement takes without the search (the roofline's denominator).
+        idx.search_record_async(dq, k, dn, dd, st, rec, itopk_size=itopk, search_width=width)
         stats = st.to_host().astype(np.int64)
+        replay_ms = idx.replay_gathers(rec, st, 32, reps=5)
         alg = float((stats[:, 0] * d * 4 + stats[:, 1] * width * degree * 4 + d * 4).sum())
+        gathered = float(np.minimum(stats[:, 0], cap).sum() * d * 4)
         traffic = read_traffic(f"cagra_search_n100k_d1024_q10000_itopk64_fp32_w{width}_traffic.txt")
         kms = kt["cagra_search"]
         ent = {"search_width": width, "qps": q / dt, "ms_per_batch": 1e3 * dt, "kernel_ms": kms,
                "recall_at_10": recall_at_k(nbr, gt_i, k),
                "mean_distance_evaluations": float(stats[:, 0].mean()),
-               "algorithmic_bytes_per_batch": alg, "algorithmic_frac": alg / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+               "max_distance_evaluations": int(stats[:, 0].max()),
+               "roofline": {"bound": "row gathers", "unit": "GB/s",
+                            "achieved": gathered / (kms * 1e-3) / 1e9,
+                            "peak": gathered / (replay_ms * 1e-3) / 1e9,
+                            "frac": replay_ms / kms,
+                            "peak_is": "the same rows gathered alone, same row shape, no search work "
+                                       "(cvs_cagra_replay_gathers), measured in this run",
+                            "gathered_bytes_per_batch": gathered, "replay_ms": replay_ms},
+               "algorithmic_bytes_per_batch": alg,
+               "algorithmic_rate_over_hbm_peak": alg / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         if traffic:
-            ent["hbm_traffic_bytes_per_batch"] = traffic
-            ent["hbm_frac"] = traffic / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS
+            # L2 -> memory-side fetches (FETCH_SIZE); on this device they
+            # include Infinity Cache hits, which no exposed counter separates.
+            ent["memory_side_bytes_per_batch"] = traffic
+            ent["memory_side_rate_over_hbm_peak"] = traffic / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS
         widths.append(ent)
+    rec.free()
     # Q=1: 100 single-query calls, launch to results on the device.
     dn1 = cvs.DeviceArray(ctx, (1, k), np.uint32)
     dd1 = cvs.DeviceArray(ctx, (1, k), np.float32)
@@ -636,6 +655,7 @@ def run_bf_large(args) -> int:
         ds.bf_search_async(dq, k, dn, dd)
     ctx.synchronize()
     steps = max(2, args.steps // 50)
+    ctx.bf_escalations(reset=True)
     t0 = time.perf_counter()
     for _ in range(steps):
         ds.bf_search_async(dq, k, dn, dd)
@@ -647,6 +667,7 @@ def run_bf_large(args) -> int:
     ctx.synchronize()
     kt = {name: ctx.kernel_time(name) for name in ("bf_prep", "bf_sample", "bf_scan", "bf_merge")}
     ctx.set_timing(False)
+    escalated, rescanned = ctx.bf_escalations(reset=True)
     kavg = {kn: v[0] / max(v[1], 1) for kn, v in kt.items()}
     flops = 2.0 * q * n * d
     nbr = dn.to_host()
@@ -665,6 +686,7 @@ def run_bf_large(args) -> int:
                      "frac": flops / (kavg["bf_scan"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
                      "step_frac": flops / dt / 1e12 / MFMA_F16_PEAK_TFLOPS},
         "recall_at_100_sampled": rec,
+        "uncertified_queries": {"escalated": escalated, "rescanned_all_rows": rescanned, "of": 2 * steps * q},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(base, qs, k, 4)
@@ -721,8 +743,14 @@ def run_cagra_search(args) -> int:
         idx.search_async(dq, k, dn, dd, itopk_size=args.itopk, search_width=width, stats=st)
         kms, _ = ctx.kernel_time("cagra_search")
         ctx.set_timing(False)
-        stats = st.to_host().astype(np.int64)
         nbr = dn.to_host()
+        # The evaluated rows recorded, then their gathers replayed alone.
+        rec = cvs.DeviceArray(ctx, (q, 8192), np.uint32)
+        idx.search_record_async(dq, k, dn, dd, st, rec, itopk_size=args.itopk, search_width=width)
+        replay_ms = idx.replay_gathers(rec, st, bits, reps=5)
+        rec.free()
+        stats = st.to_host().astype(np.int64)
+        gathered = float(np.minimum(stats[:, 0], 8192).sum() * d * (bits // 8))
         if width == 1 and bits == 16:
             nbr_w1 = nbr.copy()
         # algorithmic bytes per query: distance evaluations x D x (2 for the
@@ -758,16 +786,19 @@ def run_cagra_search(args) -> int:
             "q1_latency_ms_p99": 1e3 * lat[98], "q1_kernel_ms": k1ms / max(k1n, 1), "q1_recall_at_10": hits / 1000,
             "mean_distance_evaluations": float(stats[:, 0].mean()), "mean_iterations": float(stats[:, 1].mean()),
             "algorithmic_bytes_per_batch": alg_bytes, "algorithmic_gbs": alg_bytes / (kms * 1e-3) / 1e9,
-            "algorithmic_frac": alg_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_rate_over_hbm_peak": alg_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "roofline": {"bound": "row gathers", "unit": "GB/s", "achieved": gathered / (kms * 1e-3) / 1e9,
+                         "peak": gathered / (replay_ms * 1e-3) / 1e9, "frac": replay_ms / kms,
+                         "peak_is": "the same rows gathered alone (cvs_cagra_replay_gathers)",
+                         "replay_ms": replay_ms},
         }
-        # Rows revisited within a query or shared by concurrent queries come
-        # from L2 / MALL, so the HBM rate is taken from the committed counter
-        # profile of this kernel (bytes per launch).
+        # L2 -> memory-side fetches from the committed counter profile of this
+        # kernel; they include Infinity Cache hits (no exposed counter
+        # separates them from HBM reads).
         traffic = read_traffic(f"cagra_search_n100k_d1024_q10000_itopk64_fp{bits}_w{width}_traffic.txt")
         if traffic:
-            res["hbm_traffic_bytes_per_batch"] = traffic
-            res["hbm_gbs"] = traffic / (kms * 1e-3) / 1e9
-            res["hbm_frac"] = traffic / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS
+            res["memory_side_bytes_per_batch"] = traffic
+            res["memory_side_gbs"] = traffic / (kms * 1e-3) / 1e9
         log(json.dumps(res))
         results.append(res)
     # Q=1 latency of multi-team search (teams x per-team list, fp16 traversal)

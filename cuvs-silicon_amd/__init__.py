@@ -121,6 +121,12 @@ _SIGNATURES["cvs_cagra_search_reference"] = (c_int, [c_void_p, c_void_p, c_void_
                                                      c_uint32, c_void_p, c_void_p, c_void_p])
 _SIGNATURES["cvs_cagra_search_reference_async"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32,
                                                            c_uint32, c_void_p, c_void_p, c_void_p])
+_SIGNATURES["cvs_calibrate_gather_read"] = (c_int, [c_void_p, c_size_t, c_int64, c_int, c_int, c_int, POINTER(c_double)])
+_SIGNATURES["cvs_cagra_search_record_async"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32,
+                                                        c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                        c_uint32])
+_SIGNATURES["cvs_cagra_replay_gathers"] = (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_int64, c_int,
+                                                   c_int, POINTER(c_double)])
 _SIGNATURES["cvs_context_bf_escalations"] = (c_int, [c_void_p, POINTER(c_uint64), POINTER(c_uint64), c_int])
 
 # The bucketing permutation seed of the reference (src/metal_context.mm:803).
@@ -279,6 +285,15 @@ class Context:
         """Achievable streaming-read rate in GB/s (C: cvs_calibrate_stream_read)."""
         gbs = c_double(0)
         _check(load().cvs_calibrate_stream_read(self.handle, int(nbytes), int(workgroups), int(reps), byref(gbs)))
+        return gbs.value
+
+    def calibrate_gather_read(self, row_bytes: int, n_rows: int, workgroups: int, rows_per_team: int,
+                              reps: int = 10) -> float:
+        """Achievable rate of random whole-row gathers in GB/s (C:
+        cvs_calibrate_gather_read)."""
+        gbs = c_double(0)
+        _check(load().cvs_calibrate_gather_read(self.handle, int(row_bytes), int(n_rows), int(workgroups),
+                                                int(rows_per_team), int(reps), byref(gbs)))
         return gbs.value
 
     def set_timing(self, enable: bool) -> None:
@@ -466,6 +481,23 @@ class CagraIndex:
         _check(load().cvs_cagra_index_edge_distances(self.ctx.handle, self.handle,
                                                      host.ctypes.data_as(c_void_p), 0))
         return host
+
+    def search_record_async(self, queries: DeviceArray, k: int, nbr: DeviceArray, dist: DeviceArray,
+                            stats: DeviceArray, record: DeviceArray, itopk_size: int = 64, search_width: int = 1,
+                            max_iterations: int = 0) -> None:
+        """search_async that also records each query's evaluated row ids
+        (C: cvs_cagra_search_record_async); record is (q, cap) uint32."""
+        _check(load().cvs_cagra_search_record_async(self.ctx.handle, self.handle, queries.ptr, queries.shape[0],
+                                                    int(k), int(itopk_size), int(search_width), int(max_iterations),
+                                                    nbr.ptr, dist.ptr, stats.ptr, record.ptr, record.shape[1]))
+
+    def replay_gathers(self, record: DeviceArray, stats: DeviceArray, bits: int, reps: int = 5) -> float:
+        """Mean ms of gathering the recorded rows alone (C:
+        cvs_cagra_replay_gathers)."""
+        ms = c_double(0)
+        _check(load().cvs_cagra_replay_gathers(self.ctx.handle, self.handle, record.ptr, record.shape[1], stats.ptr,
+                                               record.shape[0], int(bits), int(reps), byref(ms)))
+        return ms.value
 
     def entry_points(self, queries) -> np.ndarray:
         """Per-query entry node: the nearest seed (navigation) node, as the

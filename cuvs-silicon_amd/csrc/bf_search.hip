@@ -726,12 +726,16 @@ __device__ __forceinline__ uint64_t key_at(const uint64_t (&v)[E], int p) {
 // certificate, and if needed the escalation described above; writes k
 // sorted results.  t_cert: the bound T above (key units); t_star: the
 // smallest list threshold; part / kp / stride: the candidate lists (entry e
-// of the query's lists at part[(e / kp) * stride + e % kp], G * kp entries).
+// of the query's lists at part[(e / kp) * stride + e % kp], G * kp entries);
+// key_r: the largest fp16 key among the candidates, which are the R smallest
+// keys of the lists, so an escalation from the lists continues with the keys
+// above it; 0 when the candidates are not known to be those (the escalation
+// then starts afresh).
 template <int E>
-__device__ void finish_query(const uint32_t* s_cid, int R, float t_cert, float t_star, const uint64_t* part, int G,
-                             int kp, int stride, const float* __restrict__ rows, int64_t n, int64_t d,
-                             const float* __restrict__ qv, int64_t q, int64_t k, const Cert& cert,
-                             uint32_t* out_nbr, float* out_dist) {
+__device__ void finish_query(const uint32_t* s_cid, int R, float t_cert, float t_star, uint64_t key_r,
+                             const uint64_t* part, int G, int kp, int stride, const float* __restrict__ rows,
+                             int64_t n, int64_t d, const float* __restrict__ qv, int64_t q, int64_t k,
+                             const Cert& cert, uint32_t* out_nbr, float* out_dist) {
   __shared__ uint64_t s_key[64 * E > 256 ? 64 * E : 256];  // exact keys: candidates, then per-wave rounds
   __shared__ uint32_t s_wid[kWaves][64];
   __shared__ uint64_t s_scr[32];
@@ -806,18 +810,24 @@ __device__ void finish_query(const uint32_t* s_cid, int R, float t_cert, float t
   }
 
   // 3. Escalation: exact keys of every row with a key up to T_need (from the
-  // lists) or of every row, 64 per wave and round, merged by wave 0 into its
-  // running exact top-128 (k <= 112 here).
+  // lists; those above key_r when the candidates were the lists' R smallest,
+  // whose exact keys seed the running list) or of every row, 64 per wave and
+  // round, merged by wave 0 into its running exact top-128 (k <= 112 here).
   const float tneed = s_tneed;
+  const bool incremental = mode == kCertKeys && key_r != 0;
   const int64_t total = mode == kCertKeys ? int64_t(G) * kp : n;
   uint64_t run[2] = {kSentinel, kSentinel};
+  if (incremental && wave == 0) {
+    run[0] = fin[0];
+    if constexpr (E > 1) run[1] = fin[1];
+  }
   for (int64_t base = 0; base < total; base += 64 * kWaves) {
     const int64_t pos = base + 64 * wave + lane;
     uint32_t id = 0xffffffffu;
     bool ok = false;
     if (mode == kCertKeys) {
       const uint64_t key = pos < total ? part[(pos / kp) * stride + pos % kp] : kSentinel;
-      ok = key != kSentinel && unord_f32(uint32_t(key >> 32)) <= tneed;
+      ok = key != kSentinel && unord_f32(uint32_t(key >> 32)) <= tneed && (!incremental || key > key_r);
       id = uint32_t(key);
     } else {
       ok = pos < n;
@@ -844,7 +854,7 @@ __device__ void finish_query(const uint32_t* s_cid, int R, float t_cert, float t
 
 // ---------------------------------------------------------------------------
 // Merge for kp <= 64, one workgroup (4 waves) per query.
-//  1. The R-th smallest list minimum (R = min(2 kp, 64)) bounds the R-th
+//  1. The R-th smallest list minimum (R = min(2 kp, 64 E)) bounds the R-th
 //     smallest key (R list minima are R distinct keys): only keys at or
 //     below it can be among the R smallest.  Wave 0 computes it (a 256-key
 //     wave sort) and the smallest list threshold T* while every wave's first
@@ -854,9 +864,10 @@ __device__ void finish_query(const uint32_t* s_cid, int R, float t_cert, float t
 //     G * kp keys and append the passing ones to an LDS buffer of that size
 //     (one atomic per wave and batch).
 //  3. Wave 0 sorts the passing keys 64 at a time and merges them into its
-//     running sorted top-64; its first R ids are finished (re-ranked,
+//     running sorted top-64 E; its first R ids are finished (re-ranked,
 //     certified) by finish_query.
 // ---------------------------------------------------------------------------
+template <int E>
 __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __restrict__ part,
                                                               const uint64_t* __restrict__ lmin,
                                                               const float* __restrict__ lcut, int G, int kp,
@@ -865,17 +876,17 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
                                                               Cert cert, uint32_t* __restrict__ out_nbr,
                                                               float* __restrict__ out_dist) {
   constexpr int kBatch = 16;        // keys per thread and batch
-  constexpr int kMaxPass = 64 * 64; // R * kp for R, kp <= 64
+  constexpr int kMaxPass = 64 * 64; // passing keys held in LDS
   __shared__ uint64_t s_pass[kMaxPass];
   __shared__ uint32_t s_npass;
-  __shared__ uint64_t s_bound;
+  __shared__ uint64_t s_bound, s_keyr;
   __shared__ float s_tcert, s_tstar;
-  __shared__ uint32_t s_cid[64];
+  __shared__ uint32_t s_cid[64 * E];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t q = blockIdx.x;
   const uint64_t* src = part + q * int64_t(G) * kp;
   const int total = G * kp;
-  const int R = 2 * kp < 64 ? 2 * kp : 64;
+  const int R = 2 * kp < 64 * E ? 2 * kp : 64 * E;
   if (tid == 0) s_npass = 0;
 
   // First batch of keys, requested before the bound is known.
@@ -930,35 +941,49 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
   }
   __syncthreads();
 
-  // 3. Wave 0: top-R of the passing keys.
+  // 3. Wave 0: top-R of the passing keys.  Should more keys pass than LDS
+  // holds (not seen in practice), the candidates are not known to be the R
+  // smallest: the certificate is then made to fail, and the escalation
+  // re-ranks from the lists afresh.
   if (wave == 0) {
-    const int np = s_npass < uint32_t(kMaxPass) ? int(s_npass) : kMaxPass;
-    uint64_t run[1] = {kSentinel};
+    const bool overflow = s_npass > uint32_t(kMaxPass);
+    const int np = overflow ? kMaxPass : int(s_npass);
+    uint64_t run[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) run[e] = kSentinel;
     for (int r0 = 0; r0 < np; r0 += 64) {
       uint64_t ck[1] = {r0 + lane < np ? s_pass[r0 + lane] : kSentinel};
       wave_sort_e<1>(ck);
-      wave_merge<1>(run, ck[0]);
+      wave_merge<E>(run, ck[0]);
     }
-    s_cid[lane] = (lane < R && run[0] != kSentinel) ? uint32_t(run[0]) : 0xffffffffu;
-    const uint64_t kr = key_at<1>(run, R - 1);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int pos = e * 64 + lane;
+      s_cid[pos] = (pos < R && run[e] != kSentinel) ? uint32_t(run[e]) : 0xffffffffu;
+    }
+    const uint64_t kr = key_at<E>(run, R - 1);
     const float tr = kr == kSentinel ? INFINITY : unord_f32(uint32_t(kr >> 32));
-    if (lane == 0) s_tcert = fminf(tr, s_tstar);
+    if (lane == 0) {
+      s_tcert = overflow ? 0.f : fminf(tr, s_tstar);
+      s_keyr = overflow ? 0ull : kr;
+    }
   }
   __syncthreads();
-  finish_query<1>(s_cid, R, s_tcert, s_tstar, src, G, kp, kp, rows, n, d, queries + q * d, q, k, cert, out_nbr,
-                  out_dist);
+  finish_query<E>(s_cid, R, s_tcert, s_tstar, s_keyr, src, G, kp, kp, rows, n, d, queries + q * d, q, k, cert,
+                  out_nbr, out_dist);
 }
 
 // ---------------------------------------------------------------------------
-// Merge for kp = 128 (global lists), one workgroup (4 waves) per query.
-//  1. The kp-th smallest list minimum bounds the kp-th smallest key (kp list
-//     minima are kp distinct keys): only keys at or below it can be among
-//     the kp smallest.  Each wave computes it (a 256-key wave sort).
+// Merge for kp = 128 (global lists), one workgroup (4 waves) per query; the
+// R = 64 E smallest keys are the candidates.
+//  1. The R-th smallest list minimum bounds the R-th smallest key (R list
+//     minima are R distinct keys): only keys at or below it can be among
+//     the R smallest.  Each wave computes it (a 256-key wave sort).
 //  2. Each wave streams a quarter of the lists, 64 keys per row, all rows of
 //     a batch loaded at once; a row holding a key within the bound is sorted
 //     (wave bitonic) and merged into the wave's running sorted top-64*E,
-//     whose kp-th key then tightens the wave's bound.
-//  3. Wave 0 merges the four running lists; the kp candidates are finished
+//     whose R-th key then tightens the wave's bound.
+//  3. Wave 0 merges the four running lists; the R candidates are finished
 //     (re-ranked, certified) by finish_query.
 // ---------------------------------------------------------------------------
 template <int E>
@@ -973,8 +998,10 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
   __shared__ uint64_t s_run[kWaves][64 * E];
   __shared__ uint32_t s_cid[64 * E];
   __shared__ float s_tcert;
+  __shared__ uint64_t s_keyr;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t q = blockIdx.x;
+  constexpr int R = 64 * E;  // candidates re-ranked (>= kp)
 
   // 1. Bound from the list minima (G <= 256), and the smallest list threshold.
   uint64_t mins[4];
@@ -988,7 +1015,7 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) cut = fminf(cut, xor_lanes_f(cut, o));
   wave_sort_e<4>(mins);
-  uint64_t bound = key_at<4>(mins, kp - 1);
+  uint64_t bound = key_at<4>(mins, R - 1);
 
   // 2. This wave's quarter of the 64-key rows.
   uint64_t run[E];
@@ -1012,7 +1039,7 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
       uint64_t ck[1] = {pass ? key[r] : kSentinel};
       wave_sort_e<1>(ck);
       wave_merge<E>(run, ck[0]);
-      const uint64_t kth = key_at<E>(run, kp - 1);
+      const uint64_t kth = key_at<E>(run, R - 1);
       bound = kth < bound ? kth : bound;
     }
   }
@@ -1029,15 +1056,18 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int pos = e * 64 + lane;
-      s_cid[pos] = (pos < kp && run[e] != kSentinel) ? uint32_t(run[e]) : 0xffffffffu;
+      s_cid[pos] = run[e] != kSentinel ? uint32_t(run[e]) : 0xffffffffu;
     }
-    const uint64_t kr = key_at<E>(run, kp - 1);
+    const uint64_t kr = key_at<E>(run, R - 1);
     const float tr = kr == kSentinel ? INFINITY : unord_f32(uint32_t(kr >> 32));
-    if (lane == 0) s_tcert = fminf(tr, cut);
+    if (lane == 0) {
+      s_tcert = fminf(tr, cut);
+      s_keyr = kr;
+    }
   }
   __syncthreads();
-  finish_query<E>(s_cid, kp, s_tcert, cut, src, G, kp, stride, rows, n, d, queries + q * d, q, k, cert, out_nbr,
-                  out_dist);
+  finish_query<E>(s_cid, R, s_tcert, cut, s_keyr, src, G, kp, stride, rows, n, d, queries + q * d, q, k, cert,
+                  out_nbr, out_dist);
 }
 
 // ---------------------------------------------------------------------------
@@ -1187,7 +1217,7 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   // large share of the rows (small n), r is raised towards R; at n = 1M the
   // rank is ~kp * 61 already and r stays kp.
   {
-    const int R = p.kp > 64 ? p.kp : std::min(2 * p.kp, 64);
+    const int R = p.kp > 64 ? 2 * p.kp : std::min(2 * p.kp, 128);
     const int64_t sampled = p.s_units * rpu;
     const int64_t want = (int64_t(R) * sampled + ds->n - 1) / ds->n;
     p.sel_rank = int(std::max<int64_t>(p.kp, std::min<int64_t>(R, want)));
@@ -1285,13 +1315,23 @@ void bf_launch(cvs_context* ctx, const cvs_dataset* ds, const BfPlan& p, const f
 
   const Cert cert = make_cert(ctx, ds, qnorms, qerr);
   const TimerSpan t3 = timed ? timer_span(ctx, "bf_merge") : TimerSpan{};
-  if (kp <= 64)
-    hipExtLaunchKernelGGL(bf_merge_filter_kernel, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
+  // Candidates re-ranked per query: 2 kp up to 128 (32 for k <= 10, 64 for
+  // k <= 24, 128 for k <= 48), 256 for kp = 128 (k <= 112).  The rank gap
+  // between the k-th result and the last candidate is what lets the
+  // certificate pass: on the benchmark's distribution at N = 1M, 16
+  // candidates for k = 10 or 128 for k = 100 leave most queries uncertified.
+  if (kp <= 32)
+    hipExtLaunchKernelGGL(bf_merge_filter_kernel<1>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
+                          t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin),
+                          static_cast<const float*>(lcut), G, kp, static_cast<const float*>(ds->rows), ds->n, ds->d,
+                          queries, k, cert, nbr, dist);
+  else if (kp <= 64)
+    hipExtLaunchKernelGGL(bf_merge_filter_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start,
                           t3.stop, 0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin),
                           static_cast<const float*>(lcut), G, kp, static_cast<const float*>(ds->rows), ds->n, ds->d,
                           queries, k, cert, nbr, dist);
   else
-    hipExtLaunchKernelGGL(bf_merge_kernel<2>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start, t3.stop,
+    hipExtLaunchKernelGGL(bf_merge_kernel<4>, dim3(unsigned(q)), dim3(kThreads), 0, ctx->stream, t3.start, t3.stop,
                           0, static_cast<const uint64_t*>(part), static_cast<const uint64_t*>(lmin),
                           static_cast<const float*>(lcut), G, kp, p.stride, static_cast<const float*>(ds->rows), ds->n,
                           ds->d, queries, k, cert, nbr, dist);

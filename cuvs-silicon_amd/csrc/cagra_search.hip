@@ -90,6 +90,8 @@ struct SearchArgs {
   int bitmap_words;     // > 0: the visited set is a bitmap of this many words (n bits, rounded up)
   int teams;            // workgroups per query (block b = query b / teams, team b % teams)
   uint64_t* team_keys;  // teams > 1: (q * teams) x itopk list keys, merged afterwards
+  uint32_t* record;     // or null: the ids of each query's distance evaluations, in order,
+  int record_cap;       // the first record_cap of them per query (q x record_cap)
 };
 
 // Merges 64 sorted keys `c` (one per lane) into the sorted list `top` of
@@ -377,6 +379,10 @@ __global__ __launch_bounds__(64 * W) void cagra_search_kernel(SearchArgs a) {
       const uint64_t m = __ballot(fresh);
       if (fresh) s_ids[mbcnt(m)] = id;
       if (lane == 0) *s_nf = uint32_t(popc(m));
+      if (a.record && fresh) {
+        const uint32_t pos = evals + uint32_t(mbcnt(m));
+        if (pos < uint32_t(a.record_cap)) a.record[qi * a.record_cap + pos] = id;
+      }
     }
     __syncthreads();
     const int nf = int(*s_nf);
@@ -686,6 +692,40 @@ __global__ __launch_bounds__(256) void edge_distances_kernel(const float4* __res
   }
 }
 
+// Gathers, for every query, the rows its search evaluated (recorded by
+// cvs_cagra_search_record_async), with the search's row shape and no search
+// work: one workgroup per query, 16 teams of 16 lanes, lane l reading the
+// 16-byte pieces l, l + 16, ... of a row (256 contiguous bytes per team and
+// load), two rows in flight per team.  The time of this launch is the
+// search's data movement alone.
+__global__ __launch_bounds__(256) void gather_replay_kernel(const uint4* __restrict__ rows, int row_vecs,
+                                                            const uint32_t* __restrict__ record, int cap,
+                                                            const uint32_t* __restrict__ stats,
+                                                            uint32_t* __restrict__ sink) {
+  const int64_t qi = blockIdx.x;
+  const int team = threadIdx.x >> 4, tp = threadIdx.x & 15;
+  const uint32_t ev = stats[2 * qi];
+  const int cnt = int(ev < uint32_t(cap) ? ev : uint32_t(cap));
+  const uint32_t* ids = record + qi * cap;
+  uint32_t acc = 0;
+  for (int i = team; i < cnt; i += 32) {
+    const uint4* r0 = rows + int64_t(ids[i]) * row_vecs + tp;
+    const uint4* r1 = rows + int64_t(ids[i + 16 < cnt ? i + 16 : i]) * row_vecs + tp;
+    for (int c0 = 0; c0 < row_vecs; c0 += 256) {
+      uint4 v0[16], v1[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int c = c0 + tp + 16 * j;
+        v0[j] = c < row_vecs ? r0[c0 + 16 * j] : uint4{0, 0, 0, 0};
+        v1[j] = (c < row_vecs && i + 16 < cnt) ? r1[c0 + 16 * j] : uint4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc ^= v0[j].x ^ v0[j].w ^ v1[j].y ^ v1[j].z;
+    }
+  }
+  if (acc == 0x9E3779B9u) sink[qi * 256 + threadIdx.x] = acc;
+}
+
 int ceil_log2(int64_t v) {
   int b = 0;
   while ((int64_t(1) << b) < v) ++b;
@@ -694,7 +734,8 @@ int ceil_log2(int64_t v) {
 
 void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const float* queries,
                          int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
-                         uint32_t max_iterations, uint32_t* nbr, float* dist, uint32_t* stats, int teams = 1) {
+                         uint32_t max_iterations, uint32_t* nbr, float* dist, uint32_t* stats, int teams = 1,
+                         uint32_t* record = nullptr, int record_cap = 0) {
   if (!idx || idx->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
   if (!queries || !nbr || !dist) fail(CVS_ERR_INVALID_ARGUMENT, "null buffer");
   if (q <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "query count must be positive");
@@ -764,6 +805,8 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   a.hash_bits = hash_bits;
   a.bitmap_words = use_bitmap ? int(bitmap_words) : 0;
   a.teams = teams;
+  a.record = teams == 1 ? record : nullptr;
+  a.record_cap = record_cap;
   if (teams > 1) {
     ctx->ws_teams.reserve(size_t(q) * size_t(teams) * size_t(itopk) * sizeof(uint64_t));
     a.team_keys = ctx->ws_teams.as<uint64_t>();
@@ -948,6 +991,65 @@ int cvs_cagra_search_teams_async(cvs_context* ctx, const cvs_cagra_index* index,
     bind(ctx);
     cagra_search_device(ctx, index, queries_dev, q, k, itopk_size, search_width, max_iterations,
                         out_neighbors_dev, out_distances_dev, nullptr, int(std::min<uint32_t>(teams, 1u << 20)));
+  });
+}
+
+int cvs_cagra_search_record_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                                  int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                                  uint32_t max_iterations, uint32_t* out_neighbors_dev, float* out_distances_dev,
+                                  uint32_t* out_stats_dev, uint32_t* record_dev, uint32_t record_cap) {
+  return guarded([&] {
+    bind(ctx);
+    if (!record_dev || record_cap == 0 || !out_stats_dev)
+      fail(CVS_ERR_INVALID_ARGUMENT, "recording needs a record buffer, a positive capacity and stats");
+    if (record_cap > (1u << 20)) fail(CVS_ERR_UNSUPPORTED, "record_cap above 2^20");
+    cagra_search_device(ctx, index, queries_dev, q, k, itopk_size, search_width, max_iterations, out_neighbors_dev,
+                        out_distances_dev, out_stats_dev, 1, record_dev, int(record_cap));
+  });
+}
+
+int cvs_cagra_replay_gathers(cvs_context* ctx, const cvs_cagra_index* index, const uint32_t* record_dev,
+                             uint32_t record_cap, const uint32_t* stats_dev, int64_t q, int bits, int reps,
+                             double* out_ms) {
+  return guarded([&] {
+    bind(ctx);
+    if (!index || index->ctx != ctx) fail(CVS_ERR_INVALID_ARGUMENT, "index does not belong to context");
+    if (!record_dev || !stats_dev || !out_ms || record_cap == 0 || q <= 0 || reps < 1)
+      fail(CVS_ERR_INVALID_ARGUMENT, "bad replay arguments");
+    if (bits != 16 && bits != 32) fail(CVS_ERR_INVALID_ARGUMENT, "bits must be 16 or 32");
+    if (q > int64_t(INT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "too many queries");
+    const int row_vecs = int(index->dpad * (bits / 8) / 16);
+    const uint4* rows = bits == 16 ? static_cast<const uint4*>(index->rows16)
+                                   : reinterpret_cast<const uint4*>(index->rows);
+    void* sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto cleanup = [&] {
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+      if (sink) (void)hipFree(sink);
+    };
+    try {
+      CVS_HIP(hipMalloc(&sink, size_t(q) * 256 * sizeof(uint32_t)));
+      CVS_HIP(hipEventCreate(&e0));
+      CVS_HIP(hipEventCreate(&e1));
+      auto launch = [&] {
+        hipLaunchKernelGGL(gather_replay_kernel, dim3(unsigned(q)), dim3(256), 0, ctx->stream, rows, row_vecs,
+                           record_dev, int(record_cap), stats_dev, static_cast<uint32_t*>(sink));
+        after_launch("gather_replay_kernel");
+      };
+      launch();  // warm-up
+      CVS_HIP(hipEventRecord(e0, ctx->stream));
+      for (int i = 0; i < reps; ++i) launch();
+      CVS_HIP(hipEventRecord(e1, ctx->stream));
+      CVS_HIP(hipEventSynchronize(e1));
+      float ms = 0.f;
+      CVS_HIP(hipEventElapsedTime(&ms, e0, e1));
+      *out_ms = double(ms) / reps;
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
   });
 }
 

@@ -323,11 +323,100 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const stream_vec* __re
   if (acc == 0x9E3779B9u) sink[blockIdx.x * 256 + threadIdx.x] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Device calibration for gather-bound kernels (the graph search): each
+// 16-lane team of a workgroup reads whole rows of `row_bytes` at random,
+// lane l taking the 16-byte pieces l, l + 16, ... of a row (so one load
+// instruction of the team covers 256 contiguous bytes, as the search's row
+// gathers do), two rows in flight per team.  Rows are picked by a
+// multiplicative hash of (team, step) over n_rows rows, so the set of rows
+// read is spread uniformly over the buffer.  The XOR of the data decides a
+// store that never happens in practice but keeps every load.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gather_read_kernel(const stream_vec* __restrict__ buf, uint64_t n_rows,
+                                                          uint32_t row_vecs, uint32_t rows_per_team, uint32_t seed,
+                                                          uint32_t* __restrict__ sink) {
+  const uint32_t team = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const uint32_t tp = threadIdx.x & 15u;
+  uint32_t acc = 0;
+  auto row_of = [&](uint32_t i) -> uint64_t {
+    uint64_t h = (uint64_t(team) << 32 | i) * 0x9E3779B97F4A7C15ull + seed;
+    h ^= h >> 29;
+    h *= 0xBF58476D1CE4E5B9ull;
+    h ^= h >> 32;
+    return h % n_rows;
+  };
+  for (uint32_t i = 0; i < rows_per_team; i += 2) {
+    const stream_vec* r0 = buf + row_of(i) * row_vecs + tp;
+    const stream_vec* r1 = buf + row_of(i + 1) * row_vecs + tp;
+    stream_vec v0[16], v1[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t c = tp + 16u * uint32_t(j);
+      v0[j] = c < row_vecs ? r0[16 * j] : stream_vec{0, 0, 0, 0};
+      v1[j] = c < row_vecs ? r1[16 * j] : stream_vec{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc ^= v0[j].x ^ v0[j].w ^ v1[j].y ^ v1[j].z;
+  }
+  if (acc == 0x9E3779B9u) sink[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
 }  // namespace cvs
 
 using namespace cvs;
 
 extern "C" {
+
+int cvs_calibrate_gather_read(cvs_context* ctx, size_t row_bytes, int64_t n_rows, int workgroups, int rows_per_team,
+                              int reps, double* out_gbs) {
+  return guarded([&] {
+    bind(ctx);
+    if (!out_gbs) fail(CVS_ERR_INVALID_ARGUMENT, "null out_gbs");
+    if (row_bytes == 0 || row_bytes % 16 != 0 || row_bytes > 4096)
+      fail(CVS_ERR_INVALID_ARGUMENT, "row_bytes must be a multiple of 16 and at most 4096");
+    if (n_rows < 1 || workgroups < 1 || rows_per_team < 2 || reps < 1)
+      fail(CVS_ERR_INVALID_ARGUMENT, "n_rows, workgroups, reps positive; rows_per_team at least 2");
+    const size_t bytes = size_t(n_rows) * row_bytes;
+    void* buf = nullptr;
+    void* sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto cleanup = [&] {
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+      if (buf) (void)hipFree(buf);
+      if (sink) (void)hipFree(sink);
+    };
+    try {
+      CVS_HIP(hipMalloc(&buf, bytes));
+      CVS_HIP(hipMalloc(&sink, size_t(workgroups) * 256 * sizeof(uint32_t)));
+      CVS_HIP(hipMemsetAsync(buf, 0x5a, bytes, ctx->stream));
+      CVS_HIP(hipEventCreate(&e0));
+      CVS_HIP(hipEventCreate(&e1));
+      const uint32_t rpt = uint32_t(rows_per_team + (rows_per_team & 1));
+      auto launch = [&](uint32_t seed) {
+        hipLaunchKernelGGL(gather_read_kernel, dim3(unsigned(workgroups)), dim3(256), 0, ctx->stream,
+                           static_cast<const stream_vec*>(buf), uint64_t(n_rows), uint32_t(row_bytes / 16), rpt, seed,
+                           static_cast<uint32_t*>(sink));
+        after_launch("gather_read_kernel");
+      };
+      for (int i = 0; i < 2; ++i) launch(uint32_t(1000 + i));  // warm-up (fills the caches)
+      CVS_HIP(hipEventRecord(e0, ctx->stream));
+      for (int i = 0; i < reps; ++i) launch(uint32_t(i));
+      CVS_HIP(hipEventRecord(e1, ctx->stream));
+      CVS_HIP(hipEventSynchronize(e1));
+      float ms = 0.f;
+      CVS_HIP(hipEventElapsedTime(&ms, e0, e1));
+      const double gathered = double(workgroups) * 16.0 * double(rpt) * double(row_bytes) * reps;
+      *out_gbs = gathered / (double(ms) * 1e-3) / 1e9;
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
+  });
+}
+
 
 const char* cvs_last_error(void) { return g_last_error.c_str(); }
 uint64_t cvs_dispatch_count(void) { return g_dispatches.load(); }

@@ -119,6 +119,16 @@ int cvs_context_bf_escalations(cvs_context* ctx, uint64_t* escalated, uint64_t* 
 int cvs_calibrate_stream_read(cvs_context* ctx, size_t bytes, int workgroups, int reps,
                               double* out_gbs);
 
+/* Device calibration for gather-bound kernels; no counterpart in the
+ * reference.  Allocates n_rows rows of row_bytes (a multiple of 16, at most
+ * 4096), then `workgroups` workgroups of 16 teams of 16 lanes each read
+ * rows_per_team rows picked uniformly at random, one 256-byte segment per
+ * team and load instruction, two rows in flight per team (the graph search's
+ * gather shape), `reps` times after two warm-up passes; returns the rate of
+ * gathered bytes in GB/s.  Frees its buffer; synchronizes. */
+int cvs_calibrate_gather_read(cvs_context* ctx, size_t row_bytes, int64_t n_rows, int workgroups, int rows_per_team,
+                              int reps, double* out_gbs);
+
 /* ---- device memory helpers (device-resident benchmarking and tests) ----- */
 
 int cvs_device_alloc(cvs_context* ctx, size_t bytes, void** out_ptr);
@@ -293,6 +303,23 @@ int cvs_cagra_search_reference_async(cvs_context* ctx, const cvs_cagra_index* in
                                      int64_t q, int64_t k, uint32_t beam_size, uint32_t max_iter,
                                      const uint32_t* entry_nodes_dev, uint32_t* out_neighbors_dev,
                                      float* out_distances_dev);
+
+/* Measurement support for the graph search's roofline; no counterpart in
+ * the reference.  cvs_cagra_search_record_async is cvs_cagra_search_async
+ * (stats required) that also writes the ids of each query's distance
+ * evaluations, in order, the first record_cap of them per query, to
+ * record_dev (q x record_cap uint32, device).  cvs_cagra_replay_gathers then
+ * gathers exactly those rows (of the fp16 copy for bits = 16, the fp32 rows
+ * for 32) with the search's row shape and no search work, one workgroup per
+ * query, `reps` times after a warm-up, and returns the mean ms per replay:
+ * the time the search's data movement takes on its own. */
+int cvs_cagra_search_record_async(cvs_context* ctx, const cvs_cagra_index* index, const float* queries_dev,
+                                  int64_t q, int64_t k, uint32_t itopk_size, uint32_t search_width,
+                                  uint32_t max_iterations, uint32_t* out_neighbors_dev, float* out_distances_dev,
+                                  uint32_t* out_stats_dev, uint32_t* record_dev, uint32_t record_cap);
+int cvs_cagra_replay_gathers(cvs_context* ctx, const cvs_cagra_index* index, const uint32_t* record_dev,
+                             uint32_t record_cap, const uint32_t* stats_dev, int64_t q, int bits, int reps,
+                             double* out_ms);
 
 /* ---- CAGRA graph build --------------------------------------------------- */
 

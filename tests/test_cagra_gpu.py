@@ -371,3 +371,40 @@ def test_teams_argument_errors(ctx, oracle):
         idx.search_teams(q, 4, 65)
     with pytest.raises(ValueError):
         idx.search_teams(q, 4, 4, itopk_size=256)   # 4 x 256 > 512
+
+
+def test_search_record_and_replay(ctx, cvs, oracle):
+    """Recording the evaluated rows changes nothing in the search's output;
+    the record holds exactly `evaluations` distinct-per-visit valid ids per
+    query; the replay of those gathers runs and takes positive time."""
+    rng = np.random.default_rng(31)
+    n, d, g, q, k = 5000, 128, 32, 300, 10
+    base = rng.standard_normal((n, d)).astype(np.float32)
+    qs = rng.standard_normal((q, d)).astype(np.float32)
+    graph = oracle.knn_graph(base, g, threads=16)
+    idx = ctx.cagra_index(base, graph, oracle.cagra_nav_nodes(n))
+    dq = cvs.DeviceArray.from_host(ctx, qs)
+    dn = cvs.DeviceArray(ctx, (q, k), np.uint32)
+    dd = cvs.DeviceArray(ctx, (q, k), np.float32)
+    st = cvs.DeviceArray(ctx, (q, 2), np.uint32)
+    rec = cvs.DeviceArray(ctx, (q, 4096), np.uint32)
+    idx.search_async(dq, k, dn, dd, itopk_size=64, stats=st)
+    ctx.synchronize()
+    plain_n, plain_d, plain_st = dn.to_host(), dd.to_host(), st.to_host()
+    idx.search_record_async(dq, k, dn, dd, st, rec, itopk_size=64)
+    ctx.synchronize()
+    np.testing.assert_array_equal(dn.to_host(), plain_n)
+    np.testing.assert_array_equal(dd.to_host(), plain_d)
+    stats = st.to_host()
+    np.testing.assert_array_equal(stats, plain_st)
+    r = rec.to_host()
+    for i in range(q):
+        ev = int(stats[i, 0])
+        assert 0 < ev <= 4096
+        ids = r[i, :ev]
+        assert (ids < n).all()
+        assert set(plain_n[i].tolist()) <= set(ids.tolist())  # every result was evaluated
+    for bits in (32, 16):
+        idx.set_traversal(bits)
+        assert idx.replay_gathers(rec, st, bits, reps=2) > 0
+    idx.close()
