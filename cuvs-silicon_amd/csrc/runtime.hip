@@ -528,15 +528,22 @@ int cvs_context_kernel_time(cvs_context* ctx, const char* kernel, double* total_
     uint64_t cnt = 0;
     auto it = ctx->timers.find(kernel);
     if (it != ctx->timers.end()) {
-      for (auto& p : it->second.pending) {
+      // The pairs leave `pending` before any is read, so every event returns
+      // to the pool exactly once.  A pair whose launch failed after it was
+      // handed out was never recorded: its elapsed-time query fails, and the
+      // pair is skipped instead of ending the loop.
+      std::vector<std::pair<hipEvent_t, hipEvent_t>> pairs;
+      pairs.swap(it->second.pending);
+      for (auto& p : pairs) {
         float ms = 0.f;
-        CVS_HIP(hipEventElapsedTime(&ms, p.first, p.second));
-        sum += ms;
-        ++cnt;
+        if (hipEventElapsedTime(&ms, p.first, p.second) == hipSuccess) {
+          sum += ms;
+          ++cnt;
+        }
         it->second.pool.push_back(p.first);
         it->second.pool.push_back(p.second);
       }
-      it->second.pending.clear();
+      (void)hipGetLastError();  // a skipped pair's error is not this call's
     }
     *total_ms = sum;
     *launches = cnt;

@@ -177,16 +177,20 @@ int cvs_bf_search_async(cvs_context* ctx, const cvs_dataset* ds,
                         uint32_t* out_neighbors_dev, float* out_distances_dev);
 
 /* cvs_bf_search_async without any allocation, for d <= 1024 and k <= 112
- * (the fused scan): no counterpart in the reference.  For callers that cannot allocate device memory (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
- * workspace (query tiles, thresholds, sample minima, candidate lists) lives in
- * a 64 MiB array that the library holds on each device it runs on until the
- * process ends; a call whose workspace would exceed it fails with
- * CVS_ERR_UNSUPPORTED and a message giving the bytes needed (on 256
- * compute units at D = 1024, every q up to 7,936 fits for k <= 10, 935 for
- * k <= 24, 488 for k <= 48 and 332 for k <= 112).  Device pointers; enqueued on the context stream; no events.
- * Calls that overlap on one GPU (several contexts or threads on the same
- * device) share that array and race: serialise them. */
+ * (the fused scan): no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The workspace (query tiles,
+ * thresholds, sample minima, candidate lists) lives in a 64 MiB array that
+ * the library holds on each device it runs on until the process ends; a call
+ * whose workspace would exceed it fails with CVS_ERR_UNSUPPORTED and a
+ * message giving the bytes needed.  On 256 compute units at D = 1024 and at
+ * least 8,192 rows, batches of up to 1,024 queries (256 candidate lists per
+ * query) fit for k <= 10, up to 922 for k <= 24, 485 for k <= 48 and 331
+ * for k <= 112; larger batches (32 lists per query) fit up to 7,808 queries
+ * for k <= 10, 5,286 for k <= 24 and 3,212 for k <= 48.  Device pointers;
+ * enqueued on the context stream; no events.  Calls that overlap on one GPU
+ * (several contexts or threads on the same device) share that array and
+ * race: serialise them. */
 #define CVS_BF_NOALLOC_SCRATCH_BYTES (64u << 20)
 int cvs_bf_search_noalloc(cvs_context* ctx, const cvs_dataset* ds,
                           const float* queries_dev, int64_t q, int64_t k,

@@ -59,6 +59,24 @@ def test_noalloc_matches_allocating_entry_point(cvs, ctx, oracle, d, k):
         ds.close()
 
 
+@pytest.mark.parametrize("q", [2000, 7800])
+def test_noalloc_large_batch(cvs, ctx, q):
+    """Batches of more than 8 query blocks (the range-major launch and its
+    32 dataset ranges, the layout that sizes the scratch for k <= 10 at
+    D = 1024) through the scratch array, bit for bit against the allocating
+    entry point; 7,800 queries is near the largest batch that fits."""
+    print(f"[no-alloc] large batch q={q}", flush=True)
+    base = cvs.synth_clustered(29, cvs.STREAM_BASE, 30_000, 1024)
+    ds = ctx.dataset(base)
+    try:
+        queries = cvs.synth_clustered(31, cvs.STREAM_QUERIES, q, 1024)
+        (n_ref, d_ref), (n_na, d_na) = run_both(cvs, ctx, ds, queries, 10)
+        assert np.array_equal(n_na, n_ref)
+        assert np.array_equal(d_na.view(np.uint32), d_ref.view(np.uint32))
+    finally:
+        ds.close()
+
+
 def test_noalloc_rejects_oversized_call(cvs, ctx):
     print("[no-alloc] oversized", flush=True)
     base = cvs.synth_clustered(3, cvs.STREAM_BASE, 50_000, 1024)
