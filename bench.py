@@ -210,6 +210,9 @@ def main() -> int:
                          "degree 64; cagra-build: graph build at N=1M D=1024")
     ap.add_argument("--itopk", type=int, default=64)
     ap.add_argument("--degree", type=int, default=64)
+    ap.add_argument("--exact-lists", action="store_true",
+                    help="cagra-build: also prune exact k-NN lists of every row (brute force, the row itself "
+                         "excluded) at the build's intermediate degree and compare the two graphs")
     args = ap.parse_args()
 
     if args.calibrate_copy:
@@ -854,6 +857,90 @@ def run_cagra_search(args) -> int:
     return 0
 
 
+def exact_list_graph(cvs, ctx, drows, inter, nav, idx, qs, gt, k: int, kd: int, args) -> dict:
+    """The build's last phase (detour pruning, cvs_cagra_optimize) applied
+    to the exact kd nearest neighbours of every row instead of the
+    nn-descent lists: exact lists of width kd + 1 from the brute-force path
+    with the rows as queries (the row itself is dropped by the pruning), in
+    batches of 65,536 rows.  Reports the seconds of both steps, how many of
+    the exact kd neighbours the nn-descent lists hold (first 2,000 rows),
+    and recall@10 at itopk 64 to 512 of graphs made from either kind of
+    list: detour-pruned with 0 to degree / 2 reverse edges, the plain k-NN
+    graph, and the nn-descent lists of length `degree` (the shape of the
+    reference's graph)."""
+    n = drows.shape[0]
+    ds = ctx.dataset(drows)
+    knn = cvs.DeviceArray(ctx, (n, kd + 1), np.uint32)
+    kdist = cvs.DeviceArray(ctx, (n, kd + 1), np.float32)
+    ctx.bf_escalations(reset=True)
+    ctx.synchronize()
+    t = time.perf_counter()
+    step = 65_536
+    for lo in range(0, n, step):
+        hi = min(n, lo + step)
+        ds.bf_search_async(drows.rows(lo, hi), kd + 1, knn.rows(lo, hi), kdist.rows(lo, hi))
+        ctx.synchronize()
+        log(f"exact lists: rows {hi} of {n}, {time.perf_counter() - t:.1f} s")
+    t_lists = time.perf_counter() - t
+    escalated, rescanned = ctx.bf_escalations(reset=True)
+    kdist.free()
+    ds.close()
+    g_ex = cvs.DeviceArray(ctx, (n, args.degree), np.uint32)
+    t = time.perf_counter()
+    ctx.cagra_optimize(knn, args.degree, out=g_ex)
+    t_prune = time.perf_counter() - t
+    g_ex_half = ctx.cagra_optimize(knn, args.degree, reverse_edges=args.degree // 2)
+    m = min(n, 2000)
+    ex = knn.to_host()
+    nd = inter.rows(0, m).to_host()
+    knn.free()
+    held = []
+    for u in range(m):
+        row = ex[u][ex[u] != u][:kd]
+        held.append(len(np.intersect1d(row, nd[u])) / len(row))
+    # the plain exact k-NN graph: each row's `degree` nearest other rows, no
+    # pruning and no reverse edges
+    g = args.degree
+    is_self = ex == np.arange(n, dtype=np.uint32)[:, None]
+    plain = np.take_along_axis(ex, np.argsort(is_self, axis=1, kind="stable")[:, :g], 1)
+    del ex, is_self
+    nd_all = inter.to_host()
+    # the graph the reference's build makes (src/cagra.cpp:47-60): nn-descent
+    # lists of length `degree`, used as they are
+    inter64 = cvs.DeviceArray(ctx, (n, g), np.uint32)
+    ctx.cagra_build(drows, intermediate_degree=g, graph_degree=g, intermediate_out=inter64)
+    nd64 = inter64.to_host()
+    inter64.free()
+    graphs = {"nn-descent 128 -> detour (this build)": None}
+    for r in (4, 8, 16, g // 2):
+        graphs[f"nn-descent 128 -> detour, {r} reverse"] = ctx.cagra_optimize(nd_all, g, reverse_edges=r)
+    graphs["nn-descent 128 -> first 64"] = np.ascontiguousarray(nd_all[:, :g])
+    graphs["nn-descent 64 (the reference's graph shape)"] = nd64
+    graphs["exact 128 -> detour"] = g_ex
+    graphs[f"exact 128 -> detour, {g // 2} reverse"] = g_ex_half
+    graphs["exact knn 64"] = plain
+    del nd_all
+    rec = {}
+    for name, gr in graphs.items():
+        ix = idx if gr is None else ctx.cagra_index(drows, gr, nav)
+        row = {}
+        for it in (args.itopk, 2 * args.itopk, 4 * args.itopk, 512):
+            for w in (1, 4):
+                r, _ = ix.search(qs, k, itopk_size=it, search_width=w)
+                row[f"itopk {it} width {w}"] = recall_at_k(r, gt, k)
+        rec[name] = row
+        if gr is not None:
+            ix.close()
+        log(f"graph variant {name}: {json.dumps(row)}")
+    g_ex.free()
+    res = {"seconds_exact_lists": t_lists, "seconds_prune": t_prune,
+           "exact_list_queries_escalated": escalated, "exact_list_queries_rescanned": rescanned,
+           "nn_descent_list_recall_of_exact": float(np.mean(held)), "list_recall_rows": m,
+           "recall_at_10": rec, "queries": len(qs)}
+    log("exact lists: " + json.dumps(res))
+    return res
+
+
 def run_cagra_build(args) -> int:
     """Graph build, N=1,000,000 D=1024 fp32, intermediate degree 128 ->
     degree 64: seconds per phase, local-join GB/s (rows gathered x fp16 row
@@ -868,9 +955,11 @@ def run_cagra_build(args) -> int:
     ctx = cvs.Context(0)
     drows = cvs.DeviceArray.from_host(ctx, base)
     g = cvs.DeviceArray(ctx, (n, args.degree), np.uint32)
+    kd = 2 * args.degree
+    inter = cvs.DeviceArray(ctx, (n, kd), np.uint32) if args.exact_lists else None
     log("building")
     t = time.perf_counter()
-    _, bst = ctx.cagra_build(drows, intermediate_degree=2 * args.degree, graph_degree=args.degree, out=g)
+    _, bst = ctx.cagra_build(drows, intermediate_degree=kd, graph_degree=args.degree, out=g, intermediate_out=inter)
     wall = time.perf_counter() - t
     log(json.dumps(bst))
     nav = cvs.cagra_nav_nodes(n)
@@ -926,6 +1015,9 @@ def run_cagra_build(args) -> int:
         out["rescore_fp32"] = {"seconds": wall2, "seconds_rescore": bst2["seconds_rescore"],
                                "iterations": bst2["iterations"], "recall_at_10": rec2, "queries": q}
         log(json.dumps(out["rescore_fp32"]))
+    if args.exact_lists:
+        out["exact_lists"] = exact_list_graph(cvs, ctx, drows, inter, nav, idx, qs, gt, k, kd, args)
+        inter.free()
     # The reference's own build algorithm at this size, on the GPU, for
     # comparison (above 200,000 rows: IVF k-means, product-quantised
     # per-cluster seeding re-scored exactly, one bucketing round, no

@@ -106,13 +106,19 @@ _SIGNATURES["cvs_cagra_build"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, 
 
 class BuildOptions(ctypes.Structure):
     """cvs_build_options (include/cvs_hip.h)."""
-    _fields_ = [("rescore_fp32", c_int)]
+    _fields_ = [("rescore_fp32", c_int), ("intermediate_out", c_void_p), ("graph_mode", c_int),
+                ("reverse_edges", c_uint32)]
+
+
+GRAPH_DETOUR, GRAPH_KNN = 0, 1
 
 
 _SIGNATURES["cvs_cagra_build_ex"] = (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_uint32, c_uint32,
                                              c_uint32, c_float, c_uint64, POINTER(BuildOptions), c_void_p, c_int,
                                              POINTER(BuildStats)])
 
+_SIGNATURES["cvs_cagra_optimize"] = (c_int, [c_void_p, c_void_p, c_int64, c_uint32, c_int, c_uint32, c_uint32,
+                                             c_void_p, c_int])
 _SIGNATURES["cvs_bf_search_noalloc"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p])
 _SIGNATURES["cvs_cagra_nav_nodes"] = (c_int, [c_int64, c_void_p, POINTER(c_int64)])
 _SIGNATURES["cvs_cagra_entry_points"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p])
@@ -225,7 +231,24 @@ class DeviceArray:
             _check(load().cvs_copy_to_host(self.ctx.handle, out.ctypes.data_as(c_void_p), self.ptr, self.nbytes))
         return out
 
+    def rows(self, lo: int, hi: int) -> "DeviceArray":
+        """A view of rows [lo, hi) of this array: same memory, not owned
+        (its free() does nothing); it must not outlive this array."""
+        if not 0 <= lo <= hi <= self.shape[0]:
+            raise ValueError(f"rows [{lo}, {hi}) outside [0, {self.shape[0]})")
+        view = DeviceArray.__new__(DeviceArray)
+        view.ctx = self.ctx
+        view.shape = (hi - lo,) + self.shape[1:]
+        view.dtype = self.dtype
+        view.nbytes = int(np.prod(view.shape)) * self.dtype.itemsize
+        row_bytes = int(np.prod(self.shape[1:])) * self.dtype.itemsize
+        view.ptr = c_void_p(self.ptr.value + lo * row_bytes)
+        view._view_of = self
+        return view
+
     def free(self) -> None:
+        if getattr(self, "_view_of", None) is not None:
+            return
         if self.ptr is not None and self.ctx.handle is not None:
             _check(load().cvs_device_free(self.ctx.handle, self.ptr))
         self.ptr = None
@@ -344,11 +367,16 @@ class Context:
 
     def cagra_build(self, rows, intermediate_degree: int = 128, graph_degree: int = 64, max_iterations: int = 20,
                     termination_threshold: float = 0.001, seed: int = DEFAULT_BUILD_SEED, out: "DeviceArray" = None,
-                    rescore_fp32: bool = False):
+                    rescore_fp32: bool = False, intermediate_out: "DeviceArray" = None,
+                    graph_mode: int = GRAPH_DETOUR, reverse_edges: int = 0):
         """GPU graph build.  Returns (graph, stats): graph is a host uint32
         array (n, g), or `out` (a device array of that shape) when given.
         rescore_fp32 re-ranks the final intermediate lists by exact fp32
-        distances before pruning (cvs_cagra_build_ex)."""
+        distances before pruning, intermediate_out (a uint32 device array
+        (n, list width)) receives the lists the graph is made from, and
+        graph_mode picks how (GRAPH_DETOUR: detour pruning, with the last
+        `reverse_edges` kept edges of each row giving way to reverse edges;
+        GRAPH_KNN: the nearest graph_degree entries) (cvs_cagra_build_ex)."""
         st = BuildStats()
         if isinstance(rows, DeviceArray):
             n, d = rows.shape
@@ -365,8 +393,14 @@ class Context:
         else:
             host = np.empty((n, max(g, 1)), np.uint32)
             gptr, gdev = host.ctypes.data_as(c_void_p), 0
-        if rescore_fp32:
-            opts = BuildOptions(rescore_fp32=1)
+        if intermediate_out is not None:
+            kd = min(max(int(intermediate_degree), int(graph_degree)), n - 1)
+            if intermediate_out.shape != (n, kd) or intermediate_out.dtype != np.uint32:
+                raise ValueError(f"intermediate_out must be a uint32 device array of shape {(n, kd)}")
+        if rescore_fp32 or intermediate_out is not None or graph_mode != GRAPH_DETOUR or reverse_edges:
+            opts = BuildOptions(rescore_fp32=int(bool(rescore_fp32)),
+                                intermediate_out=intermediate_out.ptr if intermediate_out is not None else None,
+                                graph_mode=int(graph_mode), reverse_edges=int(reverse_edges))
             _check(load().cvs_cagra_build_ex(self.handle, rptr, n, d, rdev, int(intermediate_degree),
                                              int(graph_degree), int(max_iterations), float(termination_threshold),
                                              int(seed), byref(opts), gptr, gdev, byref(st)))
@@ -375,6 +409,32 @@ class Context:
                                           int(graph_degree), int(max_iterations), float(termination_threshold),
                                           int(seed), gptr, gdev, byref(st)))
         return (out if out is not None else host), st.as_dict()
+
+    def cagra_optimize(self, knn, graph_degree: int, reverse_edges: int = 0, out: "DeviceArray" = None):
+        """Detour pruning of caller k-NN lists (n, width) uint32, nearest
+        first, with the last `reverse_edges` kept edges of each row giving way
+        to reverse edges (cvs_cagra_optimize).  Returns a host (n,
+        graph_degree) uint32 graph, or `out` when given."""
+        if isinstance(knn, DeviceArray):
+            n, kd = knn.shape
+            kptr, kdev = knn.ptr, 1
+        else:
+            knn = np.ascontiguousarray(knn, np.uint32)
+            if knn.ndim != 2:
+                raise ValueError("knn must be a 2-D array")
+            n, kd = knn.shape
+            kptr, kdev = knn.ctypes.data_as(c_void_p), 0
+        g = int(graph_degree)
+        if out is not None:
+            if out.shape != (n, g) or out.dtype != np.uint32:
+                raise ValueError(f"out must be a uint32 device array of shape {(n, g)}")
+            gptr, gdev, host = out.ptr, 1, None
+        else:
+            host = np.empty((n, max(g, 1)), np.uint32)
+            gptr, gdev = host.ctypes.data_as(c_void_p), 0
+        _check(load().cvs_cagra_optimize(self.handle, kptr, int(n), int(kd), kdev, g, int(reverse_edges), gptr,
+                                         gdev))
+        return out if out is not None else host
 
 
 class Dataset:

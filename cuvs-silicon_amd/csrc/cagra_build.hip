@@ -34,12 +34,16 @@
 //               merge); inserted entries are marked new and counted.
 //     The loop stops after max_iterations or when the number of insertions
 //     falls below termination_threshold * n * kd.
-//  4. prune     CAGRA's rank-based detour count (Ootomo et al., 2023): an
-//               edge u -> v_j (rank j) is detourable via v_i if rank
-//               max(i, rank of v_j in v_i's list) < j.  Each node keeps the g
-//               edges of fewest detours (ties by rank), then reverse edges
-//               are added: the final list is the closest g/2 kept edges, then
-//               up to g/2 reverse edges, then the remaining kept edges.
+//  4. graph     by default CAGRA's rank-based detour count (Ootomo et al.,
+//               2023): an edge u -> v_j (rank j) is detourable via v_i if
+//               rank max(i, rank of v_j in v_i's list) < j.  Each node keeps
+//               the g edges of fewest detours (ties by rank), in rank order.
+//               Options: the first g list entries (the plain k-NN graph), or
+//               the kept edges merged with r reverse edges (the closest g - r
+//               kept edges, then up to r reverse edges, then the remaining
+//               kept edges; CAGRA's graph has r = g/2).  On clustered N=1M
+//               D=1024 rows reverse edges cost recall at small search beams
+//               (itopk 64: 0.705 with r = 32 against 0.806 without).
 //
 // Lists are sorted 64-bit keys ord(distance) << 32 | id << 1 | new, so the
 // order is (distance, id) and the new flag never reorders a list.  Distances
@@ -941,6 +945,60 @@ __global__ __launch_bounds__(256) void list_ids_kernel(const uint64_t* __restric
   ids[i] = k == kEmpty ? kInvalid : key_id(k);
 }
 
+// Caller-supplied k-NN lists -> id rows for pruning, per row (one wave):
+// ids >= n, the row's own id and repeats (all but the first occurrence) are
+// dropped, the rest keep their order and the row ends in kInvalid.  The
+// pruning below needs exactly that: valid ids first, each naming a row.
+__global__ __launch_bounds__(256) void compact_lists_kernel(const uint32_t* __restrict__ knn, int64_t n, int kd,
+                                                            uint32_t* __restrict__ ids) {
+  constexpr int kHash = 512;  // at most kMaxKd = 256 ids: half full at most
+  __shared__ uint32_t s_key[4][kHash];
+  __shared__ uint32_t s_first[4][kHash];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t u = int64_t(blockIdx.x) * 4 + wave;
+  if (u >= n) return;
+  uint32_t* hk = s_key[wave];
+  uint32_t* hf = s_first[wave];
+  for (int i = lane; i < kHash; i += 64) {
+    hk[i] = kInvalid;
+    hf[i] = kInvalid;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  const uint32_t* row = knn + u * kd;
+  uint32_t w[4], slot[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = e * 64 + lane;
+    w[e] = j < kd ? row[j] : kInvalid;
+    if (int64_t(w[e]) >= n || int64_t(w[e]) == u) w[e] = kInvalid;
+    slot[e] = 0;
+    if (w[e] != kInvalid) {
+      uint32_t s = (w[e] * 0x9E3779B1u) >> 23;
+      for (;;) {
+        const uint32_t prev = atomicCAS(&hk[s], kInvalid, w[e]);
+        if (prev == kInvalid || prev == w[e]) break;
+        s = (s + 1u) & uint32_t(kHash - 1);
+      }
+      slot[e] = s;
+      atomicMin(&hf[s], uint32_t(j));
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  uint32_t* dst = ids + u * kd;
+  int m = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = e * 64 + lane;
+    const bool keep = w[e] != kInvalid && hf[slot[e]] == uint32_t(j);
+    const uint64_t mask = __ballot(keep);
+    if (keep) dst[m + int(mbcnt(mask))] = w[e];
+    m += int(popc(mask));
+  }
+  for (int j = m + lane; j < kd; j += 64) dst[j] = kInvalid;
+}
+
 // Per node (one wave): detour counts, keep g edges, append reverse edges.
 template <int E>
 __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__ ids, int64_t n, int kd, int g,
@@ -1046,7 +1104,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
     if (p < g) {
       const uint32_t w = v[e] == kEmpty ? kInvalid : s_nb[wave][uint32_t(v[e])];
       out[p] = w;
-      if (w != kInvalid) {
+      if (w != kInvalid && rev) {
         const uint32_t slot = atomicAdd(&rev_cnt[w], 1u);
         if (slot < uint32_t(g)) rev[int64_t(w) * g + slot] = uint32_t(u);
       }
@@ -1054,7 +1112,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
   }
 }
 
-// Per node (one wave): closest g/2 kept edges, then up to g/2 reverse
+// Per node (one wave): the closest g - r kept edges, then up to r reverse
 // edges, then the remaining kept edges, then the remaining reverse edges,
 // until g; no duplicates.  Each phase checks its candidates against a wave
 // hash set of the ids placed so far and takes the new ones in order (ballot
@@ -1064,7 +1122,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const uint32_t* __restrict__
 __global__ __launch_bounds__(256) void merge_reverse_kernel(const uint32_t* __restrict__ kept,
                                                             const uint32_t* __restrict__ rev,
                                                             const uint32_t* __restrict__ rev_cnt, int64_t n, int g,
-                                                            uint32_t* __restrict__ out) {
+                                                            int r, uint32_t* __restrict__ out) {
   constexpr int kHash = 1024;  // at most g <= 256 ids are placed: a quarter full at most
   __shared__ uint32_t s_hash[4][kHash];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1090,7 +1148,7 @@ __global__ __launch_bounds__(256) void merge_reverse_kernel(const uint32_t* __re
   const uint32_t* kr = kept + u * g;
   const uint32_t* rr = rev + u * g;
   const int rc = int(min(rev_cnt[u], uint32_t(g)));
-  const int half = g / 2;
+  const int half = g - r;
   uint32_t* dst = out + u * g;
   int m = 0;
   // Takes, in index order, candidates src[i] for i in [lo, hi) that are valid
@@ -1184,11 +1242,56 @@ double elapsed_s(std::chrono::steady_clock::time_point t0) {
   return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 }
 
+// n x kd id rows (valid ids first) -> n x g graph rows in out_graph (device
+// or host memory), then waits for the stream.  CVS_GRAPH_KNN: the first g ids
+// of each row.  CVS_GRAPH_DETOUR: the g edges of fewest detours
+// (prune_kernel), in rank order, of which the last r give way to reverse
+// edges if there are any (merge_reverse_kernel).
+void make_graph(DevMem& mem, hipStream_t st, const uint32_t* ids, int64_t n, int kd, int g, int mode, int r,
+                const uint32_t* order, uint32_t* out_graph, int graph_on_device) {
+  if (mode == CVS_GRAPH_KNN) {
+    CVS_HIP(hipMemcpy2DAsync(out_graph, size_t(g) * sizeof(uint32_t), ids, size_t(kd) * sizeof(uint32_t),
+                             size_t(g) * sizeof(uint32_t), size_t(n),
+                             graph_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, st));
+    CVS_HIP(hipStreamSynchronize(st));
+    return;
+  }
+  const bool reverse = r > 0;
+  const dim3 wave_grid(unsigned((n + 3) / 4));
+  uint32_t* kept = (reverse || !graph_on_device) ? mem.alloc<uint32_t>(size_t(n) * g) : out_graph;
+  uint32_t* rev = reverse ? mem.alloc<uint32_t>(size_t(n) * g) : nullptr;
+  uint32_t* rev_cnt = reverse ? mem.alloc<uint32_t>(size_t(n)) : nullptr;
+  if (reverse) CVS_HIP(hipMemsetAsync(rev_cnt, 0, size_t(n) * sizeof(uint32_t), st));
+  switch (kd <= 64 ? 1 : kd <= 128 ? 2 : 4) {
+    case 1: hipLaunchKernelGGL(prune_kernel<1>, wave_grid, dim3(256), 0, st, ids, n, kd, g, order, kept, rev, rev_cnt); break;
+    case 2: hipLaunchKernelGGL(prune_kernel<2>, wave_grid, dim3(256), 0, st, ids, n, kd, g, order, kept, rev, rev_cnt); break;
+    default: hipLaunchKernelGGL(prune_kernel<4>, wave_grid, dim3(256), 0, st, ids, n, kd, g, order, kept, rev, rev_cnt); break;
+  }
+  after_launch("prune_kernel");
+  uint32_t* final_graph = kept;
+  if (reverse) {
+    final_graph = graph_on_device ? out_graph : mem.alloc<uint32_t>(size_t(n) * g);
+    hipLaunchKernelGGL(merge_reverse_kernel, wave_grid, dim3(256), 0, st, static_cast<const uint32_t*>(kept),
+                       static_cast<const uint32_t*>(rev), static_cast<const uint32_t*>(rev_cnt), n, g, r,
+                       final_graph);
+    after_launch("merge_reverse_kernel");
+  }
+  if (!graph_on_device)
+    CVS_HIP(hipMemcpyAsync(out_graph, final_graph, size_t(n) * g * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  CVS_HIP(hipStreamSynchronize(st));
+}
+
 void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t d, int rows_on_device,
                         uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
                         float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
                         const cvs_build_options* opts, cvs_build_stats* stats) {
   const bool rescore = opts && opts->rescore_fp32;
+  const int graph_mode = opts ? opts->graph_mode : CVS_GRAPH_DETOUR;
+  const uint32_t reverse_edges = opts ? opts->reverse_edges : 0u;
+  if (graph_mode != CVS_GRAPH_KNN && graph_mode != CVS_GRAPH_DETOUR)
+    fail(CVS_ERR_INVALID_ARGUMENT, "unknown graph_mode");
+  if (reverse_edges && graph_mode != CVS_GRAPH_DETOUR)
+    fail(CVS_ERR_INVALID_ARGUMENT, "reverse_edges needs graph_mode CVS_GRAPH_DETOUR");
   const auto t_start = std::chrono::steady_clock::now();
   if (!rows || n <= 0 || d <= 0) fail(CVS_ERR_INVALID_ARGUMENT, "dataset must be non-null and non-empty");
   if (!out_graph) fail(CVS_ERR_INVALID_ARGUMENT, "null out_graph");
@@ -1344,28 +1447,41 @@ void cagra_build_device(cvs_context* ctx, const float* rows, int64_t n, int64_t 
   hipLaunchKernelGGL(list_ids_kernel, dim3(unsigned((n * kd + 255) / 256)), dim3(256), 0, st,
                      static_cast<const uint64_t*>(a.lists), n, kd, kp, ids);
   after_launch("list_ids_kernel");
-  uint32_t* kept = mem.alloc<uint32_t>(size_t(n) * g);
-  uint32_t* rev = mem.alloc<uint32_t>(size_t(n) * g);
-  uint32_t* rev_cnt = mem.alloc<uint32_t>(size_t(n));
-  CVS_HIP(hipMemsetAsync(rev_cnt, 0, size_t(n) * sizeof(uint32_t), st));
-  switch (e_slots) {
-    case 1: hipLaunchKernelGGL(prune_kernel<1>, wave_grid, dim3(256), 0, st, ids, n, kd, g, a.order, kept, rev, rev_cnt); break;
-    case 2: hipLaunchKernelGGL(prune_kernel<2>, wave_grid, dim3(256), 0, st, ids, n, kd, g, a.order, kept, rev, rev_cnt); break;
-    default: hipLaunchKernelGGL(prune_kernel<4>, wave_grid, dim3(256), 0, st, ids, n, kd, g, a.order, kept, rev, rev_cnt); break;
-  }
-  after_launch("prune_kernel");
-  uint32_t* final_graph = graph_on_device ? out_graph : mem.alloc<uint32_t>(size_t(n) * g);
-  hipLaunchKernelGGL(merge_reverse_kernel, wave_grid, dim3(256), 0, st, static_cast<const uint32_t*>(kept),
-                     static_cast<const uint32_t*>(rev), static_cast<const uint32_t*>(rev_cnt), n, g, final_graph);
-  after_launch("merge_reverse_kernel");
-  if (!graph_on_device)
-    CVS_HIP(hipMemcpyAsync(out_graph, final_graph, size_t(n) * g * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-  CVS_HIP(hipStreamSynchronize(st));
+  if (opts && opts->intermediate_out)
+    CVS_HIP(hipMemcpyAsync(opts->intermediate_out, ids, size_t(n) * kd * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+                           st));
+  make_graph(mem, st, ids, n, kd, g, graph_mode, int(std::min<uint32_t>(reverse_edges, uint32_t(g))), a.order,
+             out_graph, graph_on_device);
   s.seconds_prune = elapsed_s(t_pr);
   s.graph_degree = uint32_t(g);
   s.intermediate_degree = uint32_t(kd);
   s.seconds_total = elapsed_s(t_start);
   if (stats) *stats = s;
+}
+
+void cagra_optimize_device(cvs_context* ctx, const uint32_t* knn, int64_t n, uint32_t kd_in, int knn_on_device,
+                           uint32_t graph_degree, uint32_t reverse_edges, uint32_t* out_graph,
+                           int graph_on_device) {
+  if (!knn || !out_graph) fail(CVS_ERR_INVALID_ARGUMENT, "null k-NN lists or out_graph");
+  if (n < 2) fail(CVS_ERR_INVALID_ARGUMENT, "a graph needs at least 2 rows");
+  if (n > int64_t(INT32_MAX)) fail(CVS_ERR_UNSUPPORTED, "graph optimize needs n < 2^31");
+  if (kd_in == 0 || graph_degree == 0) fail(CVS_ERR_INVALID_ARGUMENT, "degrees must be positive");
+  if (kd_in > uint32_t(kMaxKd)) fail(CVS_ERR_UNSUPPORTED, "k-NN list width exceeds 256");
+  if (graph_degree > kd_in) fail(CVS_ERR_INVALID_ARGUMENT, "graph_degree exceeds the k-NN list width");
+  if (reverse_edges > graph_degree) fail(CVS_ERR_INVALID_ARGUMENT, "reverse_edges exceeds graph_degree");
+  const int kd = int(kd_in), g = int(graph_degree);
+  hipStream_t st = ctx->stream;
+  DevMem mem;
+  const uint32_t* src = knn;
+  if (!knn_on_device) {
+    uint32_t* tmp = mem.alloc<uint32_t>(size_t(n) * kd);
+    CVS_HIP(hipMemcpyAsync(tmp, knn, size_t(n) * kd * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    src = tmp;
+  }
+  uint32_t* ids = mem.alloc<uint32_t>(size_t(n) * kd);
+  hipLaunchKernelGGL(compact_lists_kernel, dim3(unsigned((n + 3) / 4)), dim3(256), 0, st, src, n, kd, ids);
+  after_launch("compact_lists_kernel");
+  make_graph(mem, st, ids, n, kd, g, CVS_GRAPH_DETOUR, int(reverse_edges), nullptr, out_graph, graph_on_device);
 }
 
 }  // namespace
@@ -1394,6 +1510,16 @@ int cvs_cagra_build_ex(cvs_context* ctx, const float* rows, int64_t n, int64_t d
     bind(ctx);
     cagra_build_device(ctx, rows, n, d, rows_on_device, intermediate_degree, graph_degree, max_iterations,
                        termination_threshold, seed, out_graph, graph_on_device, options, stats);
+  });
+}
+
+int cvs_cagra_optimize(cvs_context* ctx, const uint32_t* knn_graph, int64_t n, uint32_t knn_degree,
+                       int knn_on_device, uint32_t graph_degree, uint32_t reverse_edges, uint32_t* out_graph,
+                       int graph_on_device) {
+  return guarded([&] {
+    bind(ctx);
+    cagra_optimize_device(ctx, knn_graph, n, knn_degree, knn_on_device, graph_degree, reverse_edges, out_graph,
+                          graph_on_device);
   });
 }
 

@@ -100,13 +100,17 @@ std::vector<uint32_t> MetalContext::build_knn_graph(const float* dataset, int64_
   cvs_context* ctx = require(impl_->ctx);
   if (N < 2 || graph_degree == 0) throw std::invalid_argument("graph build needs N >= 2 and a positive degree");
   const uint32_t g = std::min<uint32_t>(graph_degree, static_cast<uint32_t>(N - 1));
-  // Intermediate lists twice the output degree, within the build's 128.
+  // Intermediate lists twice the output degree, within the build's 128; the
+  // result is each row's nearest g list entries, a k-NN graph as the
+  // reference's build_knn_graph returns (no pruning).
   const uint32_t inter =
       std::min<uint32_t>(std::max<uint32_t>(g, std::min<uint32_t>(2 * g, 128)), static_cast<uint32_t>(N - 1));
   std::vector<uint32_t> graph(static_cast<size_t>(N) * g);
   cvs_build_stats st{};
-  check(cvs_cagra_build(ctx, dataset, N, D, 0, inter, g, n_descent_iters, 0.001f, 0xFEDCBA9876543210ULL,
-                        graph.data(), 0, &st));
+  cvs_build_options opts{};
+  opts.graph_mode = CVS_GRAPH_KNN;
+  check(cvs_cagra_build_ex(ctx, dataset, N, D, 0, inter, g, n_descent_iters, 0.001f, 0xFEDCBA9876543210ULL, &opts,
+                           graph.data(), 0, &st));
   return graph;
 }
 

@@ -350,8 +350,9 @@ typedef struct cvs_build_stats {
  * random bucketing seeds a degree-`intermediate_degree` kNN list per row,
  * nn-descent refines it (at most `max_iterations` iterations; stops early
  * when insertions / (n * intermediate_degree) < termination_threshold), and
- * rank-based detour pruning plus reverse edges reduce it to `graph_degree`
- * (clamped to n - 1).  Writes n x min(graph_degree, n - 1) uint32 ids to
+ * rank-based detour pruning keeps `graph_degree` (clamped to n - 1) of its
+ * entries, in list order (cvs_cagra_build_ex offers the plain k-NN graph and
+ * pruning with reverse edges instead).  Writes n x min(graph_degree, n - 1) uint32 ids to
  * out_graph (host memory, or device memory if graph_on_device = 1); rows
  * with fewer neighbours end in UINT32_MAX.  `seed` drives the bucketing
  * permutation.  Replaces MetalContext::build_knn_graph
@@ -360,6 +361,11 @@ int cvs_cagra_build(cvs_context* ctx, const float* rows, int64_t n, int64_t d, i
                     uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
                     float termination_threshold, uint64_t seed, uint32_t* out_graph, int graph_on_device,
                     cvs_build_stats* stats);
+
+/* How the build turns each node's intermediate list into its graph row
+ * (cvs_build_options.graph_mode). */
+#define CVS_GRAPH_DETOUR 0 /* CAGRA's rank-based detour pruning (the default of cvs_cagra_build) */
+#define CVS_GRAPH_KNN 1    /* the first graph_degree entries: the k-NN graph, the reference's graph */
 
 /* Options of cvs_cagra_build_ex. */
 typedef struct cvs_build_options {
@@ -370,6 +376,23 @@ typedef struct cvs_build_options {
    * the build's fp16-input estimates, as cvs_cagra_build does.  Reads
    * n * intermediate_degree fp32 rows once more. */
   int rescore_fp32;
+  /* Optional device memory of n x min(max(intermediate_degree, graph_degree),
+   * n - 1) uint32: receives each node's final intermediate list (the one the
+   * pruning reads), nearest first, UINT32_MAX-padded.  NULL: not written. */
+  uint32_t* intermediate_out;
+  /* CVS_GRAPH_DETOUR (0, as cvs_cagra_build) or CVS_GRAPH_KNN. */
+  int graph_mode;
+  /* CVS_GRAPH_DETOUR only: the last reverse_edges kept edges of each row
+   * give way to reverse edges (nodes that kept this one), as in
+   * cvs_cagra_optimize; 0 (as cvs_cagra_build): none.  CAGRA's graph uses
+   * graph_degree / 2.  Measured recall@10 of the graph search at itopk 64:
+   * on clustered N=1M D=1024 rows (degree 128 -> 64) 0.806 with 0, 0.799
+   * with 4, 0.705 with 32; on 3,000 rows in 20 far-apart 4-dimensional
+   * patches (degree 64 -> 32) the queries left at zero recall fell from 7-18
+   * of 300 with 0 to 1-13 with 4.  Reverse edges help where nodes few
+   * others point to are hard to reach; on high-dimensional rows they cost
+   * recall at small search beams. */
+  uint32_t reverse_edges;
 } cvs_build_options;
 
 /* cvs_cagra_build with options (NULL: those of cvs_cagra_build).  No
@@ -379,6 +402,25 @@ int cvs_cagra_build_ex(cvs_context* ctx, const float* rows, int64_t n, int64_t d
                        uint32_t intermediate_degree, uint32_t graph_degree, uint32_t max_iterations,
                        float termination_threshold, uint64_t seed, const cvs_build_options* options,
                        uint32_t* out_graph, int graph_on_device, cvs_build_stats* stats);
+
+/* Prunes caller-supplied k-NN lists (n x knn_degree uint32 ids per row,
+ * nearest first; host memory, or device memory if knn_on_device = 1) into a
+ * search graph with the build's rank-based detour pruning (CAGRA, Ootomo et
+ * al. 2023): each node keeps the graph_degree edges of fewest detours, in
+ * rank order.  With reverse_edges = r > 0 (r <= graph_degree) the row is
+ * then the closest graph_degree - r kept edges, up to r reverse edges (nodes
+ * that kept this one), then the remaining kept edges (CAGRA's graph uses
+ * r = graph_degree / 2).  Ids >= n, a row's own id and repeated ids are
+ * ignored.  knn_degree <= 256, graph_degree <= knn_degree.  Writes n x
+ * graph_degree ids to out_graph (host, or device if graph_on_device = 1);
+ * rows with fewer neighbours end in UINT32_MAX.  The reference has no such
+ * entry point (its build keeps its k-NN lists as the graph,
+ * src/cagra.cpp:47-60, and include/cuvs/neighbors/cagra.hpp declares no
+ * cagra::optimize); it serves callers that hold k-NN lists of their own,
+ * exact ones from cvs_bf_search included. */
+int cvs_cagra_optimize(cvs_context* ctx, const uint32_t* knn_graph, int64_t n, uint32_t knn_degree,
+                       int knn_on_device, uint32_t graph_degree, uint32_t reverse_edges, uint32_t* out_graph,
+                       int graph_on_device);
 
 /* Phase timings and counters of one cvs_cagra_build_reference call. */
 typedef struct cvs_ref_build_stats {
