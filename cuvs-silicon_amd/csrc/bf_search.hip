@@ -662,8 +662,11 @@ __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 // Initial scan threshold per query: the kp-th smallest of the sample minima.
 // Any kp minima belong to kp distinct dataset rows, so at least kp rows lie
-// at or below it.  One wave per query (m <= 512 minima, 8 per lane), ballot
-// radix select on the order-preserving integer image.
+// at or below it.  One wave per query (m <= 512 minima, 8 per lane) on the
+// order-preserving integer image: for kp <= 32 a tournament (each lane sorts
+// its 8 values; each round takes the wave minimum of the lanes' smallest
+// remaining values and removes it from the lanes holding it, so kp rounds at
+// most), otherwise a ballot radix select (32 rounds of 8 ballots).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict__ sgmin, int m, int kp, int nq,
                                                         float* __restrict__ thr0) {
@@ -682,6 +685,45 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
     return;
   }
   int need = kp;
+  if (kp <= 32) {
+    // Sorting network for 8 values (19 compare-exchanges).
+    auto cx = [&](int i, int j) {
+      const uint32_t lo = min(v[i], v[j]), hi = max(v[i], v[j]);
+      v[i] = lo;
+      v[j] = hi;
+    };
+    cx(0, 1); cx(2, 3); cx(4, 5); cx(6, 7);
+    cx(0, 2); cx(1, 3); cx(4, 6); cx(5, 7);
+    cx(1, 2); cx(5, 6); cx(0, 4); cx(3, 7);
+    cx(1, 5); cx(2, 6);
+    cx(1, 4); cx(3, 6);
+    cx(2, 4); cx(3, 5);
+    cx(3, 4);
+    uint32_t ans = 0xffffffffu;
+    for (int round = 0; round <= 32; ++round) {
+      uint32_t mn = v[0];
+      mn = min(mn, xor_lanes<1>(mn));
+      mn = min(mn, xor_lanes<2>(mn));
+      mn = min(mn, xor_lanes<4>(mn));
+      mn = min(mn, xor_lanes<8>(mn));
+      mn = min(mn, xor_lanes<16>(mn));
+      mn = min(mn, xor_lanes<32>(mn));
+      const bool mine = v[0] == mn;
+      const int c = popc(__ballot(mine));
+      if (c >= need || mn == 0xffffffffu) {
+        ans = mn;
+        break;
+      }
+      need -= c;
+      if (mine) {
+#pragma unroll
+        for (int i = 0; i < 7; ++i) v[i] = v[i + 1];
+        v[7] = 0xffffffffu;
+      }
+    }
+    if (lane == 0) thr0[q] = ans == 0xffffffffu ? INFINITY : unord_f32(ans);
+    return;
+  }
   uint32_t pre = 0;
   for (int b = 31; b >= 0; --b) {
     int c = 0;
