@@ -16,7 +16,7 @@
 //          flight while the current ones multiply.
 //  select  one workgroup per query: a three-pass radix select (12 + 12 + 8
 //          bits of the keys' order image) finds the R-th smallest key
-//          (R = k + max(32, k / 4)); every row at or below it is re-ranked
+//          (R = max(2 k, k + 32)); every row at or below it is re-ranked
 //          exactly in fp32 into a running top k kept in LDS (block bitonic
 //          sort of up to 2,048 keys).  The certificate of the fused path
 //          (Cert, bf_common.hpp) then bounds the exact distance of every row
@@ -190,9 +190,39 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
       for (int i = tid; i < nb; i += kWT) s_hist[i] = 0;
       __syncthreads();
       const int hs = sh + w;  // bits above this pass must equal the prefix
-      for (int64_t i = tid; i < n; i += kWT) {
-        const uint32_t o = ord_f32(kr[i]);
-        if (hs >= 32 || (o >> hs) == prefix) atomicAdd(&s_hist[(o >> sh) & uint32_t(nb - 1)], 1u);
+      // 16 keys per thread and step as four 16-byte loads (the row starts
+      // 128-byte aligned; keys past n are masked).  Keys crowd into few
+      // bins (distances of one query span few exponents), so each wave
+      // counts its keys bin by bin: the lowest pending lane's bin, the
+      // ballot of the lanes holding it, one atomic for all of them.
+      const float4* kr4 = reinterpret_cast<const float4*>(kr);
+      const int64_t n4 = (n + 3) / 4;
+      for (int64_t b4 = 0; b4 < n4; b4 += int64_t(kWT) * 4) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t i4 = b4 + int64_t(u) * kWT + tid;
+          v[u] = i4 < n4 ? kr4[i4] : make_float4(INFINITY, INFINITY, INFINITY, INFINITY);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t i0 = (b4 + int64_t(u) * kWT + tid) * 4;
+          const float c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t o = ord_f32(c[e]);
+            const bool in = i0 + e < n && (hs >= 32 || (o >> hs) == prefix);
+            const uint32_t bin = (o >> sh) & uint32_t(nb - 1);
+            uint64_t todo = __ballot(in);
+            while (todo) {
+              const int leader = __builtin_ctzll(todo);
+              const uint32_t lb = uint32_t(__builtin_amdgcn_readlane(int(bin), leader));
+              const uint64_t same = __ballot(in && bin == lb);
+              if (lane == leader) atomicAdd(&s_hist[lb], uint32_t(popc(same)));
+              todo &= ~same;
+            }
+          }
+        }
       }
       __syncthreads();
       // Bin holding the need-th key: each thread sums nb / 256 bins, a block
@@ -375,7 +405,10 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   const TimerSpan t0 = timer_span(ctx, "bf_prep");
   launch_query_tiles(ctx, ds, queries, q, q_tiles4 * 32, qtiles, qnorms, qerr, t0.start, t0.stop);
   const Cert cert = make_cert(ctx, ds, qnorms, qerr);
-  const int R = int(std::min<int64_t>(ds->n, k + std::max<int64_t>(32, k / 4)));
+  // Rows re-ranked before the certificate: twice k (at least k + 32), as
+  // the fused path keeps, so that the rank gap between the k-th result and
+  // the R-th key clears the fp16 error on dense neighbourhoods.
+  const int R = int(std::min<int64_t>(ds->n, std::max<int64_t>(2 * k, k + 32)));
   for (int64_t c0 = 0; c0 < q; c0 += qc) {
     const int64_t nq = std::min(qc, q - c0);
     KeysArgs ka{};
