@@ -372,6 +372,44 @@ void metal_context_matches_c_abi() {
   CHECK(n1 == n2 && d1 == d2);
   cvs_cagra_index_destroy(ix);
 
+  // build_knn_graph returns k-NN lists (nearest first), as the reference's
+  // does: G distinct ids per row, never the row itself, distances
+  // non-decreasing along each row (up to the build's fp16 ranking of near
+  // ties), and almost every row holding its exact nearest neighbour.
+  {
+    const auto knn = mc.build_knn_graph(base.data(), N, D, G, 10, 0);
+    CHECK(knn.size() == std::size_t(N) * G);
+    auto dist2 = [&](std::int64_t a, std::int64_t b) {
+      float s2 = 0.f;
+      for (std::int64_t j = 0; j < D; ++j) {
+        const float t = base[a * D + j] - base[b * D + j];
+        s2 += t * t;
+      }
+      return s2;
+    };
+    int nn_held = 0, misordered = 0;
+    for (std::int64_t i = 0; i < N; ++i) {
+      std::set<std::uint32_t> seen;
+      float prev = -1.f;
+      for (std::uint32_t g = 0; g < G; ++g) {
+        const std::uint32_t v = knn[i * G + g];
+        CHECK(v < std::uint32_t(N) && v != std::uint32_t(i) && seen.insert(v).second);
+        const float dv = dist2(i, v);
+        misordered += dv < prev ? 1 : 0;
+        prev = dv;
+      }
+      float best = 3.0e38f;
+      std::int64_t arg = -1;
+      for (std::int64_t j = 0; j < N; ++j)
+        if (j != i && dist2(i, j) < best) best = dist2(i, j), arg = j;
+      nn_held += (seen.count(std::uint32_t(arg)) || dist2(i, knn[i * G]) == best) ? 1 : 0;
+    }
+    std::printf("build_knn_graph: exact nearest neighbour held by %d of %lld rows, %d misordered steps\n", nn_held,
+                (long long)N, misordered);
+    CHECK(nn_held >= N * 95 / 100);
+    CHECK(misordered <= int(N * G / 100));
+  }
+
   // With no edges each query can only return its own entry node.
   std::vector<std::uint32_t> empty(N * G, kNone);
   CHECK(mc.search_cagra(base.data(), N, D, empty.data(), G, qs.data(), Q, n1.data(), d1.data(), K, 32, 100,
