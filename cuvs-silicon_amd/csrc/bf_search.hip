@@ -1235,17 +1235,17 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   p.stride = global_lists ? Lists<128, kModeScan>::CAP : p.kp;
 
   // Sample: 16,384 rows for small batches, 65,536 for other large ones and
-  // 131,072 for the register-blocked scan, in whole units, evenly strided,
+  // 32,768 for the register-blocked scan, in whole units, evenly strided,
   // over Gs workgroups; 2 minima per (query, workgroup).  The initial
-  // threshold then sits near rank kp * n / sample of each query's
-  // distances, so a workgroup's lists see about kp * n / (sample * G)
+  // threshold (below) then sits near rank r * n / sample of each query's
+  // distances, so a workgroup's lists see about r * n / (sample * G)
   // appends per query over its range.  Small batches are bound by the
   // scan's HBM stream, where a few more appends cost little and the
   // sample's own latency is what shows.  The register-blocked scan's appends
-  // and compactions sit on its critical path: at N=1M D=1024 Q=10,000
-  // K=100 its launch takes 26.9 / 24.7 / 22.5 ms after samples of
-  // 32,768 / 65,536 / 131,072 rows, which themselves take 1.2 / 2.1 / 4.1 ms.
-  p.s_units = (p.gemm ? 131072 : p.large_batch ? 65536 : 16384) / rpu;
+  // and compactions sit on its critical path, so its threshold rank matters
+  // (about 2 ms per doubling at N=1M Q=10,000 K=100); with the rank rule
+  // below a 32,768-row sample keeps it at ~977 for 1.15 ms of sampling.
+  p.s_units = (p.gemm ? 32768 : p.large_batch ? 65536 : 16384) / rpu;
   if (p.s_units < 1) p.s_units = 1;
   if (p.s_units > p.n_units) p.s_units = p.n_units;
   p.s_stride = p.n_units / p.s_units;
@@ -1253,21 +1253,28 @@ BfPlan plan_bf(cvs_context* ctx, const cvs_dataset* ds, const float* queries, in
   if (int64_t(p.Gs) > p.s_units) p.Gs = int(p.s_units);
   p.m_min = 2 * p.Gs;
   // The r-th smallest sample minimum bounds r distinct rows (the minima
-  // are over disjoint row sets), so about r * n / sampled of the query's n
-  // keys lie at or below it, with a relative spread of about 1 / sqrt(r).
-  // The merge certifies its R candidates against the lists' final
-  // thresholds, so that rank should clear R: r is the smallest rank >= 8
-  // whose expected rank is R (1 + 4 / sqrt(r)) or more, at most R (where
-  // the sample covers nearly every row, rank r is certain).  A lower
-  // threshold means fewer appends for the scan: at N=1M D=1024 Q=10,000
-  // K=100 this is r = 53 (expected rank 404) where r = kp = 128 sat at
-  // rank 977, and the scan took 4% less time; at Q=100 K=10, r = 8 (rank
-  // 488) where r = 16 sat at 977, and the search took 1.8% less.
+  // are over disjoint row sets).  The merge certifies its R candidates
+  // against the lists' final thresholds, so that threshold should lie at
+  // rank R or beyond among the query's n keys.  It lies below rank R only if
+  // r of the sampled rows fall among the query's R nearest, and that count
+  // is close to Poisson with mean lambda = R * sampled / n: r is the
+  // smallest rank with P(Poisson(lambda) >= r) <= 1e-9, at most R (where
+  // the sample covers every row, rank r is certain).  A threshold set too
+  // low is caught by the certificate, but its remedy re-ranks every row.
+  // A lower threshold means fewer appends for the scan, which is what lets
+  // the large-batch sample shrink: at N=1M D=1024 Q=10,000 K=100, 32,768
+  // rows and r = 32 put it at expected rank 977 (as 131,072 rows and
+  // r = kp = 128 did), for a third of the sample's time.
   {
     const int R = p.kp > 64 ? 2 * p.kp : std::min(2 * p.kp, 128);
-    const double per = double(ds->n) / double(p.s_units * rpu);  // keys per sampled row
-    int r = 8;
-    while (r < R && double(r) * per < double(R) * (1.0 + 4.0 / std::sqrt(double(r)))) ++r;
+    const double lambda = double(R) * double(p.s_units * rpu) / double(ds->n);
+    double term = std::exp(-lambda), cdf = term;
+    int r = 1;
+    while (1.0 - cdf > 1e-9 && r < R) {
+      term *= lambda / double(r);
+      cdf += term;
+      ++r;
+    }
     p.sel_rank = std::max(1, std::min({r, R, p.m_min}));
   }
 
