@@ -931,6 +931,22 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
   const int R = 2 * kp < 64 * E ? 2 * kp : 64 * E;
   if (tid == 0) s_npass = 0;
 
+  // 1. Bound from the list minima and the smallest list threshold (G <= 256),
+  // by wave 0, which requests them before its share of the keys, so that it
+  // waits for them alone.  For R <= 32 the bound is the R-th smallest of the
+  // lanes' minima of their four list minima: those are R distinct list
+  // minima, so at least R keys lie at or below it (one 64-key sort instead
+  // of a 256-key one; the bound is a little looser).
+  uint64_t mins[4];
+  float cut = INFINITY;
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = lane + 64 * i;
+      mins[i] = x < G ? lmin[q * G + x] : kSentinel;
+      if (x < G) cut = fminf(cut, lcut[q * G + x]);
+    }
+  }
   // First batch of keys, requested before the bound is known.
   uint64_t key[kBatch];
 #pragma unroll
@@ -938,20 +954,20 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
     const int e = r * kThreads + tid;
     key[r] = e < total ? src[e] : kSentinel;
   }
-  // 1. Bound from the list minima and the smallest list threshold (G <= 256), by wave 0.
   if (wave == 0) {
-    uint64_t mins[4];
-    float cut = INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int x = lane + 64 * i;
-      mins[i] = x < G ? lmin[q * G + x] : kSentinel;
-      if (x < G) cut = fminf(cut, lcut[q * G + x]);
-    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) cut = fminf(cut, xor_lanes_f(cut, o));
-    wave_sort_e<4>(mins);
-    const uint64_t bound = key_at<4>(mins, R - 1);
+    uint64_t bound;
+    if (R <= 32) {
+      uint64_t lm[1] = {mins[0]};
+#pragma unroll
+      for (int i = 1; i < 4; ++i) lm[0] = mins[i] < lm[0] ? mins[i] : lm[0];
+      wave_sort_e<1>(lm);
+      bound = key_at<1>(lm, R - 1);
+    } else {
+      wave_sort_e<4>(mins);
+      bound = key_at<4>(mins, R - 1);
+    }
     if (lane == 0) {
       s_bound = bound;
       s_tstar = cut;
@@ -960,7 +976,8 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
   __syncthreads();
   const uint64_t bound = s_bound;
 
-  // 2. Filter every key; append the passing ones.
+  // 2. Filter every key; append the passing ones (the ballots of the whole
+  // batch first, then one LDS atomic per wave for their slots).
   for (int b0 = 0; b0 < total; b0 += kBatch * kThreads) {
     if (b0 > 0) {
 #pragma unroll
@@ -969,16 +986,22 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
         key[r] = e < total ? src[e] : kSentinel;
       }
     }
+    uint64_t m[kBatch];
+    uint32_t tot = 0;
 #pragma unroll
     for (int r = 0; r < kBatch; ++r) {
-      const bool pass = key[r] <= bound && key[r] != kSentinel;
-      const uint64_t m = __ballot(pass);
-      if (m == 0) continue;
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&s_npass, uint32_t(popc(m)));
-      base = uint32_t(__shfl(int(base), 0));
-      const uint32_t slot = base + uint32_t(mbcnt(m));
-      if (pass && slot < uint32_t(kMaxPass)) s_pass[slot] = key[r];
+      m[r] = __ballot(key[r] <= bound && key[r] != kSentinel);
+      tot += uint32_t(popc(m[r]));
+    }
+    if (tot == 0) continue;
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(&s_npass, tot);
+    base = uint32_t(__shfl(int(base), 0));
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r) {
+      const uint32_t slot = base + uint32_t(mbcnt(m[r]));
+      if (((m[r] >> lane) & 1ull) && slot < uint32_t(kMaxPass)) s_pass[slot] = key[r];
+      base += uint32_t(popc(m[r]));
     }
   }
   __syncthreads();
