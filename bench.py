@@ -137,6 +137,32 @@ def calibrate_mfma() -> int:
         out[name] = {"m": m, "n": n_, "k": k, "tflops": tflops, "frac_of_nominal": tflops / MFMA_F16_PEAK_TFLOPS}
         del a, b
     print(json.dumps({"calibrate_mfma_fp16_gemm": out}), flush=True)
+
+    # The library's own matrix-core loop (cvs_calibrate_mfma): the large-batch
+    # scan's 4 x 4 register block of 32 x 32 x 16 MFMAs, one workgroup of 4
+    # waves per compute unit, no memory traffic; operands held in registers
+    # or re-read from LDS every k-step as the scan reads them.  The operand
+    # values change the rate (power): random normals, the scan's own value
+    # distribution (benchmark rows centred and scaled by a power of two so
+    # that the largest magnitude lies in [128, 256), as the index stores
+    # them), and zeros.
+    cvs = load_package()
+    ctx = cvs.Context(0)
+    rows = torch.from_numpy(cvs.synth_clustered(12345, cvs.STREAM_BASE, 8192, 1024)).to("cuda:0")
+    rows = rows - rows.mean(0)
+    rows = rows * float(2.0 ** (8 - int(np.frexp(np.float32(rows.abs().max().item()))[1])))
+    data = {"randn": torch.randn(8192, 1024, device="cuda:0", dtype=torch.float16),
+            "scan_values": rows.to(torch.float16).contiguous(),
+            "zeros": torch.zeros(8192, 1024, device="cuda:0", dtype=torch.float16)}
+    loop = {}
+    for name, t in data.items():
+        for from_lds in (False, True):
+            tf = ctx.calibrate_mfma(t.data_ptr(), t.numel() * 2, ctx.device_info()["compute_units"], 65536,
+                                    from_lds=from_lds, reps=5)
+            loop[f"{name}_{'lds' if from_lds else 'registers'}"] = {
+                "tflops": tf, "frac_of_nominal": tf / MFMA_F16_PEAK_TFLOPS}
+    ctx.close()
+    print(json.dumps({"calibrate_mfma_loop": loop}), flush=True)
     return 0
 
 

@@ -128,6 +128,8 @@ _SIGNATURES["cvs_cagra_search_reference"] = (c_int, [c_void_p, c_void_p, c_void_
 _SIGNATURES["cvs_cagra_search_reference_async"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32,
                                                            c_uint32, c_void_p, c_void_p, c_void_p])
 _SIGNATURES["cvs_calibrate_gather_read"] = (c_int, [c_void_p, c_size_t, c_int64, c_int, c_int, c_int, POINTER(c_double)])
+_SIGNATURES["cvs_calibrate_mfma"] = (c_int, [c_void_p, c_void_p, c_size_t, c_int, c_int64, c_int, c_int,
+                                             POINTER(c_double)])
 _SIGNATURES["cvs_cagra_search_record_async"] = (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_uint32,
                                                         c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p,
                                                         c_uint32])
@@ -318,6 +320,18 @@ class Context:
         _check(load().cvs_calibrate_gather_read(self.handle, int(row_bytes), int(n_rows), int(workgroups),
                                                 int(rows_per_team), int(reps), byref(gbs)))
         return gbs.value
+
+    def calibrate_mfma(self, data_ptr, nbytes: int, workgroups: int, ksteps: int, from_lds: bool = False,
+                       reps: int = 5) -> float:
+        """fp16 MFMA rate in TFLOP/s of the large-batch scan's register
+        block on the fp16 data at device address data_ptr (an int or a
+        c_void_p; C:
+        cvs_calibrate_mfma)."""
+        tf = c_double(0)
+        ptr = data_ptr if isinstance(data_ptr, c_void_p) else c_void_p(int(data_ptr))
+        _check(load().cvs_calibrate_mfma(self.handle, ptr, int(nbytes), int(workgroups),
+                                         int(ksteps), 1 if from_lds else 0, int(reps), byref(tf)))
+        return tf.value
 
     def set_timing(self, enable: bool) -> None:
         _check(load().cvs_context_set_timing(self.handle, 1 if enable else 0))

@@ -34,6 +34,9 @@
 //    workgroup's position among those covering it, so each list has one
 //    writer; the workgroup that ends a block fills the unused list slots
 //    with empty lists.
+//
+// The same file holds cvs_calibrate_mfma, this register block's matrix-core
+// rate with no memory traffic, the reference point for the scan's own rate.
 #include <algorithm>
 #include <cmath>
 
@@ -559,6 +562,14 @@ void bf_gemm_scan_kernel(GemmArgs a) {
           for (int e = 0; e < 16; ++e) acc[r][j][e] = 0.f;
         }
       }
+      // Nothing of this block may stay outstanding into the next block's
+      // stages.  The compiler reloads spilled values here, and it counts
+      // none of the inline-assembly LDS loads, so the wait it would place
+      // for such a reload inside the stage loop is vmcnt(0) at every
+      // stage, which drains the whole prefetch each time.  Waiting once
+      // here costs the reload's latency alone: the epilogue has let every
+      // prefetched load land.
+      __builtin_amdgcn_s_waitcnt(0);
     }
     end_block();
     // The workgroup that ends a block fills the block's unused list slots
@@ -568,6 +579,78 @@ void bf_gemm_scan_kernel(GemmArgs a) {
   }
   // Drain the loads issued past the last stage before the workgroup ends.
   __builtin_amdgcn_s_waitcnt(0);
+}
+
+// ---------------------------------------------------------------------------
+// Device calibration for matrix-core-bound kernels: the rate this device
+// sustains on this scan's register block with no memory traffic (built,
+// like the scan, with the accumulators in AGPRs).  A workgroup of 4 waves (one per SIMD, as the scan runs)
+// repeats k-steps of 16 v_mfma_f32_32x32x16_f16 on a 4 x 4 block of
+// accumulators (256 fp32 per lane, in AGPRs), from two sets of 4 row and
+// 4 query fragments that alternate between k-steps.  With kLds the
+// fragments of every k-step are read from LDS under the previous k-step's
+// MFMAs, one read after each of the first 8 MFMAs, as the scan reads them
+// (rows shared by the 4 waves, query tiles per wave).  The fragments come
+// from the caller's fp16 data: the rate of fp16 MFMA depends on the operand
+// bits it switches, so random data and the scan's own tiles can differ.
+// The sum of the accumulators decides a store that never happens in
+// practice but keeps every MFMA.
+// ---------------------------------------------------------------------------
+constexpr int kCalTiles = 4 + 16;  // fragments of one k-step: 4 row tiles + 16 query tiles (4 per wave)
+constexpr uint32_t kCalVecs = 2u * kCalTiles * 64;  // 16-byte vectors of the two k-steps (40 KiB)
+
+template <bool kLds>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void mfma_rate_kernel(const u32x4* __restrict__ src, uint32_t src_sets, int64_t ksteps, float* __restrict__ sink) {
+  __shared__ u32x4 s_f[kLds ? kCalVecs : 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const u32x4* set = src + uint64_t(blockIdx.x % src_sets) * kCalVecs;
+  // Vector index of fragment (k-step t, row tile r) and (t, this wave's query tile j).
+  auto row_at = [&](int t, int r) { return uint32_t((t * kCalTiles + r) * 64 + lane); };
+  auto qry_at = [&](int t, int j) { return uint32_t((t * kCalTiles + 4 + wave * 4 + j) * 64 + lane); };
+  half8 fa[2][4], fb[2][4];
+  if constexpr (kLds) {
+    for (uint32_t i = threadIdx.x; i < kCalVecs; i += 256) s_f[i] = set[i];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[t][i] = __builtin_bit_cast(half8, kLds ? s_f[row_at(t, i)] : set[row_at(t, i)]);
+      fb[t][i] = __builtin_bit_cast(half8, kLds ? s_f[qry_at(t, i)] : set[qry_at(t, i)]);
+    }
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[r][j][e] = 0.f;
+  for (int64_t s = 0; s < ksteps; s += 2) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        acc[i / 4][i % 4] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[t][i / 4], fb[t][i % 4], acc[i / 4][i % 4], 0, 0, 0);
+        if constexpr (kLds) {
+          // The other set's fragments, re-read for the k-step after next.
+          if (i < 4) fa[t ^ 1][i] = __builtin_bit_cast(half8, s_f[row_at(t ^ 1, i)]);
+          else if (i < 8) fb[t ^ 1][i - 4] = __builtin_bit_cast(half8, s_f[qry_at(t ^ 1, i - 4)]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum += acc[r][j][e];
+  if (sum == 1.2345678e30f) sink[blockIdx.x * 256 + threadIdx.x] = sum;
 }
 
 }  // namespace
@@ -607,3 +690,61 @@ void launch_gemm_scan(cvs_context* ctx, const GemmArgs& args, int n_wg, hipEvent
 
 }  // namespace bf
 }  // namespace cvs
+
+using namespace cvs;
+using namespace cvs::bf;
+
+extern "C" {
+
+int cvs_calibrate_mfma(cvs_context* ctx, const void* fp16_data, size_t data_bytes, int workgroups, int64_t ksteps,
+                       int from_lds, int reps, double* out_tflops) {
+  return guarded([&] {
+    bind(ctx);
+    if (!out_tflops) fail(CVS_ERR_INVALID_ARGUMENT, "null out_tflops");
+    if (!fp16_data) fail(CVS_ERR_INVALID_ARGUMENT, "null fp16_data");
+    if (workgroups < 1 || reps < 1 || ksteps < 2)
+      fail(CVS_ERR_INVALID_ARGUMENT, "workgroups and reps must be positive, ksteps at least 2");
+    if (reinterpret_cast<uintptr_t>(fp16_data) % 16 != 0) fail(CVS_ERR_INVALID_ARGUMENT, "fp16_data must be 16-byte aligned");
+    const size_t set_bytes = size_t(kCalVecs) * 16;
+    const size_t sets = data_bytes / set_bytes;
+    if (sets == 0) fail(CVS_ERR_INVALID_ARGUMENT, "fp16_data must hold at least 40 KiB");
+    const int64_t ks = ksteps + (ksteps & 1);
+    void* sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto cleanup = [&] {
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+      if (sink) (void)hipFree(sink);
+    };
+    try {
+      CVS_HIP(hipMalloc(&sink, size_t(workgroups) * 256 * sizeof(float)));
+      CVS_HIP(hipEventCreate(&e0));
+      CVS_HIP(hipEventCreate(&e1));
+      const uint32_t n_sets = uint32_t(std::min<size_t>(sets, size_t(1) << 20));
+      auto launch = [&] {
+        if (from_lds)
+          hipLaunchKernelGGL(mfma_rate_kernel<true>, dim3(unsigned(workgroups)), dim3(256), 0, ctx->stream,
+                             static_cast<const u32x4*>(fp16_data), n_sets, ks, static_cast<float*>(sink));
+        else
+          hipLaunchKernelGGL(mfma_rate_kernel<false>, dim3(unsigned(workgroups)), dim3(256), 0, ctx->stream,
+                             static_cast<const u32x4*>(fp16_data), n_sets, ks, static_cast<float*>(sink));
+        after_launch("mfma_rate_kernel");
+      };
+      for (int i = 0; i < 2; ++i) launch();  // warm-up
+      CVS_HIP(hipEventRecord(e0, ctx->stream));
+      for (int i = 0; i < reps; ++i) launch();
+      CVS_HIP(hipEventRecord(e1, ctx->stream));
+      CVS_HIP(hipEventSynchronize(e1));
+      float ms = 0.f;
+      CVS_HIP(hipEventElapsedTime(&ms, e0, e1));
+      const double flop = double(workgroups) * 4.0 * double(ks) * 16.0 * (2.0 * 32 * 32 * 16) * reps;
+      *out_tflops = flop / (double(ms) * 1e-3) / 1e12;
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
+  });
+}
+
+}  // extern "C"

@@ -129,6 +129,18 @@ int cvs_calibrate_stream_read(cvs_context* ctx, size_t bytes, int workgroups, in
 int cvs_calibrate_gather_read(cvs_context* ctx, size_t row_bytes, int64_t n_rows, int workgroups, int rows_per_team,
                               int reps, double* out_gbs);
 
+/* Device calibration for matrix-core-bound kernels; no counterpart in the
+ * reference.  `workgroups` workgroups of 4 waves (one per SIMD) each run
+ * `ksteps` (rounded up to even) k-steps of 16 v_mfma_f32_32x32x16_f16 on the
+ * large-batch scan's 4 x 4 block of 32 x 32 accumulators, with fragments
+ * taken from `fp16_data` (device memory, 16-byte aligned, whole 40 KiB
+ * sets, workgroup i using set i mod sets) and held in registers, or, with
+ * from_lds, re-read from LDS every k-step as the scan reads them; `reps`
+ * launches after two warm-up launches.  Returns fp16 dense TFLOP/s, next to
+ * the nominal 2.5 PFLOP/s.  Synchronizes. */
+int cvs_calibrate_mfma(cvs_context* ctx, const void* fp16_data, size_t data_bytes, int workgroups, int64_t ksteps,
+                       int from_lds, int reps, double* out_tflops);
+
 /* ---- device memory helpers (device-resident benchmarking and tests) ----- */
 
 int cvs_device_alloc(cvs_context* ctx, size_t bytes, void** out_ptr);

@@ -1,6 +1,10 @@
-"""Device calibration (cvs_calibrate_stream_read): the achievable
-streaming-read rate that the HBM-bound kernels are compared with."""
+"""Device calibration: the achievable streaming-read and gather rates that
+the HBM-bound kernels are compared with (cvs_calibrate_stream_read,
+cvs_calibrate_gather_read), and the matrix-core rate of the large-batch
+scan's register block (cvs_calibrate_mfma)."""
 import math
+
+import numpy as np
 
 import pytest
 
@@ -30,3 +34,20 @@ def test_gather_read_rate(ctx):
 def test_gather_read_rejects_bad_rows(ctx):
     with pytest.raises(ValueError):
         ctx.calibrate_gather_read(4100, 1000, 64, 8)
+
+
+def test_mfma_rate(cvs, ctx):
+    """The matrix-core loop: a finite rate below the nominal 2.5 PFLOP/s of
+    fp16 dense MFMA, with operands in registers and from LDS; its argument
+    checks."""
+    data = cvs.DeviceArray.from_host(ctx, np.random.default_rng(0).standard_normal((64, 1024)).astype(np.float16))
+    try:
+        for lds in (False, True):
+            tf = ctx.calibrate_mfma(data.ptr, data.nbytes, 256, 4096, from_lds=lds, reps=2)
+            assert math.isfinite(tf) and 100.0 < tf < 2600.0, (lds, tf)
+        with pytest.raises(ValueError, match="40 KiB"):
+            ctx.calibrate_mfma(data.ptr, 1024, 256, 64)
+        with pytest.raises(ValueError):
+            ctx.calibrate_mfma(data.ptr, data.nbytes, 0, 64)
+    finally:
+        data.free()
