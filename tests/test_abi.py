@@ -46,6 +46,9 @@ def test_null_arguments_are_rejected(cvs):
     assert lib.cvs_dataset_shape(None, None, None) == cvs.CVS_ERR_INVALID_ARGUMENT
     assert lib.cvs_context_destroy(None) == cvs.CVS_OK
     assert lib.cvs_dataset_destroy(None) == cvs.CVS_OK
+    out = ctypes.c_double(0)
+    assert lib.cvs_calibrate_mfma(None, None, 0, 1, 2, 0, 1, ctypes.byref(out)) == cvs.CVS_ERR_INVALID_ARGUMENT
+    assert lib.cvs_calibrate_stream_read(None, 1 << 20, 1, 1, ctypes.byref(out)) == cvs.CVS_ERR_INVALID_ARGUMENT
 
 
 def test_no_device_is_an_error_not_a_fallback(cvs):
