@@ -11,14 +11,15 @@
 //  prep     queries fp32 -> fp16 32-row tiles + norms (the dataset layout),
 //           one wave per query.
 //  sample   the scan kernel over an evenly strided sample of 16,384 rows
-//           (65,536 for large batches, 131,072 when the register-blocked
+//           (65,536 for other large batches, 32,768 when the register-blocked
 //           scan of bf_gemm.hip follows); each lane keeps the minimum distance
 //           of the rows it sees, so every (query, workgroup, half-wave)
 //           yields one minimum.
-//  select   per query (one wave), the kp-th smallest of those minima, T0.
-//           The kp smallest minima are kp distinct dataset rows, so at least
-//           kp rows lie at or below T0 and every row above it can be dropped
-//           by the scan.
+//  select   per query (one wave), the r-th smallest of those minima, T0.
+//           The r smallest minima are r distinct dataset rows, so at least r
+//           rows lie at or below T0 and every row above it can be dropped by
+//           the scan.  r is set on the host (plan_bf) so that T0 falls below
+//           the merge's R candidates with probability at most 1e-9.
 //  scan     one persistent workgroup per compute unit streams a contiguous
 //           range of fp16 tiles HBM -> VGPRs -> LDS (double-buffered LDS, two
 //           stages of loads in flight).  Each wave keeps the fp16 operands of
@@ -34,20 +35,22 @@
 //           keys (ballot radix select), lowering the threshold.  Lists of
 //           kp <= 64 live in LDS, kp = 128 lists in global memory.  Each list
 //           ends with its smallest key published for the merge.
-//  merge    one workgroup per query: the kp-th smallest list minimum bounds
-//           the kp-th smallest key.  For kp <= 64 every key within it (at
-//           most kp * kp) is gathered into LDS and one wave keeps the kp
+//  merge    one workgroup per query: the R-th smallest list minimum bounds
+//           the R-th smallest key (R = 2 kp, at most 256).  For kp <= 64 every
+//           key within it is gathered into LDS and one wave keeps the R
 //           smallest; for kp = 128 each wave merges the 64-key rows holding a
-//           key within the bound into its running top-kp.  The kp candidates
+//           key within the bound into its running top-R.  The R candidates
 //           are re-ranked with exact fp32 distances from the fp32 rows,
-//           sorted by (distance, id), and k results written, padded with
-//           UINT32_MAX / +inf (src/cagra.cpp:240-251).
+//           sorted by (distance, id), certified against the fp16 error bound
+//           (bf_common.hpp, Cert; a query that fails is re-ranked over more
+//           rows), and k results written, padded with UINT32_MAX / +inf
+//           (src/cagra.cpp:240-251).
 //
 // The fp16 pass only *selects*; reported distances come from the fp32
 // re-rank, so distances agree with the reference's fp32 loop
-// (src/cagra.cpp:218-226) up to summation order.  kp > k candidates are kept
-// because fp16 inputs perturb |q-x|^2 by up to ~1e-4 absolute at unit norm,
-// far below the gap between rank k and rank kp on the target data.
+// (src/cagra.cpp:218-226) up to summation order, and the certificate makes
+// the selection exact on any finite input: rows and queries are centred and
+// scaled by a power of two before the fp16 conversion (runtime.hip).
 #include <algorithm>
 #include <cmath>
 #include <mutex>
