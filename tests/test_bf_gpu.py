@@ -126,10 +126,10 @@ def test_random_shapes(ctx, oracle, n, d, q, k):
     (20000, 512, 5000, 112),  # 10 query blocks: two per XCD for XCDs 0 and 1, largest k
     (12000, 1024, 1300, 10),  # range-major pipelined scan (64 k-steps), kp = 16 LDS lists
     (12000, 512, 1100, 40),   # range-major pipelined scan (32 k-steps), kp = 64 LDS lists
-    (7000, 384, 1100, 100),   # register-blocked scan at 24 k-steps
-    (5000, 640, 1030, 50),    # 40 k-steps; the last 512-query block holds one 32-query tile
-    (9000, 768, 1200, 112),   # 48 k-steps, largest k
-    (3000, 896, 2100, 77),    # 56 k-steps, 5 query blocks
+    (7000, 384, 1100, 100),   # d 384 padded to 512: 128 zero columns in every tile
+    (5000, 640, 1030, 50),    # d 640 padded to 1024; the last 512-query block holds one 32-query tile
+    (9000, 768, 1200, 112),   # d 768 padded to 1024, largest k
+    (3000, 896, 2100, 77),    # d 896 padded to 1024, 5 query blocks
 ])
 def test_large_batches(ctx, oracle, n, d, q, k):
     rng = np.random.default_rng(q + k)
