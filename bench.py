@@ -201,11 +201,17 @@ def calibrate_copy(mib: int) -> int:
     # The library's own streaming read (cvs_calibrate_stream_read): each
     # workgroup reads one contiguous share with non-temporal 16-byte loads,
     # as the brute-force scan reads its row range.
+    # And its random whole-row gathers (cvs_calibrate_gather_read), the graph
+    # search's access shape: 16-lane teams reading 256-byte segments of rows
+    # picked at random over 100,000 rows, the graph-search configuration's
+    # fp32 rows (4 KiB, a 410 MB set) and fp16 copy (2 KiB, 205 MB).
     cvs = load_package()
     with cvs.Context(0) as ctx:
         stream = {str(g): ctx.calibrate_stream_read(n * 4, g) for g in (256, 512, 1024, 2048, 4096, 8192)}
+        gather = {f"{rb}B_rows": ctx.calibrate_gather_read(rb, 100_000, 1024, 64, reps=10) for rb in (4096, 2048)}
     print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": 5, "read_gbs": read_gbs,
-                      "copy_gbs_read_plus_write": copy_gbs, "stream_read_gbs_by_workgroups": stream}), flush=True)
+                      "copy_gbs_read_plus_write": copy_gbs, "stream_read_gbs_by_workgroups": stream,
+                      "gather_read_gbs_100k_rows": gather}), flush=True)
     return 0
 
 
