@@ -61,6 +61,7 @@ constexpr int kMaxDv = kBigDim / 64;   // float4 per lane and row (fp32 traversa
 constexpr int kMaxDv8 = kBigDim / 128; // 8-column pieces per lane and row (fp16 traversal)
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 struct SearchArgs {
   const float4* rows;     // n rows of dq float4, zero-padded
@@ -132,10 +133,9 @@ __device__ __forceinline__ void merge_into(uint64_t (&top)[E], uint64_t c) {
 // barriers between waves are needed then); the host launches W = 2 for large
 // batches, where the other wave's gathers hide the lead wave's serial work,
 // and W = 4 or 8 when few queries would leave most of the GPU idle.
-// The large-batch fp16 instance (W = 2) asks for four waves per SIMD: at 128
-// VGPRs it spills 80 bytes per lane, but two queries per SIMD in flight
-// instead of one and a half hide more of the lead wave's serial work
-// (Q=10,000 at N=100K: 4.46 -> 4.21 ms; Q=1,000 unchanged).
+// The large-batch fp16 instance (W = 2) runs four waves per SIMD (113 VGPRs):
+// two queries per SIMD in flight instead of one and a half hide more of the
+// lead wave's serial work.
 template <int E, int W, bool F16, bool BIG>
 __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra_search_kernel(SearchArgs a) {
   extern __shared__ uint32_t s_mem[];
@@ -181,10 +181,15 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
   // Query slice of this lane (d <= 1024).  fp32 traversal: float4 columns tp + 16 j of
   // the padded row.  fp16 traversal (and its fp32 re-rank): 8-column pieces
   // tp + 16 j, so that a 16-lane team reads 256 contiguous bytes of an fp16
-  // row (512 of an fp32 row) per piece.
+  // row (512 of an fp32 row) per piece.  The fp16 traversal keeps its slice
+  // of the centred, scaled query in fp16, as the rows are: a piece's
+  // distance is four packed differences and four fp32-accumulating dot2s,
+  // and the slice takes 32 VGPRs instead of 64.  The traversal's distances
+  // only steer the search; the list is re-ranked against the fp32 query and
+  // rows at the end.
   const float* qsrc = a.queries + qi * a.d;
   float4 qv[F16 || BIG ? 1 : kMaxDv];
-  float qh[F16 && !BIG ? kMaxDv8 : 1][8];
+  half8_t qh[F16 && !BIG ? kMaxDv8 : 1];
   if constexpr (BIG) {
   } else if constexpr (!F16) {
 #pragma unroll
@@ -201,13 +206,13 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
     }
   } else {
     // Centred and scaled as the traversal copy is (distances in the
-    // traversal are scale^2 times the squared distance).
+    // traversal are scale^2 times the squared distance), rounded to fp16.
 #pragma unroll
     for (int j = 0; j < kMaxDv8; ++j)
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int64_t c = int64_t(tp + 16 * j) * 8 + t;
-        qh[j][t] = (j < a.dv8 && c < a.d) ? (qsrc[c] - a.mu[c]) * a.scale : 0.f;
+        qh[j][t] = _Float16((j < a.dv8 && c < a.d) ? (qsrc[c] - a.mu[c]) * a.scale : 0.f);
       }
   }
 
@@ -287,14 +292,13 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
 #pragma unroll
       for (int j = 0; j < kMaxDv8; ++j) {
         if (j < a.dv8) {
-          const half8_t h = __builtin_bit_cast(half8_t, x[j]);
-          float p[8];
+          const uint4 qw = __builtin_bit_cast(uint4, qh[j]);
+          const uint32_t qa[4] = {qw.x, qw.y, qw.z, qw.w}, xa[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const float dt = qh[j][t] - float(h[t]);
-            p[t] = dt * dt;
+          for (int t = 0; t < 4; ++t) {
+            const half2_t d2 = __builtin_bit_cast(half2_t, qa[t]) - __builtin_bit_cast(half2_t, xa[t]);
+            acc = __builtin_amdgcn_fdot2(d2, d2, acc, false);
           }
-          acc += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
         }
       }
     } else {
