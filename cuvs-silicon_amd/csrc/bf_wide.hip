@@ -14,9 +14,17 @@
 //          layout is the MFMA operand layout) and four
 //          v_mfma_f32_32x32x16_f16, the loads of the next two k-steps in
 //          flight while the current ones multiply.
-//  select  one workgroup per query: a three-pass radix select (12 + 12 + 8
-//          bits of the keys' order image) finds the R-th smallest key
-//          (R = max(2 k, k + 32)); every row at or below it is re-ranked
+//  select  one workgroup per query finds the R-th smallest key
+//          (R = max(2 k, k + 32)).  First from a sample: the r-th smallest of
+//          up to 16,384 evenly strided keys is a threshold T0 that lies at
+//          or above the R-th smallest key of all with probability at least
+//          1 - 1e-9 (r from the Poisson rule of the fused path's sample);
+//          one pipelined pass over the query's keys collects every (key,
+//          row) at or below T0 into LDS, and a radix select among those
+//          finds the R-th key exactly.  When T0 fell short (fewer than R
+//          keys collected) or too many keys share it, a three-pass radix
+//          select (12 + 12 + 8 bits of the keys' order image) over all keys
+//          finds it instead.  Every row at or below it is re-ranked
 //          exactly in fp32 into a running top k kept in LDS (block bitonic
 //          sort of up to 2,048 keys).  The certificate of the fused path
 //          (Cert, bf_common.hpp) then bounds the exact distance of every row
@@ -26,8 +34,9 @@
 //          needed; a query whose fp16 copy is not finite re-ranks every
 //          row.
 //
-// Bytes per chunk: N * dp * 2 (tiles) + chunk * N * 4 (keys, written and
-// read three times by the select) + the re-ranked rows.
+// Bytes per chunk: N * dp * 2 (tiles) + chunk * N * 4 (keys, written, and
+// read once by the select's collecting pass; three more times when a
+// query falls back to the full radix select) + the re-ranked rows.
 #include <algorithm>
 #include <cmath>
 
@@ -43,6 +52,9 @@ constexpr int kWT = 256;           // threads per workgroup (4 waves)
 constexpr int kChunkQ = 512;       // queries per chunk at most
 constexpr int kAccCap = 2048;      // exact keys held by the select's accumulator
 constexpr int kIdsCap = 4096;      // candidate ids per streaming step (16 keys per thread)
+constexpr int kSampleM = 64;       // sampled keys per thread (16,384 per query at most)
+constexpr int kCandCap = 8192;     // (key, row) candidates collected below the sampled threshold
+constexpr int kCandM = kCandCap / kWT;
 
 struct KeysArgs {
   const u32x4* tiles;   // dataset tiles
@@ -142,6 +154,91 @@ __device__ __forceinline__ void block_sort(uint64_t* s, int p) {
     }
 }
 
+// Bin of the need-th smallest key counted in s_hist[0, nb) (1 <= need <= the
+// count), for every thread of the workgroup: the bin, the keys in lower bins
+// and the keys in the bin.  nb is a multiple of kWT.
+__device__ __forceinline__ void hist_find(const uint32_t* s_hist, int nb, uint32_t need, uint32_t* s_wsum,
+                                          uint32_t* s_sel, uint32_t& bin, uint32_t& lower, uint32_t& inbin) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = nb / kWT;
+  uint32_t mine = 0;
+  for (int b = 0; b < per; ++b) mine += s_hist[tid * per + b];
+  uint32_t incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  uint32_t off = 0;
+  for (int w2 = 0; w2 < wave; ++w2) off += s_wsum[w2];
+  const uint32_t excl = off + incl - mine;
+  if (excl < need && need <= excl + mine) {
+    uint32_t c = excl;
+    for (int b = 0; b < per; ++b) {
+      const uint32_t h = s_hist[tid * per + b];
+      if (need <= c + h) {
+        s_sel[0] = uint32_t(tid * per + b);
+        s_sel[1] = c;
+        s_sel[2] = h;
+        break;
+      }
+      c += h;
+    }
+  }
+  __syncthreads();
+  bin = s_sel[0];
+  lower = s_sel[1];
+  inbin = s_sel[2];
+  __syncthreads();
+}
+
+// The need-th smallest (1 <= need <= the count) order image among keys the
+// threads of the workgroup hold, M per thread (key(m) returns whether the
+// m-th is one, and its order image): three radix passes of 12, 12 and 8 bits
+// with wave-aggregated histogram counts.  tau is that key; below and eq count
+// the keys under it and equal to it.
+template <int M, typename Key>
+__device__ __forceinline__ void select_held(Key key, uint32_t need, uint32_t* s_hist, uint32_t* s_wsum,
+                                            uint32_t* s_sel, uint32_t& tau, uint32_t& below, uint32_t& eq) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t prefix = 0;
+  below = 0;
+  eq = 0;
+  const int shifts[3] = {20, 8, 0}, widths[3] = {12, 12, 8};
+#pragma unroll 1
+  for (int p = 0; p < 3; ++p) {
+    const int sh = shifts[p], w = widths[p], nb = 1 << w, hs = sh + w;
+    for (int i = tid; i < nb; i += kWT) s_hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      bool in;
+      uint32_t o;
+      key(m, in, o);
+      in = in && (hs >= 32 || (o >> hs) == prefix);
+      const uint32_t bin = (o >> sh) & uint32_t(nb - 1);
+      uint64_t todo = __ballot(in);
+      while (todo) {
+        const int leader = __builtin_ctzll(todo);
+        const uint32_t lb = uint32_t(__builtin_amdgcn_readlane(int(bin), leader));
+        const uint64_t same = __ballot(in && bin == lb);
+        if (lane == leader) atomicAdd(&s_hist[lb], uint32_t(popc(same)));
+        todo &= ~same;
+      }
+    }
+    __syncthreads();
+    uint32_t b, lower, inbin;
+    hist_find(s_hist, nb, need, s_wsum, s_sel, b, lower, inbin);
+    prefix = (prefix << w) | b;
+    below += lower;
+    need -= lower;
+    eq = inbin;
+  }
+  tau = prefix;
+}
+
 struct SelectArgs {
   const float* keys;     // [nq][ldk] of the chunk
   int64_t ldk;
@@ -149,6 +246,8 @@ struct SelectArgs {
   int64_t d;
   int q0;                // first query of the chunk
   int R;                 // rank of the radix select
+  int s_count;           // sampled keys per query (0: no sample, full radix select)
+  int s_rank;            // the threshold is the s_rank-th smallest sampled key
   int64_t k;
   const float* rows;     // fp32 rows
   const float* queries;  // fp32 queries of the call
@@ -157,6 +256,8 @@ struct SelectArgs {
 };
 
 __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cert) {
+  extern __shared__ uint64_t s_cand[];  // kCandCap (key << 32 | row) candidates, dynamic LDS
+  __shared__ uint32_t s_ncand;
   __shared__ uint32_t s_hist[4096];
   __shared__ uint64_t s_acc[kAccCap];
   __shared__ uint32_t s_ids[kIdsCap];
@@ -177,9 +278,97 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
   const float qn = cert.qnorms[q];
   const bool finite = qn <= 3.0e38f && cert.rmax <= 3.0e38f;
 
-  // 1. Radix select of the R-th smallest order image among the n keys.
+  // 1. The R-th smallest order image among the n keys, tau.
   uint32_t tau = 0xffffffffu, below = 0, eq = uint32_t(n);
-  if (finite) {
+  // 1a. From a sample: the s_rank-th smallest of s_count evenly strided keys
+  // is the threshold t0; every (key, row) at or below it is collected into
+  // s_cand in one pass (loads of the next step in flight while a step is
+  // tested), and the R-th smallest is selected among those.  Valid when at
+  // least R keys were collected and all of them fit.
+  bool use_cand = false;
+  uint32_t t0 = 0;
+  int ncand = 0;
+  if (finite && a.s_count > 0) {
+    const int S = a.s_count;
+    uint32_t sv[kSampleM];
+#pragma unroll
+    for (int m = 0; m < kSampleM; ++m) {
+      const int j = m * kWT + tid;
+      sv[m] = j < S ? ord_f32(kr[(int64_t(j) * n) / S]) : 0xffffffffu;
+    }
+    uint32_t sb, se;
+    select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
+                          uint32_t(a.s_rank), s_hist, s_wsum, s_sel, t0, sb, se);
+    if (tid == 0) s_ncand = 0;
+    __syncthreads();
+    constexpr int kL = 8;  // float4 of keys per thread and step
+    const float4* kr4 = reinterpret_cast<const float4*>(kr);
+    const int64_t n4 = (n + 3) / 4;
+    float4 cur[kL], nxt[kL];
+    auto load = [&](float4 (&v)[kL], int64_t b4) {
+#pragma unroll
+      for (int u = 0; u < kL; ++u) {
+        const int64_t i4 = b4 + int64_t(u) * kWT + tid;
+        v[u] = i4 < n4 ? kr4[i4] : make_float4(INFINITY, INFINITY, INFINITY, INFINITY);
+      }
+    };
+    load(cur, 0);
+    for (int64_t b4 = 0; b4 < n4; b4 += int64_t(kWT) * kL) {
+      if (b4 + int64_t(kWT) * kL < n4) load(nxt, b4 + int64_t(kWT) * kL);
+      uint32_t bits = 0;
+#pragma unroll
+      for (int u = 0; u < kL; ++u) {
+        const int64_t i0 = (b4 + int64_t(u) * kWT + tid) * 4;
+        const float c[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i0 + e < n && ord_f32(c[e]) <= t0) bits |= 1u << (4 * u + e);
+      }
+      if (__ballot(bits != 0) != 0) {
+        const uint32_t mine = uint32_t(__builtin_popcount(bits));
+        uint32_t incl = mine;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+          if (lane >= o) incl += y;
+        }
+        const uint32_t total = uint32_t(__shfl(int(incl), 63));
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&s_ncand, total);
+        base = uint32_t(__shfl(int(base), 0));
+        uint32_t pos = base + incl - mine;
+        // Static indices only: a register array indexed at run time would
+        // live in scratch memory.
+#pragma unroll
+        for (int u = 0; u < kL; ++u) {
+          const float c[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if ((bits >> (4 * u + e)) & 1u) {
+              const int64_t i = (b4 + int64_t(u) * kWT + tid) * 4 + e;
+              if (pos < uint32_t(kCandCap)) s_cand[pos] = (uint64_t(ord_f32(c[e])) << 32) | uint32_t(i);
+              ++pos;
+            }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kL; ++u) cur[u] = nxt[u];
+    }
+    __syncthreads();
+    ncand = int(s_ncand);
+    if (ncand >= a.R && ncand <= kCandCap) {
+      use_cand = true;
+      select_held<kCandM>(
+          [&](int m, bool& in, uint32_t& o) {
+            const int i = m * kWT + tid;
+            in = i < ncand;
+            o = in ? uint32_t(s_cand[i] >> 32) : 0xffffffffu;
+          },
+          uint32_t(a.R), s_hist, s_wsum, s_sel, tau, below, eq);
+    }
+  }
+  // 1b. Otherwise radix select over all n keys.
+  if (finite && !use_cand) {
     uint32_t prefix = 0;
     int need = a.R;
     below = 0;
@@ -327,7 +516,59 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
     }
   };
 
-  if (finite) {
+  // The same over the collected candidates (every key at or below t0).
+  auto stream_cand = [&](auto take) {
+    for (int base = 0; base < ncand; base += kWT * 16) {
+      uint32_t bits = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int i = base + j * kWT + tid;
+        if (i < ncand && take(uint32_t(s_cand[i] >> 32))) bits |= 1u << j;
+      }
+      const uint32_t mine = uint32_t(__builtin_popcount(bits));
+      uint32_t incl = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+        if (lane >= o) incl += y;
+      }
+      if (lane == 63) s_wsum[wave] = incl;
+      __syncthreads();
+      uint32_t off = 0, total = 0;
+      for (int w2 = 0; w2 < 4; ++w2) {
+        if (w2 < wave) off += s_wsum[w2];
+        total += s_wsum[w2];
+      }
+      uint32_t pos = off + incl - mine;
+      while (bits) {
+        const int j = __builtin_ctz(bits);
+        bits &= bits - 1;
+        s_ids[pos++] = uint32_t(s_cand[base + j * kWT + tid]);
+      }
+      __syncthreads();
+      for (uint32_t done = 0; done < total;) {
+        const int m = int(std::min<uint32_t>(total - done, uint32_t(kAccCap - fill)));
+        for (int c = kExactU * wave; c < m; c += kExactU * 4) {
+          uint32_t id[kExactU];
+#pragma unroll
+          for (int u = 0; u < kExactU; ++u) id[u] = c + u < m ? s_ids[done + c + u] : 0xffffffffu;
+          float dd[kExactU];
+          wave_exact<kExactU>(id, a.rows, n, a.d, qv, vec, dd);
+#pragma unroll
+          for (int u = 0; u < kExactU; ++u)
+            if (lane == u && c + u < m) s_acc[fill + c + u] = (uint64_t(ord_f32(dd[u])) << 32) | id[u];
+        }
+        fill += m;
+        done += uint32_t(m);
+        __syncthreads();
+        if (fill == kAccCap) flush();
+      }
+    }
+  };
+
+  if (use_cand) {
+    stream_cand([&](uint32_t o) { return o <= tau; });
+  } else if (finite) {
     stream([&](uint32_t o) { return o <= tau; });
   } else {
     stream([](uint32_t) { return true; });
@@ -367,7 +608,10 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
   __syncthreads();
   if (s_mode != kCertPass) {
     const uint32_t hi = ord_f32(s_tneed);
-    stream([&](uint32_t o) { return o > tau && o <= hi; });
+    if (use_cand && hi <= t0)
+      stream_cand([&](uint32_t o) { return o > tau && o <= hi; });
+    else
+      stream([&](uint32_t o) { return o > tau && o <= hi; });
     flush();
   }
 
@@ -409,6 +653,31 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   // the fused path keeps, so that the rank gap between the k-th result and
   // the R-th key clears the fp16 error on dense neighbourhoods.
   const int R = int(std::min<int64_t>(ds->n, std::max<int64_t>(2 * k, k + 32)));
+  // Sampled threshold: S evenly strided keys of a query; the r-th smallest
+  // lies below the query's R-th smallest key only if r of the sampled rows
+  // fall among its R nearest, a count close to Poisson with mean
+  // lambda = R * S / n, so r is the smallest rank with
+  // P(Poisson(lambda) >= r) <= 1e-9 (r = R when every key is sampled).
+  // About r * n / S keys then lie at or below it; the sample is used only
+  // when that many, six standard deviations over, fit the candidate list.
+  const int64_t S = std::min<int64_t>(ds->n, int64_t(kSampleM) * kWT);
+  int s_rank = R;
+  if (S < ds->n) {
+    const double lambda = double(R) * double(S) / double(ds->n);
+    double term = std::exp(-lambda), cdf = term;
+    int r = 1;
+    while (1.0 - cdf > 1e-9 && r < S) {
+      term *= lambda / double(r);
+      cdf += term;
+      ++r;
+    }
+    s_rank = r;
+  }
+  const double per = double(ds->n) / double(S);
+  const bool sampled = (double(s_rank) + 6.0 * std::sqrt(double(s_rank))) * per + per <= double(kCandCap);
+  const size_t cand_lds = size_t(kCandCap) * sizeof(uint64_t);
+  CVS_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(wide_select_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, int(cand_lds)));
   for (int64_t c0 = 0; c0 < q; c0 += qc) {
     const int64_t nq = std::min(qc, q - c0);
     KeysArgs ka{};
@@ -432,14 +701,16 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     sa.d = ds->d;
     sa.q0 = int(c0);
     sa.R = R;
+    sa.s_count = sampled ? int(S) : 0;
+    sa.s_rank = s_rank;
     sa.k = k;
     sa.rows = ds->rows;
     sa.queries = queries;
     sa.out_nbr = nbr;
     sa.out_dist = dist;
     const TimerSpan t2 = timer_span(ctx, "bf_merge");
-    hipExtLaunchKernelGGL(wide_select_kernel, dim3(unsigned(nq)), dim3(kWT), 0, ctx->stream, t2.start, t2.stop, 0, sa,
-                          cert);
+    hipExtLaunchKernelGGL(wide_select_kernel, dim3(unsigned(nq)), dim3(kWT), cand_lds, ctx->stream, t2.start, t2.stop,
+                          0, sa, cert);
     after_launch("wide_select_kernel");
   }
 }

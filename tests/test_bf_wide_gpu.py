@@ -1,7 +1,9 @@
 """GPU: brute force beyond the fused scan's limits (d > 1024 or k > 112),
 which the reference's CPU loop (src/cagra.cpp:211-252) handles for any d and
 k.  These calls run the keys-matrix path (bf_wide.hip): fp16 MFMA keys of
-the centred rows, a radix select, the certificate and the exact re-rank.
+the centred rows, a select of the R-th key (a sampled threshold and the
+keys collected below it, or a radix select over every key), the certificate
+and the exact re-rank.
 
 Same gate as tests/test_bf_gpu.py against the oracle's restatement of the
 reference loop: id sets equal except at near-ties of the k-th distance
@@ -100,3 +102,37 @@ def test_wide_integer_ties(ctx, oracle):
     ref_nbr, ref_dist = oracle.bf_exact(base, qs, 150)
     np.testing.assert_array_equal(nbr, ref_nbr)
     np.testing.assert_array_equal(dist, ref_dist)
+
+
+def test_wide_sample_threshold_short(ctx, oracle):
+    """The select's sampled threshold falls short and the full radix select
+    takes over.  With n = 32,768 the sample is every second row (16,384
+    evenly strided keys); here those are exactly the rows near the queries
+    and the odd rows are far, so the threshold (rank ~286 of the sample for
+    R = 400) has only ~286 keys at or below it, fewer than R."""
+    rng = np.random.default_rng(31)
+    n, d, q, k = 32768, 128, 4, 200
+    c = rng.standard_normal(d).astype(np.float32)
+    base = np.empty((n, d), np.float32)
+    base[0::2] = c + 0.5 * rng.standard_normal((n // 2, d)).astype(np.float32)
+    base[1::2] = -30.0 * c + 0.5 * rng.standard_normal((n // 2, d)).astype(np.float32)
+    qs = c + 0.5 * rng.standard_normal((q, d)).astype(np.float32)
+    nbr, _ = run(ctx, oracle, base, qs, k)
+    assert (nbr % 2 == 0).all()
+
+
+def test_wide_sample_threshold_crowded(ctx, oracle):
+    """More keys tie at the sampled threshold than the candidate list holds
+    (8,192): 10,000 identical integer rows, each at distance 0 from the
+    query; the full radix select takes over and ties resolve by id."""
+    rng = np.random.default_rng(32)
+    n, d, q, k = 20000, 128, 2, 150
+    v = rng.integers(-3, 4, d).astype(np.float32)
+    base = rng.integers(-3, 4, (n, d)).astype(np.float32)
+    base[:10000] = v
+    qs = np.stack([v, v])
+    nbr, dist = ctx.dataset(base).bf_search(qs, k)
+    ref_nbr, ref_dist = oracle.bf_exact(base, qs, k)
+    np.testing.assert_array_equal(nbr, ref_nbr)
+    np.testing.assert_array_equal(dist, ref_dist)
+    assert (nbr == np.arange(k)).all() and (dist == 0).all()
