@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
                                                         0);
     }
   };
-  // ks is a power of two >= 2 (the padded dimension is 32 * 2^j).
+  // ks is even (the padded dimension is a multiple of 32).
   load(0, 0);
   for (int s = 0; s < a.ks; s += 4) {
     if (s + 2 < a.ks) load(1, s + 2);
@@ -294,65 +294,84 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 #pragma unroll
     for (int m = 0; m < kSampleM; ++m) {
       const int j = m * kWT + tid;
-      sv[m] = j < S ? ord_f32(kr[(int64_t(j) * n) / S]) : 0xffffffffu;
+      // Unconditional loads (index clamped, value masked after): a load
+      // under a lane condition is waited for before the next is issued.
+      const uint32_t o = ord_f32(kr[(int64_t(j < S ? j : S - 1) * n) / S]);
+      sv[m] = j < S ? o : 0xffffffffu;
     }
     uint32_t sb, se;
     select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
                           uint32_t(a.s_rank), s_hist, s_wsum, s_sel, t0, sb, se);
     if (tid == 0) s_ncand = 0;
     __syncthreads();
-    constexpr int kL = 8;  // float4 of keys per thread and step
+    constexpr int kL = 16;  // float4 of keys per thread and step
     const float4* kr4 = reinterpret_cast<const float4*>(kr);
-    const int64_t n4 = (n + 3) / 4;
-    float4 cur[kL], nxt[kL];
+    const int64_t n4 = (n + 3) / 4, st = int64_t(kWT) * kL;
+    // Indices clamped to the last float4 and keys past n masked by the
+    // test: no load sits under a lane condition (each such load would be
+    // waited for before the next is issued).
     auto load = [&](float4 (&v)[kL], int64_t b4) {
 #pragma unroll
       for (int u = 0; u < kL; ++u) {
         const int64_t i4 = b4 + int64_t(u) * kWT + tid;
-        v[u] = i4 < n4 ? kr4[i4] : make_float4(INFINITY, INFINITY, INFINITY, INFINITY);
+        v[u] = kr4[i4 < n4 ? i4 : n4 - 1];
       }
     };
-    load(cur, 0);
-    for (int64_t b4 = 0; b4 < n4; b4 += int64_t(kWT) * kL) {
-      if (b4 + int64_t(kWT) * kL < n4) load(nxt, b4 + int64_t(kWT) * kL);
-      uint32_t bits = 0;
+    auto collect = [&](const float4 (&v)[kL], int64_t b4) {
+      uint64_t bits = 0;
 #pragma unroll
       for (int u = 0; u < kL; ++u) {
         const int64_t i0 = (b4 + int64_t(u) * kWT + tid) * 4;
-        const float c[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+        const float c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // Both tests evaluated (no short circuit): a branch here would make
+          // the compiler wait for every outstanding load.
+          const bool hit = (ord_f32(c[e]) <= t0) & (i0 + e < n);
+          bits |= uint64_t(hit) << (4 * u + e);
+        }
+      }
+      if (__ballot(bits != 0) == 0) return;
+      const uint32_t mine = uint32_t(__builtin_popcountll(bits));
+      uint32_t incl = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+        if (lane >= o) incl += y;
+      }
+      const uint32_t total = uint32_t(__shfl(int(incl), 63));
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&s_ncand, total);
+      base = uint32_t(__shfl(int(base), 0));
+      uint32_t pos = base + incl - mine;
+      // Static indices only: a register array indexed at run time would
+      // live in scratch memory.
+#pragma unroll
+      for (int u = 0; u < kL; ++u) {
+        const float c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (i0 + e < n && ord_f32(c[e]) <= t0) bits |= 1u << (4 * u + e);
+          if ((bits >> (4 * u + e)) & 1u) {
+            const int64_t i = (b4 + int64_t(u) * kWT + tid) * 4 + e;
+            if (pos < uint32_t(kCandCap)) s_cand[pos] = (uint64_t(ord_f32(c[e])) << 32) | uint32_t(i);
+            ++pos;
+          }
       }
-      if (__ballot(bits != 0) != 0) {
-        const uint32_t mine = uint32_t(__builtin_popcount(bits));
-        uint32_t incl = mine;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t y = uint32_t(__shfl_up(int(incl), o));
-          if (lane >= o) incl += y;
-        }
-        const uint32_t total = uint32_t(__shfl(int(incl), 63));
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(&s_ncand, total);
-        base = uint32_t(__shfl(int(base), 0));
-        uint32_t pos = base + incl - mine;
-        // Static indices only: a register array indexed at run time would
-        // live in scratch memory.
-#pragma unroll
-        for (int u = 0; u < kL; ++u) {
-          const float c[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if ((bits >> (4 * u + e)) & 1u) {
-              const int64_t i = (b4 + int64_t(u) * kWT + tid) * 4 + e;
-              if (pos < uint32_t(kCandCap)) s_cand[pos] = (uint64_t(ord_f32(c[e])) << 32) | uint32_t(i);
-              ++pos;
-            }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kL; ++u) cur[u] = nxt[u];
+    };
+    // Two register buffers in turn: while one step's keys are tested, the
+    // next step's loads are in flight (no copies between the buffers, which
+    // would wait for those loads).
+    // The scheduling barriers keep the compiler from sinking a buffer's
+    // loads below the test of the other one.
+    float4 va[kL], vb[kL];
+    load(va, 0);
+    for (int64_t b4 = 0; b4 < n4; b4 += 2 * st) {
+      load(vb, b4 + st);
+      __builtin_amdgcn_sched_barrier(0);
+      collect(va, b4);
+      load(va, b4 + 2 * st);
+      __builtin_amdgcn_sched_barrier(0);
+      collect(vb, b4 + st);
     }
     __syncthreads();
     ncand = int(s_ncand);
@@ -380,7 +399,7 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
       __syncthreads();
       const int hs = sh + w;  // bits above this pass must equal the prefix
       // 16 keys per thread and step as four 16-byte loads (the row starts
-      // 128-byte aligned; keys past n are masked).  Keys crowd into few
+      // 128-byte aligned; indices clamped, keys past n masked).  Keys crowd into few
       // bins (distances of one query span few exponents), so each wave
       // counts its keys bin by bin: the lowest pending lane's bin, the
       // ballot of the lanes holding it, one atomic for all of them.
@@ -391,7 +410,7 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int64_t i4 = b4 + int64_t(u) * kWT + tid;
-          v[u] = i4 < n4 ? kr4[i4] : make_float4(INFINITY, INFINITY, INFINITY, INFINITY);
+          v[u] = kr4[i4 < n4 ? i4 : n4 - 1];  // clamped; keys past n are masked below
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -473,7 +492,8 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int64_t i = base + int64_t(j) * kWT + tid;
-        if (i < n && take(ord_f32(kr[i]))) bits |= 1u << j;
+        const uint32_t o = ord_f32(kr[i < n ? i : n - 1]);  // unconditional load
+        if (i < n && take(o)) bits |= 1u << j;
       }
       const uint32_t mine = uint32_t(__builtin_popcount(bits));
       uint32_t incl = mine;

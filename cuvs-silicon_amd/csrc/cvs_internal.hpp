@@ -100,7 +100,7 @@ struct cvs_dataset {
   cvs_context* ctx = nullptr;
   int64_t n = 0;          // rows
   int64_t d = 0;          // dimensions
-  int64_t dp = 0;         // padded dimensions (32 * power of two)
+  int64_t dp = 0;         // padded dimensions (padded_dim)
   int64_t n_tiles = 0;    // 32-row tiles, padded to a multiple of kTilePad
   float* rows = nullptr;          // n x d fp32, row-major
   uint16_t* tiles = nullptr;      // n_tiles x (dp/16) x 64 lanes x 8 fp16 of scale * (row - mu)
@@ -182,7 +182,11 @@ constexpr int kStepBytes = 1024;
 constexpr int kTilePad = 64;
 constexpr int kNormSlack = 256;  // floats allocated past the last tile's norms
 
+// Padded dimensions of a dataset's tiles: 32 times a power of two up to 1024
+// (the fused scan is instantiated per k-step count), a multiple of 64 beyond
+// (only the keys-matrix path reads those, four k-steps at a time).
 inline int64_t padded_dim(int64_t d) {
+  if (d > 1024) return (d + 63) / 64 * 64;
   int64_t p = 32;
   while (p < d) p *= 2;
   return p;
