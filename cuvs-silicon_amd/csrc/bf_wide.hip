@@ -72,47 +72,82 @@ struct KeysArgs {
 // tile 4 bx + w with the query tiles qt0 + 4 by + j, j = 0..3.  Lane l holds,
 // for query tile j, query 32 (qt0 + 4 by + j) + l % 32 against rows
 // 32 t + 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
+//
+// The k-steps run in blocks of KB (8; 4 or 2 for the 64- and 32-column
+// padded dimensions).  The four waves share the query tiles:
+// each block's 32 fragments (k-step, query tile; 1 KiB each) are loaded once
+// per workgroup (wave w loads query tile w) into one of two LDS buffers,
+// and every wave reads them from there.  Each wave's own dataset fragments
+// for the next block are loaded into the other of two register sets while
+// the current block multiplies, so that a whole block of loads (8 KiB per
+// wave) is in flight behind the matrix cores.
+template <int kKB>
 __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
+  __shared__ u32x4 s_b[2][kKB * 4 * 64];  // [buffer][k-step * 4 + query tile][lane]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t t = int64_t(blockIdx.x) * 4 + wave;
   const int qtb = a.qt0 + int(blockIdx.y) * 4;
   const int64_t tstep = int64_t(a.ks) * 64;  // u32x4 per tile
   const u32x4* A = a.tiles + t * tstep + lane;
-  const u32x4* B = a.qtiles + int64_t(qtb) * tstep + lane;
+  const u32x4* Bg = a.qtiles + int64_t(qtb + wave) * tstep + lane;
+  const int nb = a.ks / kKB;
   f32x16 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
 
-  // Two k-steps per group; group g + 1 is loaded before group g multiplies.
-  u32x4 ra[2][2], rb[2][2][4];
-  auto load = [&](int buf, int s0) {
+  u32x4 aa[kKB], ab[kKB], bs[kKB];
+  auto load_a = [&](u32x4 (&v)[kKB], int blk) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int s = s0 + u;
-      ra[buf][u] = A[int64_t(s) * 64];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) rb[buf][u][j] = B[int64_t(j) * tstep + int64_t(s) * 64];
-    }
+    for (int s = 0; s < kKB; ++s) v[s] = A[int64_t(blk * kKB + s) * 64];
   };
-  auto mult = [&](int buf) {
+  auto load_b = [&](int blk) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const half8 av = __builtin_bit_cast(half8, ra[buf][u]);
+    for (int s = 0; s < kKB; ++s) bs[s] = Bg[int64_t(blk * kKB + s) * 64];
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < kKB; ++s) s_b[buf][(s * 4 + wave) * 64 + lane] = bs[s];
+  };
+  auto mult = [&](const u32x4 (&v)[kKB], int buf) {
+#pragma unroll
+    for (int s = 0; s < kKB; ++s) {
+      const half8 av = __builtin_bit_cast(half8, v[s]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, __builtin_bit_cast(half8, rb[buf][u][j]), acc[j], 0, 0,
-                                                        0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            av, __builtin_bit_cast(half8, s_b[buf][(s * 4 + j) * 64 + lane]), acc[j], 0, 0, 0);
     }
   };
-  // ks is even (the padded dimension is a multiple of 32).
-  load(0, 0);
-  for (int s = 0; s < a.ks; s += 4) {
-    if (s + 2 < a.ks) load(1, s + 2);
-    mult(0);
-    if (s + 4 < a.ks) load(0, s + 4);
-    if (s + 2 < a.ks) mult(1);
+  // Blocks in pairs: register set aa and LDS buffer 0 for even blocks, ab
+  // and buffer 1 for odd ones.  Loads are issued unconditionally (block
+  // index clamped to the last block; the repeated loads of the last pair hit
+  // the cache): a load under a branch, even a uniform one, makes the
+  // compiler wait at the join for nearly every load in flight.  The
+  // scheduling barriers keep a block's loads ahead of the previous block's
+  // products; the workgroup barrier after a block both publishes the next
+  // block's query fragments and retires the buffer just read before it is
+  // written again.
+  load_b(0);
+  load_a(aa, 0);
+  store_b(0);
+  __syncthreads();
+  for (int blk = 0; blk < nb; blk += 2) {
+    const int b1 = blk + 1 < nb ? blk + 1 : nb - 1;
+    const int b2 = blk + 2 < nb ? blk + 2 : nb - 1;
+    load_b(b1);
+    load_a(ab, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mult(aa, 0);
+    store_b(1);
+    __syncthreads();
+    load_b(b2);
+    load_a(aa, b2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (blk + 1 < nb) mult(ab, 1);
+    store_b(0);
+    __syncthreads();
   }
 
   const int half = lane >> 5;
@@ -648,6 +683,10 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
                     uint32_t* nbr, float* dist) {
   const int ks = int(ds->dp / kStepCols);
+  // k-steps per block of the keys kernel: 8 (padded dimensions of 128 and
+  // more are multiples of 128), else the whole of 2 or 4.
+  const int kb = ks % 8 == 0 ? 8 : ks;
+  if (kb != 8 && kb != 4 && kb != 2) fail(CVS_ERR_RUNTIME, "bf_wide_search: unexpected padded dimension");
   const int64_t q_tiles4 = ((q + 31) / 32 + 3) / 4 * 4;
   const int64_t ldk = ds->n_tiles * kTileRows;
   // Queries per chunk: a multiple of 128, at most 512, keys within ~2 GiB.
@@ -711,8 +750,13 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     ka.keys = keys;
     ka.ldk = ldk;
     const TimerSpan t1 = timer_span(ctx, "bf_scan");
-    hipExtLaunchKernelGGL(wide_keys_kernel, dim3(unsigned(ds->n_tiles / 4), unsigned((nq + 127) / 128)), dim3(kWT),
-                          0, ctx->stream, t1.start, t1.stop, 0, ka);
+    const dim3 kgrid(unsigned(ds->n_tiles / 4), unsigned((nq + 127) / 128));
+    if (kb == 8)
+      hipExtLaunchKernelGGL(wide_keys_kernel<8>, kgrid, dim3(kWT), 0, ctx->stream, t1.start, t1.stop, 0, ka);
+    else if (kb == 4)
+      hipExtLaunchKernelGGL(wide_keys_kernel<4>, kgrid, dim3(kWT), 0, ctx->stream, t1.start, t1.stop, 0, ka);
+    else
+      hipExtLaunchKernelGGL(wide_keys_kernel<2>, kgrid, dim3(kWT), 0, ctx->stream, t1.start, t1.stop, 0, ka);
     after_launch("wide_keys_kernel");
     SelectArgs sa{};
     sa.keys = keys;
