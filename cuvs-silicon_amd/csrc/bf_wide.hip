@@ -65,7 +65,17 @@ struct KeysArgs {
   int qt0;              // first query tile of the chunk
   int nq;               // queries of the chunk
   float* keys;          // [nq][ldk]
-  int64_t ldk;          // padded rows (n_tiles * 32)
+  int64_t ldk;          // keys per query row (32 per tile index)
+  int64_t n_idx;        // tile indices of this launch (indices past it repeat the last)
+  int64_t tile_stride;  // tile index i multiplies dataset tile i * tile_stride
+  int64_t n;            // dataset rows
+  // Collection (t0 null: none): every key of query ql at or below the order
+  // image t0[ql], with its row, is appended to cand[ql * cand_cap ...] at a
+  // slot taken from cnt[ql] (slots past cand_cap are counted, not written).
+  const uint32_t* t0;
+  uint32_t* cnt;
+  uint64_t* cand;
+  int cand_cap;
 };
 
 // Block (dataset tile group bx, query block by): wave w multiplies dataset
@@ -85,7 +95,8 @@ template <int kKB>
 __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
   __shared__ u32x4 s_b[2][kKB * 4 * 64];  // [buffer][k-step * 4 + query tile][lane]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t t = int64_t(blockIdx.x) * 4 + wave;
+  const int64_t idx = int64_t(blockIdx.x) * 4 + wave;                    // tile index (key columns)
+  const int64_t t = (idx < a.n_idx ? idx : a.n_idx - 1) * a.tile_stride;  // dataset tile
   const int qtb = a.qt0 + int(blockIdx.y) * 4;
   const int64_t tstep = int64_t(a.ks) * 64;  // u32x4 per tile
   const u32x4* A = a.tiles + t * tstep + lane;
@@ -160,16 +171,40 @@ __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
     const int ql = (qtb + j) * 32 + (lane & 31) - a.qt0 * 32;  // query of the chunk
     if (ql >= a.nq) continue;
     const float qn = a.qnorms[a.qt0 * 32 + ql];
-    float* dst = a.keys + int64_t(ql) * a.ldk + row0 + 4 * half;
+    float* dst = a.keys + int64_t(ql) * a.ldk + idx * 32 + 4 * half;
+    f32x4 v[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      f32x4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = qn + xn[g][e] - 2.0f * acc[j][4 * g + e];
-      *reinterpret_cast<f32x4*>(dst + 8 * g) = v;
+      for (int e = 0; e < 4; ++e) v[g][e] = qn + xn[g][e] - 2.0f * acc[j][4 * g + e];
+      *reinterpret_cast<f32x4*>(dst + 8 * g) = v[g];
+    }
+    if (a.t0) {
+      // Row of v[g][e]: row0 + 8 g + 4 half + e (padding rows excluded).
+      const uint32_t th = a.t0[ql];
+      uint32_t hits = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          hits |= uint32_t((ord_f32(v[g][e]) <= th) & (row0 + 8 * g + 4 * half + e < a.n)) << (4 * g + e);
+      if (hits) {
+        uint32_t pos = atomicAdd(&a.cnt[ql], uint32_t(__builtin_popcount(hits)));
+        uint64_t* out = a.cand + int64_t(ql) * a.cand_cap;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if ((hits >> (4 * g + e)) & 1u) {
+              if (pos < uint32_t(a.cand_cap))
+                out[pos] = (uint64_t(ord_f32(v[g][e])) << 32) | uint32_t(row0 + 8 * g + 4 * half + e);
+              ++pos;
+            }
+      }
     }
   }
 }
+
 
 // Ascending bitonic sort of s[0..p) (p a power of two, <= kAccCap) by the
 // whole workgroup.
@@ -274,6 +309,34 @@ __device__ __forceinline__ void select_held(Key key, uint32_t need, uint32_t* s_
   tau = prefix;
 }
 
+// Per query of a chunk: the s_rank-th smallest order image among its S
+// sampled keys (skeys[ql * lds ...], S <= kSampleM * kWT), into t0[ql]; and
+// cnt[ql] = 0 for the collection that follows.
+__global__ __launch_bounds__(256) void wide_threshold_kernel(const float* skeys, int64_t lds, int S, int s_rank,
+                                                             uint32_t* t0, uint32_t* cnt) {
+  __shared__ uint32_t s_hist[4096];
+  __shared__ uint32_t s_wsum[4];
+  __shared__ uint32_t s_sel[4];
+  const int tid = threadIdx.x;
+  const float* kr = skeys + int64_t(blockIdx.x) * lds;
+  uint32_t sv[kSampleM];
+#pragma unroll
+  for (int m = 0; m < kSampleM; ++m) {
+    const int j = m * kWT + tid;
+    // Unconditional loads (index clamped, value masked after): a load under
+    // a lane condition is waited for before the next is issued.
+    const uint32_t o = ord_f32(kr[j < S ? j : S - 1]);
+    sv[m] = j < S ? o : 0xffffffffu;
+  }
+  uint32_t tau, below, eq;
+  select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
+                        uint32_t(s_rank), s_hist, s_wsum, s_sel, tau, below, eq);
+  if (tid == 0) {
+    t0[blockIdx.x] = tau;
+    cnt[blockIdx.x] = 0;
+  }
+}
+
 struct SelectArgs {
   const float* keys;     // [nq][ldk] of the chunk
   int64_t ldk;
@@ -281,8 +344,12 @@ struct SelectArgs {
   int64_t d;
   int q0;                // first query of the chunk
   int R;                 // rank of the radix select
-  int s_count;           // sampled keys per query (0: no sample, full radix select)
-  int s_rank;            // the threshold is the s_rank-th smallest sampled key
+  // Keys collected below a sampled threshold by the keys kernel (cand null:
+  // none): t0, cnt and cand of KeysArgs, per query of the chunk.
+  const uint32_t* t0;
+  const uint32_t* cnt;
+  const uint64_t* cand;
+  int cand_cap;
   int64_t k;
   const float* rows;     // fp32 rows
   const float* queries;  // fp32 queries of the call
@@ -292,7 +359,6 @@ struct SelectArgs {
 
 __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cert) {
   extern __shared__ uint64_t s_cand[];  // kCandCap (key << 32 | row) candidates, dynamic LDS
-  __shared__ uint32_t s_ncand;
   __shared__ uint32_t s_hist[4096];
   __shared__ uint64_t s_acc[kAccCap];
   __shared__ uint32_t s_ids[kIdsCap];
@@ -315,102 +381,21 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 
   // 1. The R-th smallest order image among the n keys, tau.
   uint32_t tau = 0xffffffffu, below = 0, eq = uint32_t(n);
-  // 1a. From a sample: the s_rank-th smallest of s_count evenly strided keys
-  // is the threshold t0; every (key, row) at or below it is collected into
-  // s_cand in one pass (loads of the next step in flight while a step is
-  // tested), and the R-th smallest is selected among those.  Valid when at
-  // least R keys were collected and all of them fit.
+  // 1a. From the collected keys: every (key, row) at or below the query's
+  // sampled threshold t0, when there are at least R of them and all fit the
+  // list, contains the R smallest keys and every key tied with the R-th.
+  // They are copied to s_cand and the R-th is selected among them.
   bool use_cand = false;
   uint32_t t0 = 0;
   int ncand = 0;
-  if (finite && a.s_count > 0) {
-    const int S = a.s_count;
-    uint32_t sv[kSampleM];
-#pragma unroll
-    for (int m = 0; m < kSampleM; ++m) {
-      const int j = m * kWT + tid;
-      // Unconditional loads (index clamped, value masked after): a load
-      // under a lane condition is waited for before the next is issued.
-      const uint32_t o = ord_f32(kr[(int64_t(j < S ? j : S - 1) * n) / S]);
-      sv[m] = j < S ? o : 0xffffffffu;
-    }
-    uint32_t sb, se;
-    select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
-                          uint32_t(a.s_rank), s_hist, s_wsum, s_sel, t0, sb, se);
-    if (tid == 0) s_ncand = 0;
-    __syncthreads();
-    constexpr int kL = 16;  // float4 of keys per thread and step
-    const float4* kr4 = reinterpret_cast<const float4*>(kr);
-    const int64_t n4 = (n + 3) / 4, st = int64_t(kWT) * kL;
-    // Indices clamped to the last float4 and keys past n masked by the
-    // test: no load sits under a lane condition (each such load would be
-    // waited for before the next is issued).
-    auto load = [&](float4 (&v)[kL], int64_t b4) {
-#pragma unroll
-      for (int u = 0; u < kL; ++u) {
-        const int64_t i4 = b4 + int64_t(u) * kWT + tid;
-        v[u] = kr4[i4 < n4 ? i4 : n4 - 1];
-      }
-    };
-    auto collect = [&](const float4 (&v)[kL], int64_t b4) {
-      uint64_t bits = 0;
-#pragma unroll
-      for (int u = 0; u < kL; ++u) {
-        const int64_t i0 = (b4 + int64_t(u) * kWT + tid) * 4;
-        const float c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // Both tests evaluated (no short circuit): a branch here would make
-          // the compiler wait for every outstanding load.
-          const bool hit = (ord_f32(c[e]) <= t0) & (i0 + e < n);
-          bits |= uint64_t(hit) << (4 * u + e);
-        }
-      }
-      if (__ballot(bits != 0) == 0) return;
-      const uint32_t mine = uint32_t(__builtin_popcountll(bits));
-      uint32_t incl = mine;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = uint32_t(__shfl_up(int(incl), o));
-        if (lane >= o) incl += y;
-      }
-      const uint32_t total = uint32_t(__shfl(int(incl), 63));
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&s_ncand, total);
-      base = uint32_t(__shfl(int(base), 0));
-      uint32_t pos = base + incl - mine;
-      // Static indices only: a register array indexed at run time would
-      // live in scratch memory.
-#pragma unroll
-      for (int u = 0; u < kL; ++u) {
-        const float c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if ((bits >> (4 * u + e)) & 1u) {
-            const int64_t i = (b4 + int64_t(u) * kWT + tid) * 4 + e;
-            if (pos < uint32_t(kCandCap)) s_cand[pos] = (uint64_t(ord_f32(c[e])) << 32) | uint32_t(i);
-            ++pos;
-          }
-      }
-    };
-    // Two register buffers in turn: while one step's keys are tested, the
-    // next step's loads are in flight (no copies between the buffers, which
-    // would wait for those loads).
-    // The scheduling barriers keep the compiler from sinking a buffer's
-    // loads below the test of the other one.
-    float4 va[kL], vb[kL];
-    load(va, 0);
-    for (int64_t b4 = 0; b4 < n4; b4 += 2 * st) {
-      load(vb, b4 + st);
-      __builtin_amdgcn_sched_barrier(0);
-      collect(va, b4);
-      load(va, b4 + 2 * st);
-      __builtin_amdgcn_sched_barrier(0);
-      collect(vb, b4 + st);
-    }
-    __syncthreads();
-    ncand = int(s_ncand);
-    if (ncand >= a.R && ncand <= kCandCap) {
+  if (finite && a.cand) {
+    const uint32_t nc = a.cnt[ql];
+    t0 = a.t0[ql];
+    if (nc >= uint32_t(a.R) && nc <= uint32_t(a.cand_cap) && nc <= uint32_t(kCandCap)) {
+      ncand = int(nc);
+      const uint64_t* src = a.cand + ql * a.cand_cap;
+      for (int i = tid; i < ncand; i += kWT) s_cand[i] = src[i];
+      __syncthreads();
       use_cand = true;
       select_held<kCandM>(
           [&](int m, bool& in, uint32_t& o) {
@@ -571,7 +556,7 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
     }
   };
 
-  // The same over the collected candidates (every key at or below t0).
+  // The same over the collected keys (every key at or below t0).
   auto stream_cand = [&](auto take) {
     for (int base = 0; base < ncand; base += kWT * 16) {
       uint32_t bits = 0;
@@ -698,30 +683,26 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   const size_t off_qe = off_qn + align(size_t(q_tiles4) * 32 * sizeof(float));
   const size_t off_keys = off_qe + align(size_t(q) * sizeof(float));
   const size_t total = off_keys + align(size_t(qc) * size_t(ldk) * sizeof(float));
-  ctx->ws_search.reserve(total);
-  char* ws = ctx->ws_search.as<char>();
-  u32x4* qtiles = reinterpret_cast<u32x4*>(ws);
-  float* qnorms = reinterpret_cast<float*>(ws + off_qn);
-  float* qerr = reinterpret_cast<float*>(ws + off_qe);
-  float* keys = reinterpret_cast<float*>(ws + off_keys);
 
-  const TimerSpan t0 = timer_span(ctx, "bf_prep");
-  launch_query_tiles(ctx, ds, queries, q, q_tiles4 * 32, qtiles, qnorms, qerr, t0.start, t0.stop);
-  const Cert cert = make_cert(ctx, ds, qnorms, qerr);
   // Rows re-ranked before the certificate: twice k (at least k + 32), as
   // the fused path keeps, so that the rank gap between the k-th result and
   // the R-th key clears the fp16 error on dense neighbourhoods.
   const int R = int(std::min<int64_t>(ds->n, std::max<int64_t>(2 * k, k + 32)));
-  // Sampled threshold: S evenly strided keys of a query; the r-th smallest
-  // lies below the query's R-th smallest key only if r of the sampled rows
-  // fall among its R nearest, a count close to Poisson with mean
-  // lambda = R * S / n, so r is the smallest rank with
-  // P(Poisson(lambda) >= r) <= 1e-9 (r = R when every key is sampled).
-  // About r * n / S keys then lie at or below it; the sample is used only
-  // when that many, six standard deviations over, fit the candidate list.
-  const int64_t S = std::min<int64_t>(ds->n, int64_t(kSampleM) * kWT);
+  // Sampled threshold: the keys of S_tiles evenly strided dataset tiles
+  // (S = 32 S_tiles rows, at most 16,384); the r-th smallest lies below the
+  // query's R-th smallest key only if r of the sampled rows fall among its R
+  // nearest, a count close to Poisson with mean lambda = R * S / n, so r is
+  // the smallest rank with P(Poisson(lambda) >= r) <= 1e-9 (r = R when every
+  // tile is sampled).  About r * n / S keys then lie at or below it; the
+  // sample is used only when that many, six standard deviations over, fit
+  // the candidate list.
+  const int64_t real_tiles = (ds->n + kTileRows - 1) / kTileRows;
+  const int64_t s_tiles = std::min<int64_t>(real_tiles, int64_t(kSampleM) * kWT / kTileRows);
+  const int64_t s_stride = real_tiles / s_tiles;
+  const int64_t S = s_tiles * kTileRows;
+  const int64_t s_ld = (s_tiles + 3) / 4 * 4 * kTileRows;  // sample keys per query row
   int s_rank = R;
-  if (S < ds->n) {
+  if (s_tiles < real_tiles) {
     const double lambda = double(R) * double(S) / double(ds->n);
     double term = std::exp(-lambda), cdf = term;
     int r = 1;
@@ -734,11 +715,42 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   }
   const double per = double(ds->n) / double(S);
   const bool sampled = (double(s_rank) + 6.0 * std::sqrt(double(s_rank))) * per + per <= double(kCandCap);
+
+  const size_t off_skeys = total;
+  const size_t off_t0 = off_skeys + (sampled ? align(size_t(qc) * size_t(s_ld) * sizeof(float)) : 0);
+  const size_t off_cnt = off_t0 + (sampled ? align(size_t(qc) * sizeof(uint32_t)) : 0);
+  const size_t off_cand = off_cnt + (sampled ? align(size_t(qc) * sizeof(uint32_t)) : 0);
+  const size_t total_all = off_cand + (sampled ? align(size_t(qc) * kCandCap * sizeof(uint64_t)) : 0);
+  ctx->ws_search.reserve(total_all);
+  char* ws = ctx->ws_search.as<char>();
+  u32x4* qtiles = reinterpret_cast<u32x4*>(ws);
+  float* qnorms = reinterpret_cast<float*>(ws + off_qn);
+  float* qerr = reinterpret_cast<float*>(ws + off_qe);
+  float* keys = reinterpret_cast<float*>(ws + off_keys);
+  float* skeys = sampled ? reinterpret_cast<float*>(ws + off_skeys) : nullptr;
+  uint32_t* t0s = sampled ? reinterpret_cast<uint32_t*>(ws + off_t0) : nullptr;
+  uint32_t* cnt = sampled ? reinterpret_cast<uint32_t*>(ws + off_cnt) : nullptr;
+  uint64_t* cand = sampled ? reinterpret_cast<uint64_t*>(ws + off_cand) : nullptr;
+
+  const TimerSpan t0 = timer_span(ctx, "bf_prep");
+  launch_query_tiles(ctx, ds, queries, q, q_tiles4 * 32, qtiles, qnorms, qerr, t0.start, t0.stop);
+  const Cert cert = make_cert(ctx, ds, qnorms, qerr);
+
   const size_t cand_lds = size_t(kCandCap) * sizeof(uint64_t);
   CVS_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(wide_select_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, int(cand_lds)));
+  auto launch_keys = [&](dim3 grid, const KeysArgs& ka, hipEvent_t e0, hipEvent_t e1) {
+    if (kb == 8)
+      hipExtLaunchKernelGGL(wide_keys_kernel<8>, grid, dim3(kWT), 0, ctx->stream, e0, e1, 0, ka);
+    else if (kb == 4)
+      hipExtLaunchKernelGGL(wide_keys_kernel<4>, grid, dim3(kWT), 0, ctx->stream, e0, e1, 0, ka);
+    else
+      hipExtLaunchKernelGGL(wide_keys_kernel<2>, grid, dim3(kWT), 0, ctx->stream, e0, e1, 0, ka);
+    after_launch("wide_keys_kernel");
+  };
   for (int64_t c0 = 0; c0 < q; c0 += qc) {
     const int64_t nq = std::min(qc, q - c0);
+    const unsigned qgroups = unsigned((nq + 127) / 128);
     KeysArgs ka{};
     ka.tiles = reinterpret_cast<const u32x4*>(ds->tiles);
     ka.norms = ds->norms;
@@ -747,17 +759,30 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     ka.qnorms = qnorms;
     ka.qt0 = int(c0 / 32);
     ka.nq = int(nq);
+    ka.n = ds->n;
+    if (sampled) {
+      // Keys of the sampled tiles, then each query's threshold.
+      KeysArgs sk = ka;
+      sk.keys = skeys;
+      sk.ldk = s_ld;
+      sk.n_idx = s_tiles;
+      sk.tile_stride = s_stride;
+      const TimerSpan ts = timer_span(ctx, "bf_sample");
+      launch_keys(dim3(unsigned(s_ld / kTileRows / 4), qgroups), sk, ts.start, nullptr);
+      hipExtLaunchKernelGGL(wide_threshold_kernel, dim3(unsigned(nq)), dim3(kWT), 0, ctx->stream, nullptr, ts.stop,
+                            0, skeys, int64_t(s_ld), int(S), s_rank, t0s, cnt);
+      after_launch("wide_threshold_kernel");
+      ka.t0 = t0s;
+      ka.cnt = cnt;
+      ka.cand = cand;
+      ka.cand_cap = kCandCap;
+    }
     ka.keys = keys;
     ka.ldk = ldk;
+    ka.n_idx = ds->n_tiles;
+    ka.tile_stride = 1;
     const TimerSpan t1 = timer_span(ctx, "bf_scan");
-    const dim3 kgrid(unsigned(ds->n_tiles / 4), unsigned((nq + 127) / 128));
-    if (kb == 8)
-      hipExtLaunchKernelGGL(wide_keys_kernel<8>, kgrid, dim3(kWT), 0, ctx->stream, t1.start, t1.stop, 0, ka);
-    else if (kb == 4)
-      hipExtLaunchKernelGGL(wide_keys_kernel<4>, kgrid, dim3(kWT), 0, ctx->stream, t1.start, t1.stop, 0, ka);
-    else
-      hipExtLaunchKernelGGL(wide_keys_kernel<2>, kgrid, dim3(kWT), 0, ctx->stream, t1.start, t1.stop, 0, ka);
-    after_launch("wide_keys_kernel");
+    launch_keys(dim3(unsigned(ds->n_tiles / 4), qgroups), ka, t1.start, t1.stop);
     SelectArgs sa{};
     sa.keys = keys;
     sa.ldk = ldk;
@@ -765,8 +790,10 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     sa.d = ds->d;
     sa.q0 = int(c0);
     sa.R = R;
-    sa.s_count = sampled ? int(S) : 0;
-    sa.s_rank = s_rank;
+    sa.t0 = t0s;
+    sa.cnt = cnt;
+    sa.cand = cand;
+    sa.cand_cap = kCandCap;
     sa.k = k;
     sa.rows = ds->rows;
     sa.queries = queries;

@@ -106,20 +106,20 @@ def test_wide_integer_ties(ctx, oracle):
 
 
 def test_wide_sample_threshold_short(ctx, oracle):
-    """The select's sampled threshold falls short and the full radix select
-    takes over.  With n = 32,768 the sample is every second row (16,384
-    evenly strided keys); here those are exactly the rows near the queries
-    and the odd rows are far, so the threshold (rank ~286 of the sample for
-    R = 400) has only ~286 keys at or below it, fewer than R."""
+    """The sampled threshold falls short and the full radix select takes
+    over.  With n = 32,768 rows (1,024 tiles of 32) the sample is every second
+    tile (16,384 rows); here those are exactly the rows near the queries and
+    the rows of odd tiles are far, so the threshold (rank ~286 of the sample
+    for R = 400) has only ~286 keys at or below it, fewer than R."""
     rng = np.random.default_rng(31)
     n, d, q, k = 32768, 128, 4, 200
     c = rng.standard_normal(d).astype(np.float32)
-    base = np.empty((n, d), np.float32)
-    base[0::2] = c + 0.5 * rng.standard_normal((n // 2, d)).astype(np.float32)
-    base[1::2] = -30.0 * c + 0.5 * rng.standard_normal((n // 2, d)).astype(np.float32)
+    near = (np.arange(n) // 32) % 2 == 0
+    base = np.where(near[:, None], c, -30.0 * c).astype(np.float32) + \
+        0.5 * rng.standard_normal((n, d)).astype(np.float32)
     qs = c + 0.5 * rng.standard_normal((q, d)).astype(np.float32)
     nbr, _ = run(ctx, oracle, base, qs, k)
-    assert (nbr % 2 == 0).all()
+    assert near[nbr.astype(np.int64)].all()
 
 
 def test_wide_sample_threshold_crowded(ctx, oracle):
