@@ -309,15 +309,41 @@ __device__ __forceinline__ void select_held(Key key, uint32_t need, uint32_t* s_
   tau = prefix;
 }
 
+// Ascending bitonic sort of the 32-bit values s[0..p) (p a power of two, at
+// most 4096) by the whole workgroup.
+__device__ __forceinline__ void block_sort32(uint32_t* s, int p) {
+  for (int size = 2; size <= p; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < p / 2; i += kWT) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const uint32_t x = s[lo], y = s[hi];
+        if (asc ? y < x : x < y) {
+          s[lo] = y;
+          s[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+}
+
 // Per query of a chunk: the s_rank-th smallest order image among its S
 // sampled keys (skeys[ql * lds ...], S <= kSampleM * kWT), into t0[ql]; and
 // cnt[ql] = 0 for the collection that follows.
+//
+// For s_rank <= kWT: each thread takes the minimum of its keys; the
+// s_rank-th smallest of those kWT minima, U, is at least the s_rank-th
+// smallest key (the minima are s_rank distinct keys at or below U).  Every
+// key at or below U is then gathered and sorted, and the s_rank-th of them
+// is the answer.  About s_rank keys lie at or below U, so the sorts are of
+// a few hundred values.  A larger rank, or more than 4096 keys at or below
+// U, takes the radix select over all S keys.
 __global__ __launch_bounds__(256) void wide_threshold_kernel(const float* skeys, int64_t lds, int S, int s_rank,
                                                              uint32_t* t0, uint32_t* cnt) {
   __shared__ uint32_t s_hist[4096];
   __shared__ uint32_t s_wsum[4];
   __shared__ uint32_t s_sel[4];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* kr = skeys + int64_t(blockIdx.x) * lds;
   uint32_t sv[kSampleM];
 #pragma unroll
@@ -328,9 +354,55 @@ __global__ __launch_bounds__(256) void wide_threshold_kernel(const float* skeys,
     const uint32_t o = ord_f32(kr[j < S ? j : S - 1]);
     sv[m] = j < S ? o : 0xffffffffu;
   }
-  uint32_t tau, below, eq;
-  select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
-                        uint32_t(s_rank), s_hist, s_wsum, s_sel, tau, below, eq);
+  bool done = false;
+  uint32_t tau = 0;
+  if (s_rank <= kWT) {
+    uint32_t mn = 0xffffffffu;
+#pragma unroll
+    for (int m = 0; m < kSampleM; ++m) mn = sv[m] < mn ? sv[m] : mn;
+    s_hist[tid] = mn;
+    __syncthreads();
+    block_sort32(s_hist, kWT);
+    const uint32_t U = s_hist[s_rank - 1];
+    __syncthreads();
+    // Gather every key at or below U (positions from a block scan).
+    uint64_t bits = 0;
+#pragma unroll
+    for (int m = 0; m < kSampleM; ++m) bits |= uint64_t(sv[m] <= U) << m;
+    const uint32_t mine = uint32_t(__builtin_popcountll(bits));
+    uint32_t incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = uint32_t(__shfl_up(int(incl), o));
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
+    __syncthreads();
+    uint32_t off = 0, total = 0;
+    for (int w2 = 0; w2 < 4; ++w2) {
+      if (w2 < wave) off += s_wsum[w2];
+      total += s_wsum[w2];
+    }
+    if (total <= 4096u) {
+      uint32_t pos = off + incl - mine;
+#pragma unroll
+      for (int m = 0; m < kSampleM; ++m)
+        if ((bits >> m) & 1u) s_hist[pos++] = sv[m];
+      int p = 1;
+      while (p < int(total)) p <<= 1;
+      for (int i = int(total) + tid; i < p; i += kWT) s_hist[i] = 0xffffffffu;
+      __syncthreads();
+      block_sort32(s_hist, p);
+      tau = s_hist[s_rank - 1];
+      done = true;
+    }
+    __syncthreads();
+  }
+  if (!done) {
+    uint32_t below, eq;
+    select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
+                          uint32_t(s_rank), s_hist, s_wsum, s_sel, tau, below, eq);
+  }
   if (tid == 0) {
     t0[blockIdx.x] = tau;
     cnt[blockIdx.x] = 0;
