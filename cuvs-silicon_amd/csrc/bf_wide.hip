@@ -76,6 +76,8 @@ struct KeysArgs {
   uint32_t* cnt;
   uint64_t* cand;
   int cand_cap;
+  int write_keys;         // 0: the key matrix is not written
+  const uint32_t* gflag;  // non-null: only query blocks with gflag[blockIdx.y] set run
 };
 
 // Block (dataset tile group bx, query block by): wave w multiplies dataset
@@ -94,6 +96,7 @@ struct KeysArgs {
 template <int kKB>
 __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
   __shared__ u32x4 s_b[2][kKB * 4 * 64];  // [buffer][k-step * 4 + query tile][lane]
+  if (a.gflag && a.gflag[blockIdx.y] == 0) return;  // uniform per workgroup, before any barrier
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t idx = int64_t(blockIdx.x) * 4 + wave;                    // tile index (key columns)
   const int64_t t = (idx < a.n_idx ? idx : a.n_idx - 1) * a.tile_stride;  // dataset tile
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
     for (int g = 0; g < 4; ++g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[g][e] = qn + xn[g][e] - 2.0f * acc[j][4 * g + e];
-      *reinterpret_cast<f32x4*>(dst + 8 * g) = v[g];
+      if (a.write_keys) *reinterpret_cast<f32x4*>(dst + 8 * g) = v[g];
     }
     if (a.t0) {
       // Row of v[g][e]: row0 + 8 g + 4 half + e (padding rows excluded).
@@ -329,7 +332,8 @@ __device__ __forceinline__ void block_sort32(uint32_t* s, int p) {
 
 // Per query of a chunk: the s_rank-th smallest order image among its S
 // sampled keys (skeys[ql * lds ...], S <= kSampleM * kWT), into t0[ql]; and
-// cnt[ql] = 0 for the collection that follows.
+// cnt[ql] = 0 for the collection that follows, flag[ql] = 0 and, for the
+// first query of each 128-query block, gflag[ql / 128] = 0.
 //
 // For s_rank <= kWT: each thread takes the minimum of its keys; the
 // s_rank-th smallest of those kWT minima, U, is at least the s_rank-th
@@ -339,7 +343,8 @@ __device__ __forceinline__ void block_sort32(uint32_t* s, int p) {
 // a few hundred values.  A larger rank, or more than 4096 keys at or below
 // U, takes the radix select over all S keys.
 __global__ __launch_bounds__(256) void wide_threshold_kernel(const float* skeys, int64_t lds, int S, int s_rank,
-                                                             uint32_t* t0, uint32_t* cnt) {
+                                                             uint32_t* t0, uint32_t* cnt, uint32_t* flag,
+                                                             uint32_t* gflag) {
   __shared__ uint32_t s_hist[4096];
   __shared__ uint32_t s_wsum[4];
   __shared__ uint32_t s_sel[4];
@@ -406,6 +411,8 @@ __global__ __launch_bounds__(256) void wide_threshold_kernel(const float* skeys,
   if (tid == 0) {
     t0[blockIdx.x] = tau;
     cnt[blockIdx.x] = 0;
+    flag[blockIdx.x] = 0;
+    if (blockIdx.x % 128 == 0) gflag[blockIdx.x / 128] = 0;
   }
 }
 
@@ -422,6 +429,14 @@ struct SelectArgs {
   const uint32_t* cnt;
   const uint64_t* cand;
   int cand_cap;
+  // Deferred keys: with `lazy` the key matrix has not been written; a query
+  // that needs it sets flag[ql] and gflag[ql / 128] and returns without
+  // output, for a second pass (`only_flagged`: other queries return at once)
+  // after the matrix has been written for the flagged query blocks.
+  uint32_t* flag;
+  uint32_t* gflag;
+  int lazy;
+  int only_flagged;
   int64_t k;
   const float* rows;     // fp32 rows
   const float* queries;  // fp32 queries of the call
@@ -440,6 +455,7 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
   __shared__ float s_tneed;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t ql = blockIdx.x;          // query of the chunk
+  if (a.only_flagged && a.flag[ql] == 0) return;
   const int64_t q = a.q0 + ql;            // query of the call
   const float* kr = a.keys + ql * a.ldk;
   const float* qv = a.queries + q * a.d;
@@ -476,6 +492,13 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
             o = in ? uint32_t(s_cand[i] >> 32) : 0xffffffffu;
           },
           uint32_t(a.R), s_hist, s_wsum, s_sel, tau, below, eq);
+    } else if (a.lazy) {
+      // The list does not serve: the second pass takes this query.
+      if (tid == 0) {
+        a.flag[ql] = 1;
+        a.gflag[ql / 128] = 1;
+      }
+      return;
     }
   }
   // 1b. Otherwise radix select over all n keys.
@@ -689,14 +712,11 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 
   // 2. Certificate (see Cert): every row not re-ranked has a key of at least
   // unord(tau).
+  constexpr int kDeferred = -1;
   if (tid == 0) {
     int mode = kCertPass;
     float tneed = INFINITY;
     const uint64_t kth = k <= fill ? s_acc[k - 1] : kSentinel;
-    if (!finite) {
-      atomicAdd(&cert.counters[0], 1ull);
-      atomicAdd(&cert.counters[1], 1ull);
-    }
     if (finite && uint64_t(below) + eq < uint64_t(n)) {
       const double dk = kth == kSentinel ? INFINITY : double(unord_f32(uint32_t(kth >> 32)));
       const double qt = std::sqrt(double(qn)) * (1.0 + 0x1p-20);
@@ -711,13 +731,26 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
         mode = kCertKeys;
         tneed = V > 3.0e38 ? INFINITY
                            : float(((std::sqrt(V) + E_) * (std::sqrt(V) + E_) + A) * (1.0 + 0x1p-20));
+      }
+    }
+    // Rows with keys up to T_need are re-ranked from the list when it holds
+    // them all; otherwise from the key matrix, which a lazy pass defers.
+    if (mode == kCertKeys && a.lazy && !(use_cand && ord_f32(tneed) <= t0)) {
+      a.flag[ql] = 1;
+      a.gflag[ql / 128] = 1;
+      mode = kDeferred;
+    } else {
+      if (mode == kCertKeys) atomicAdd(&cert.counters[0], 1ull);
+      if (!finite) {
         atomicAdd(&cert.counters[0], 1ull);
+        atomicAdd(&cert.counters[1], 1ull);
       }
     }
     s_mode = mode;
     s_tneed = tneed;
   }
   __syncthreads();
+  if (s_mode == kDeferred) return;
   if (s_mode != kCertPass) {
     const uint32_t hi = ord_f32(s_tneed);
     if (use_cand && hi <= t0)
@@ -791,7 +824,9 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   const size_t off_skeys = total;
   const size_t off_t0 = off_skeys + (sampled ? align(size_t(qc) * size_t(s_ld) * sizeof(float)) : 0);
   const size_t off_cnt = off_t0 + (sampled ? align(size_t(qc) * sizeof(uint32_t)) : 0);
-  const size_t off_cand = off_cnt + (sampled ? align(size_t(qc) * sizeof(uint32_t)) : 0);
+  const size_t off_flag = off_cnt + (sampled ? align(size_t(qc) * sizeof(uint32_t)) : 0);
+  const size_t off_gflag = off_flag + (sampled ? align(size_t(qc) * sizeof(uint32_t)) : 0);
+  const size_t off_cand = off_gflag + (sampled ? align(size_t(qc / 128 + 1) * sizeof(uint32_t)) : 0);
   const size_t total_all = off_cand + (sampled ? align(size_t(qc) * kCandCap * sizeof(uint64_t)) : 0);
   ctx->ws_search.reserve(total_all);
   char* ws = ctx->ws_search.as<char>();
@@ -803,6 +838,8 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   uint32_t* t0s = sampled ? reinterpret_cast<uint32_t*>(ws + off_t0) : nullptr;
   uint32_t* cnt = sampled ? reinterpret_cast<uint32_t*>(ws + off_cnt) : nullptr;
   uint64_t* cand = sampled ? reinterpret_cast<uint64_t*>(ws + off_cand) : nullptr;
+  uint32_t* flag = sampled ? reinterpret_cast<uint32_t*>(ws + off_flag) : nullptr;
+  uint32_t* gflag = sampled ? reinterpret_cast<uint32_t*>(ws + off_gflag) : nullptr;
 
   const TimerSpan t0 = timer_span(ctx, "bf_prep");
   launch_query_tiles(ctx, ds, queries, q, q_tiles4 * 32, qtiles, qnorms, qerr, t0.start, t0.stop);
@@ -832,6 +869,7 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     ka.qt0 = int(c0 / 32);
     ka.nq = int(nq);
     ka.n = ds->n;
+    ka.write_keys = 1;
     if (sampled) {
       // Keys of the sampled tiles, then each query's threshold.
       KeysArgs sk = ka;
@@ -842,12 +880,13 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
       const TimerSpan ts = timer_span(ctx, "bf_sample");
       launch_keys(dim3(unsigned(s_ld / kTileRows / 4), qgroups), sk, ts.start, nullptr);
       hipExtLaunchKernelGGL(wide_threshold_kernel, dim3(unsigned(nq)), dim3(kWT), 0, ctx->stream, nullptr, ts.stop,
-                            0, skeys, int64_t(s_ld), int(S), s_rank, t0s, cnt);
+                            0, skeys, int64_t(s_ld), int(S), s_rank, t0s, cnt, flag, gflag);
       after_launch("wide_threshold_kernel");
       ka.t0 = t0s;
       ka.cnt = cnt;
       ka.cand = cand;
       ka.cand_cap = kCandCap;
+      ka.write_keys = 0;  // written later, for flagged query blocks only
     }
     ka.keys = keys;
     ka.ldk = ldk;
@@ -866,15 +905,35 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     sa.cnt = cnt;
     sa.cand = cand;
     sa.cand_cap = kCandCap;
+    sa.flag = flag;
+    sa.gflag = gflag;
+    sa.lazy = sampled ? 1 : 0;
     sa.k = k;
     sa.rows = ds->rows;
     sa.queries = queries;
     sa.out_nbr = nbr;
     sa.out_dist = dist;
     const TimerSpan t2 = timer_span(ctx, "bf_merge");
-    hipExtLaunchKernelGGL(wide_select_kernel, dim3(unsigned(nq)), dim3(kWT), cand_lds, ctx->stream, t2.start, t2.stop,
-                          0, sa, cert);
+    hipExtLaunchKernelGGL(wide_select_kernel, dim3(unsigned(nq)), dim3(kWT), cand_lds, ctx->stream, t2.start,
+                          sampled ? nullptr : t2.stop, 0, sa, cert);
     after_launch("wide_select_kernel");
+    if (sampled) {
+      // Second pass for the queries the list did not serve (none on most
+      // batches: its launches then return at once): the key matrix of the
+      // flagged query blocks, then the full radix select for those queries.
+      KeysArgs fk = ka;
+      fk.t0 = nullptr;
+      fk.write_keys = 1;
+      fk.gflag = gflag;
+      launch_keys(dim3(unsigned(ds->n_tiles / 4), qgroups), fk, nullptr, nullptr);
+      SelectArgs fs = sa;
+      fs.cand = nullptr;
+      fs.lazy = 0;
+      fs.only_flagged = 1;
+      hipExtLaunchKernelGGL(wide_select_kernel, dim3(unsigned(nq)), dim3(kWT), cand_lds, ctx->stream, nullptr,
+                            t2.stop, 0, fs, cert);
+      after_launch("wide_select_kernel");
+    }
   }
 }
 
