@@ -269,10 +269,12 @@ __device__ __forceinline__ void hist_find(const uint32_t* s_hist, int nb, uint32
 
 // The need-th smallest (1 <= need <= the count) order image among keys the
 // threads of the workgroup hold, M per thread (key(m) returns whether the
-// m-th is one, and its order image): three radix passes of 12, 12 and 8 bits
-// with wave-aggregated histogram counts.  tau is that key; below and eq count
-// the keys under it and equal to it.
-template <int M, typename Key>
+// m-th is one, and its order image): three radix passes of 12, 12 and 8 bits.
+// With kAgg each wave counts a step's keys bin by bin (one atomic per distinct
+// bin, for keys that crowd into few bins); without, one atomic per key (for
+// few keys per thread, where the bin-by-bin loop's latency dominates).  tau is
+// that key; below and eq count the keys under it and equal to it.
+template <int M, bool kAgg, typename Key>
 __device__ __forceinline__ void select_held(Key key, uint32_t need, uint32_t* s_hist, uint32_t* s_wsum,
                                             uint32_t* s_sel, uint32_t& tau, uint32_t& below, uint32_t& eq) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -292,13 +294,17 @@ __device__ __forceinline__ void select_held(Key key, uint32_t need, uint32_t* s_
       key(m, in, o);
       in = in && (hs >= 32 || (o >> hs) == prefix);
       const uint32_t bin = (o >> sh) & uint32_t(nb - 1);
-      uint64_t todo = __ballot(in);
-      while (todo) {
-        const int leader = __builtin_ctzll(todo);
-        const uint32_t lb = uint32_t(__builtin_amdgcn_readlane(int(bin), leader));
-        const uint64_t same = __ballot(in && bin == lb);
-        if (lane == leader) atomicAdd(&s_hist[lb], uint32_t(popc(same)));
-        todo &= ~same;
+      if (kAgg) {
+        uint64_t todo = __ballot(in);
+        while (todo) {
+          const int leader = __builtin_ctzll(todo);
+          const uint32_t lb = uint32_t(__builtin_amdgcn_readlane(int(bin), leader));
+          const uint64_t same = __ballot(in && bin == lb);
+          if (lane == leader) atomicAdd(&s_hist[lb], uint32_t(popc(same)));
+          todo &= ~same;
+        }
+      } else if (in) {
+        atomicAdd(&s_hist[bin], 1u);
       }
     }
     __syncthreads();
@@ -405,7 +411,7 @@ __global__ __launch_bounds__(256) void wide_threshold_kernel(const float* skeys,
   }
   if (!done) {
     uint32_t below, eq;
-    select_held<kSampleM>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
+    select_held<kSampleM, true>([&](int m, bool& in, uint32_t& o) { in = m * kWT + tid < S; o = sv[m]; },
                           uint32_t(s_rank), s_hist, s_wsum, s_sel, tau, below, eq);
   }
   if (tid == 0) {
@@ -463,6 +469,10 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
                    (reinterpret_cast<uintptr_t>(a.rows) & 15) == 0;
   const int64_t n = a.n, k = a.k;
 
+  // The query's list size and threshold are loaded with its norm, so that
+  // the three round trips overlap.
+  const uint32_t nc = a.cand ? a.cnt[ql] : 0u;
+  const uint32_t t0l = a.cand ? a.t0[ql] : 0u;
   // Finite inputs?  Otherwise no key means anything: every row is re-ranked.
   const float qn = cert.qnorms[q];
   const bool finite = qn <= 3.0e38f && cert.rmax <= 3.0e38f;
@@ -477,15 +487,27 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
   uint32_t t0 = 0;
   int ncand = 0;
   if (finite && a.cand) {
-    const uint32_t nc = a.cnt[ql];
-    t0 = a.t0[ql];
+    t0 = t0l;
     if (nc >= uint32_t(a.R) && nc <= uint32_t(a.cand_cap) && nc <= uint32_t(kCandCap)) {
       ncand = int(nc);
       const uint64_t* src = a.cand + ql * a.cand_cap;
-      for (int i = tid; i < ncand; i += kWT) s_cand[i] = src[i];
+      // Eight loads per thread in flight (indices clamped, stores masked).
+      for (int base = 0; base < ncand; base += 8 * kWT) {
+        uint64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = base + u * kWT + tid;
+          v[u] = src[i < ncand ? i : ncand - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = base + u * kWT + tid;
+          if (i < ncand) s_cand[i] = v[u];
+        }
+      }
       __syncthreads();
       use_cand = true;
-      select_held<kCandM>(
+      select_held<kCandM, false>(
           [&](int m, bool& in, uint32_t& o) {
             const int i = m * kWT + tid;
             in = i < ncand;
