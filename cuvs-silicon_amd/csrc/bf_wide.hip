@@ -85,14 +85,15 @@ struct KeysArgs {
 // for query tile j, query 32 (qt0 + 4 by + j) + l % 32 against rows
 // 32 t + 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
 //
-// The k-steps run in blocks of KB (8; 4 or 2 for the 64- and 32-column
-// padded dimensions).  The four waves share the query tiles:
-// each block's 32 fragments (k-step, query tile; 1 KiB each) are loaded once
-// per workgroup (wave w loads query tile w) into one of two LDS buffers,
-// and every wave reads them from there.  Each wave's own dataset fragments
-// for the next block are loaded into the other of two register sets while
-// the current block multiplies, so that a whole block of loads (8 KiB per
-// wave) is in flight behind the matrix cores.
+// The k-steps run in blocks of KB (4; 2 for the 32-column padded
+// dimension).  The four waves share the query tiles: each block's 4 KB
+// fragments (k-step, query tile; 1 KiB each) are loaded once per workgroup
+// (wave w loads query tile w) into one of two LDS buffers, and every wave
+// reads them from there.  Each wave's own dataset fragments for the next
+// block are loaded into the other of two register sets while the current
+// block multiplies.  At 128 VGPRs and 32 KB of LDS four workgroups share a
+// CU (16 waves, 4 KiB of dataset loads each in flight); blocks of 8 k-steps
+// (180 VGPRs, 64 KB, two workgroups per CU) took 5% longer.
 template <int kKB>
 __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
   __shared__ u32x4 s_b[2][kKB * 4 * 64];  // [buffer][k-step * 4 + query tile][lane]
@@ -795,10 +796,10 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
 void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
                     uint32_t* nbr, float* dist) {
   const int ks = int(ds->dp / kStepCols);
-  // k-steps per block of the keys kernel: 8 (padded dimensions of 128 and
-  // more are multiples of 128), else the whole of 2 or 4.
-  const int kb = ks % 8 == 0 ? 8 : ks;
-  if (kb != 8 && kb != 4 && kb != 2) fail(CVS_ERR_RUNTIME, "bf_wide_search: unexpected padded dimension");
+  // k-steps per block of the keys kernel: 4 (padded dimensions of 64 and
+  // more are multiples of 64), else the whole of 2.
+  const int kb = ks % 4 == 0 ? 4 : ks;
+  if (kb != 4 && kb != 2) fail(CVS_ERR_RUNTIME, "bf_wide_search: unexpected padded dimension");
   const int64_t q_tiles4 = ((q + 31) / 32 + 3) / 4 * 4;
   const int64_t ldk = ds->n_tiles * kTileRows;
   // Queries per chunk: a multiple of 128, at most 512, keys within ~2 GiB.
@@ -871,9 +872,7 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
   CVS_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(wide_select_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, int(cand_lds)));
   auto launch_keys = [&](dim3 grid, const KeysArgs& ka, hipEvent_t e0, hipEvent_t e1) {
-    if (kb == 8)
-      hipExtLaunchKernelGGL(wide_keys_kernel<8>, grid, dim3(kWT), 0, ctx->stream, e0, e1, 0, ka);
-    else if (kb == 4)
+    if (kb == 4)
       hipExtLaunchKernelGGL(wide_keys_kernel<4>, grid, dim3(kWT), 0, ctx->stream, e0, e1, 0, ka);
     else
       hipExtLaunchKernelGGL(wide_keys_kernel<2>, grid, dim3(kWT), 0, ctx->stream, e0, e1, 0, ka);

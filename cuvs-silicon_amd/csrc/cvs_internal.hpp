@@ -183,10 +183,10 @@ constexpr int kTilePad = 64;
 constexpr int kNormSlack = 256;  // floats allocated past the last tile's norms
 
 // Padded dimensions of a dataset's tiles: 32 times a power of two up to 1024
-// (the fused scan is instantiated per k-step count), a multiple of 128 beyond
-// (only the keys-matrix path reads those, eight k-steps at a time).
+// (the fused scan is instantiated per k-step count), a multiple of 64 beyond
+// (only the keys-matrix path reads those, four k-steps at a time).
 inline int64_t padded_dim(int64_t d) {
-  if (d > 1024) return (d + 127) / 128 * 128;
+  if (d > 1024) return (d + 63) / 64 * 64;
   int64_t p = 32;
   while (p < d) p *= 2;
   return p;

@@ -34,7 +34,7 @@ def run(ctx, oracle, base, qs, k):
     (20000, 1536, 50, 10),
     (12000, 3072, 40, 10),
     (6000, 4096, 20, 100),
-    (3000, 3000, 17, 77),      # d padded to 3072
+    (3000, 3000, 17, 77),      # d padded to 3008
     (4000, 1100, 9, 10),       # d padded to 1152
     (30000, 128, 60, 200),     # k above the fused scan's limit, small d
     (20000, 256, 40, 1000),
