@@ -5,38 +5,39 @@
 // returns the same answers for d up to CVS_BF_MAX_DIM and k up to
 // CVS_BF_MAX_K.
 //
-// Per chunk of up to 512 queries (keys of the chunk within ~2 GiB):
-//  keys    fp16 MFMA keys d~ = |q~|^2 + |x~|^2 - 2 q~.x~ of the centred,
-//          scaled copies (the dataset's tiles and the queries converted the
-//          same way) for every (query, row), written to a chunk x N fp32
-//          matrix.  One wave per (32-row dataset tile, 4 query tiles): each
-//          k-step is one 16-byte load per lane of each operand (the tile
-//          layout is the MFMA operand layout) and four
-//          v_mfma_f32_32x32x16_f16, the loads of the next two k-steps in
-//          flight while the current ones multiply.
-//  select  one workgroup per query finds the R-th smallest key
-//          (R = max(2 k, k + 32)).  First from a sample: the r-th smallest of
-//          up to 16,384 evenly strided keys is a threshold T0 that lies at
-//          or above the R-th smallest key of all with probability at least
-//          1 - 1e-9 (r from the Poisson rule of the fused path's sample);
-//          one pipelined pass over the query's keys collects every (key,
-//          row) at or below T0 into LDS, and a radix select among those
-//          finds the R-th key exactly.  When T0 fell short (fewer than R
-//          keys collected) or too many keys share it, a three-pass radix
-//          select (12 + 12 + 8 bits of the keys' order image) over all keys
-//          finds it instead.  Every row at or below it is re-ranked
-//          exactly in fp32 into a running top k kept in LDS (block bitonic
-//          sort of up to 2,048 keys).  The certificate of the fused path
-//          (Cert, bf_common.hpp) then bounds the exact distance of every row
-//          above the R-th key; if it does not clear the k-th exact distance,
-//          every row with a key up to the bound T_need is re-ranked too.
-//          Every key exists here, so no row outside the matrix is ever
-//          needed; a query whose fp16 copy is not finite re-ranks every
-//          row.
+// Per chunk of up to 512 queries (a key matrix of the chunk within ~2 GiB):
+//  sample     the fp16 MFMA keys d~ = |q~|^2 + |x~|^2 - 2 q~.x~ (centred,
+//             scaled copies: the dataset's tiles and the queries converted
+//             the same way) of up to 512 evenly strided dataset tiles, by the
+//             keys kernel below with a strided tile index.
+//  threshold  one workgroup per query: the r-th smallest sampled key, T0,
+//             lies at or above the query's R-th smallest key
+//             (R = max(2 k, k + 32)) with probability at least 1 - 1e-9 (r
+//             from the Poisson rule of the fused path's sample).
+//  keys       every (query, row) key, one wave per (32-row dataset tile, 4
+//             query tiles), four v_mfma_f32_32x32x16_f16 per k-step; every key
+//             at or below the query's T0 is appended with its row to the
+//             query's list.  No key matrix is written on this pass.
+//  select     one workgroup per query: when the list holds at least R keys
+//             and fits, a radix select over it finds the R-th key exactly
+//             (every key at or below T0 is listed).  Every row at or below it
+//             is re-ranked exactly in fp32 into a running top k kept in LDS
+//             (block bitonic sort of up to 2,048 keys).  The certificate of
+//             the fused path (Cert, bf_common.hpp) then bounds the exact
+//             distance of every row above the R-th key; if it does not clear
+//             the k-th exact distance, every row with a key up to the bound
+//             T_need is re-ranked too (from the list when T_need <= T0).  A
+//             query the list does not serve is flagged and returns.
+//  second     for flagged 128-query blocks only (the launches return at once
+//  pass       otherwise): the keys kernel writes the block's chunk x N fp32
+//             key matrix, and the select takes each flagged query through a
+//             three-pass radix select (12 + 12 + 8 bits of the keys' order
+//             image) over all its keys.  A query whose fp16 copy is not
+//             finite re-ranks every row.
 //
-// Bytes per chunk: N * dp * 2 (tiles) + chunk * N * 4 (keys, written, and
-// read once by the select's collecting pass; three more times when a
-// query falls back to the full radix select) + the re-ranked rows.
+// Bytes per search: N * dp * 2 (tiles) + the sample tiles + the lists + the
+// re-ranked rows; a flagged block adds its key matrix (128 * N * 4, written
+// once and read three times) and another pass over the tiles.
 #include <algorithm>
 #include <cmath>
 
