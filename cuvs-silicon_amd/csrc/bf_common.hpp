@@ -236,8 +236,10 @@ void launch_query_tiles(cvs_context* ctx, const cvs_dataset* ds, const float* qu
                         u32x4* qtiles, float* qnorms, float* qerr, hipEvent_t e0, hipEvent_t e1);
 
 // Exact k-NN outside the fused scan's limits (d > 1024 or k > 112): fp16
-// MFMA keys of a query chunk against every row, a radix select and the
-// certified exact re-rank (bf_wide.hip).  Device pointers, context stream.
+// MFMA keys of a query chunk against every row, listed below a sampled
+// per-query threshold (a radix select over the full key matrix where the list
+// does not serve), and the certified exact re-rank (bf_wide.hip).  Device
+// pointers, context stream.
 void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* queries, int64_t q, int64_t k,
                     uint32_t* nbr, float* dist);
 constexpr int64_t kFusedMaxDim = 1024;  // the fused scan holds a query tile's operands for d <= 1024
