@@ -78,12 +78,13 @@ struct KeysArgs {
   uint64_t* cand;
   int cand_cap;
   int write_keys;         // 0: the key matrix is not written
-  const uint32_t* gflag;  // non-null: only query blocks with gflag[blockIdx.y] set run
+  const uint32_t* gflag;  // non-null: only query blocks with gflag[query block] set run
+  int qgroups;            // 128-query blocks of the chunk (the grid is tile groups x qgroups)
 };
 
-// Block (dataset tile group bx, query block by): wave w multiplies dataset
-// tile 4 bx + w with the query tiles qt0 + 4 by + j, j = 0..3.  Lane l holds,
-// for query tile j, query 32 (qt0 + 4 by + j) + l % 32 against rows
+// Workgroup (dataset tile group tg, 128-query block qg): wave w multiplies
+// dataset tile 4 tg + w with the query tiles qt0 + 4 qg + j, j = 0..3.  Lane
+// l holds, for query tile j, query 32 (qt0 + 4 qg + j) + l % 32 against rows
 // 32 t + 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15.
 //
 // The k-steps run in blocks of KB (4; 2 for the 32-column padded
@@ -98,11 +99,20 @@ struct KeysArgs {
 template <int kKB>
 __global__ __launch_bounds__(256) void wide_keys_kernel(KeysArgs a) {
   __shared__ u32x4 s_b[2][kKB * 4 * 64];  // [buffer][k-step * 4 + query tile][lane]
-  if (a.gflag && a.gflag[blockIdx.y] == 0) return;  // uniform per workgroup, before any barrier
+  // One-dimensional grid of tile groups x query blocks.  Workgroup w runs on
+  // XCD w % 8, so w is renumbered XCD-major: each XCD takes a contiguous run
+  // of (tile group, query block) pairs, query block fastest, and the query
+  // blocks of one tile group follow each other on one XCD, whose L2 then
+  // serves their repeated reads of the tile group.
+  const uint32_t wg = blockIdx.x, total = gridDim.x;
+  const uint32_t L = total % 8 == 0 ? (wg % 8) * (total / 8) + wg / 8 : wg;
+  const int qg = int(L % uint32_t(a.qgroups));
+  const int64_t tg = L / uint32_t(a.qgroups);
+  if (a.gflag && a.gflag[qg] == 0) return;  // uniform per workgroup, before any barrier
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t idx = int64_t(blockIdx.x) * 4 + wave;                    // tile index (key columns)
+  const int64_t idx = tg * 4 + wave;                                      // tile index (key columns)
   const int64_t t = (idx < a.n_idx ? idx : a.n_idx - 1) * a.tile_stride;  // dataset tile
-  const int qtb = a.qt0 + int(blockIdx.y) * 4;
+  const int qtb = a.qt0 + qg * 4;
   const int64_t tstep = int64_t(a.ks) * 64;  // u32x4 per tile
   const u32x4* A = a.tiles + t * tstep + lane;
   const u32x4* Bg = a.qtiles + int64_t(qtb + wave) * tstep + lane;
@@ -890,6 +900,7 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     ka.qnorms = qnorms;
     ka.qt0 = int(c0 / 32);
     ka.nq = int(nq);
+    ka.qgroups = int(qgroups);
     ka.n = ds->n;
     ka.write_keys = 1;
     if (sampled) {
@@ -900,7 +911,7 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
       sk.n_idx = s_tiles;
       sk.tile_stride = s_stride;
       const TimerSpan ts = timer_span(ctx, "bf_sample");
-      launch_keys(dim3(unsigned(s_ld / kTileRows / 4), qgroups), sk, ts.start, nullptr);
+      launch_keys(dim3(unsigned(s_ld / kTileRows / 4) * qgroups), sk, ts.start, nullptr);
       hipExtLaunchKernelGGL(wide_threshold_kernel, dim3(unsigned(nq)), dim3(kWT), 0, ctx->stream, nullptr, ts.stop,
                             0, skeys, int64_t(s_ld), int(S), s_rank, t0s, cnt, flag, gflag);
       after_launch("wide_threshold_kernel");
@@ -915,7 +926,7 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
     ka.n_idx = ds->n_tiles;
     ka.tile_stride = 1;
     const TimerSpan t1 = timer_span(ctx, "bf_scan");
-    launch_keys(dim3(unsigned(ds->n_tiles / 4), qgroups), ka, t1.start, t1.stop);
+    launch_keys(dim3(unsigned(ds->n_tiles / 4) * qgroups), ka, t1.start, t1.stop);
     SelectArgs sa{};
     sa.keys = keys;
     sa.ldk = ldk;
@@ -947,7 +958,7 @@ void bf_wide_search(cvs_context* ctx, const cvs_dataset* ds, const float* querie
       fk.t0 = nullptr;
       fk.write_keys = 1;
       fk.gflag = gflag;
-      launch_keys(dim3(unsigned(ds->n_tiles / 4), qgroups), fk, nullptr, nullptr);
+      launch_keys(dim3(unsigned(ds->n_tiles / 4) * qgroups), fk, nullptr, nullptr);
       SelectArgs fs = sa;
       fs.cand = nullptr;
       fs.lazy = 0;
