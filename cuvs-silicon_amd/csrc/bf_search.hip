@@ -634,8 +634,17 @@ __global__ __launch_bounds__(256) void query_tiles_kernel(const float* __restric
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = (ok && c0 + j < d) ? src[c0 + j] : 0.f;
       }
+      // The means are loaded unconditionally (column clamped) and the result
+      // masked by an AND of its bits, which the compiler cannot move into a
+      // branch: a load used only under its lane condition is waited for
+      // before the next one is issued.
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = (ok && c0 + j < d) ? (v[j] - mu[c0 + j]) * scale : 0.f;
+      for (int j = 0; j < 8; ++j) {
+        const bool in = ok && c0 + j < d;
+        const float mj = mu[c0 + j < d ? c0 + j : d - 1];
+        const float r = (v[j] - mj) * scale;
+        v[j] = __uint_as_float(__float_as_uint(r) & (in ? 0xffffffffu : 0u));
+      }
       _Float16 h[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -680,8 +689,12 @@ __global__ __launch_bounds__(256) void bf_select_kernel(const float* __restrict_
   uint32_t v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
+    // Unconditional loads (index clamped, value masked after by an OR, which
+    // the compiler cannot move into a branch): a load under a lane condition
+    // is waited for before the next one is issued.
     const int e = lane + 64 * i;
-    v[i] = e < m ? ord_f32(src[e]) : 0xffffffffu;
+    const float x = src[e < m ? e : (m > 0 ? m - 1 : 0)];
+    v[i] = ord_f32(x) | (e < m ? 0u : 0xffffffffu);
   }
   if (m < kp) {
     if (lane == 0) thr0[q] = INFINITY;
