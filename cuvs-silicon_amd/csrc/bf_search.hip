@@ -953,14 +953,19 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
   // lanes' minima of their four list minima: those are R distinct list
   // minima, so at least R keys lie at or below it (one 64-key sort instead
   // of a 256-key one; the bound is a little looser).
+  // Loads unconditional (index clamped); the values past G are masked, by
+  // bitwise operations the compiler keeps out of branches, after the key
+  // batch has been requested, so that all of them are in flight together.
   uint64_t mins[4];
+  uint32_t cuts[4];
   float cut = INFINITY;
   if (wave == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int x = lane + 64 * i;
-      mins[i] = x < G ? lmin[q * G + x] : kSentinel;
-      if (x < G) cut = fminf(cut, lcut[q * G + x]);
+      const int64_t xi = q * G + (x < G ? x : G - 1);
+      mins[i] = lmin[xi];
+      cuts[i] = __float_as_uint(lcut[xi]);
     }
   }
   // First batch of keys, requested before the bound is known.
@@ -971,6 +976,12 @@ __global__ __launch_bounds__(256) void bf_merge_filter_kernel(const uint64_t* __
     key[r] = e < total ? src[e] : kSentinel;
   }
   if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool in = lane + 64 * i < G;
+      mins[i] |= in ? 0ull : kSentinel;
+      cut = fminf(cut, __uint_as_float((cuts[i] & (in ? 0xffffffffu : 0u)) | (in ? 0u : 0x7f800000u)));
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) cut = fminf(cut, xor_lanes_f(cut, o));
     uint64_t bound;
