@@ -137,3 +137,13 @@ def test_wide_sample_threshold_crowded(ctx, oracle):
     np.testing.assert_array_equal(nbr, ref_nbr)
     np.testing.assert_array_equal(dist, ref_dist)
     assert (nbr == np.arange(k)).all() and (dist == 0).all()
+
+
+def test_wide_maximum_sizes(ctx, oracle):
+    """The largest shapes the entry point accepts: d = CVS_BF_MAX_DIM
+    (16,384: 1,024 k-steps per tile) with k = CVS_BF_MAX_K (1,024; R = 2,048
+    rows re-ranked), three queries (one partial query tile)."""
+    rng = np.random.default_rng(33)
+    n, d, q, k = 2500, 16384, 3, 1024
+    centres = rng.standard_normal((16, d)).astype(np.float32)
+    run(ctx, oracle, clustered(rng, n, d, centres), clustered(rng, q, d, centres), k)
