@@ -548,9 +548,9 @@ __global__ __launch_bounds__(256) void wide_select_kernel(SelectArgs a, Cert cer
       __syncthreads();
       const int hs = sh + w;  // bits above this pass must equal the prefix
       // 16 keys per thread and step as four 16-byte loads (the row starts
-      // 128-byte aligned; indices clamped, keys past n masked).  Keys crowd into few
-      // bins (distances of one query span few exponents), so each wave
-      // counts its keys bin by bin: the lowest pending lane's bin, the
+      // 128-byte aligned; indices clamped, keys past n masked).  Keys crowd
+      // into few bins (distances of one query span few exponents), so each
+      // wave counts its keys bin by bin: the lowest pending lane's bin, the
       // ballot of the lanes holding it, one atomic for all of them.
       const float4* kr4 = reinterpret_cast<const float4*>(kr);
       const int64_t n4 = (n + 3) / 4;
