@@ -155,7 +155,8 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
   uint32_t* s_ctl = s_par + CVS_CAGRA_MAX_WIDTH;
   // d > 1024 (BIG): the query stays in LDS, as given (s_q) and, for fp16
   // traversal, centred and scaled (s_qc); dpad floats each, after the
-  // control words.
+  // control words.  fp16 traversal with d <= 1024: s_q receives the query as
+  // given (kBigDim floats, zero past d) for the final exact re-rank.
   float* s_q = reinterpret_cast<float*>(s_ctl + 8);
   float* s_qc = s_q + (BIG ? a.dq * 4 : 0);
 
@@ -302,9 +303,11 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
         }
       }
     } else {
-      // Exact: the fp32 rows against the query as given (read again; this
-      // runs once per list entry at the end of the search).
+      // Exact: the fp32 rows against the query as given (staged in LDS, zero
+      // past d as the rows are; this runs once per list entry at the end of
+      // the search).
       const float4* row = a.rows + int64_t(rid) * a.dq + 2 * tp;
+      const float4* qq = reinterpret_cast<const float4*>(s_q) + 2 * tp;
       float4 x[2 * kMaxDv8];
 #pragma unroll
       for (int j = 0; j < kMaxDv8; ++j) {
@@ -316,12 +319,8 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
 #pragma unroll
       for (int j = 0; j < kMaxDv8; ++j) {
         if (j < a.dv8) {
-          float qr[8];
-#pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const int64_t c = int64_t(tp + 16 * j) * 8 + t;
-            qr[t] = c < a.d ? qsrc[c] : 0.f;
-          }
+          const float4 ql = qq[32 * j], qh4 = qq[32 * j + 1];
+          const float qr[8] = {ql.x, ql.y, ql.z, ql.w, qh4.x, qh4.y, qh4.z, qh4.w};
           const float4 lo = x[2 * j], hi = x[2 * j + 1];
           const float d0 = qr[0] - lo.x, d1 = qr[1] - lo.y, d2 = qr[2] - lo.z, d3 = qr[3] - lo.w;
           const float d4 = qr[4] - hi.x, d5 = qr[5] - hi.y, d6 = qr[6] - hi.z, d7 = qr[7] - hi.w;
@@ -501,6 +500,16 @@ __global__ __launch_bounds__(64 * W, (F16 && W == 2 && !BIG) ? 4 : 1) void cagra
   // fp32 rows (all teams, 64 entries per round) and the list re-sorted, so
   // the output is the exact top-k of the visited rows in the list.
   if constexpr (F16) {
+    if constexpr (!BIG) {
+      // The query as given into LDS for the exact distances (the loop's
+      // first barrier publishes it): global loads issued together (column
+      // clamped, value masked by an AND of its bits), where per-element
+      // loads under the column test took one round trip per 8 columns.
+      for (int i = tid; i < kBigDim; i += kThreads) {
+        const float x = qsrc[i < a.d ? i : a.d - 1];
+        s_q[i] = __uint_as_float(__float_as_uint(x) & (i < a.d ? 0xffffffffu : 0u));
+      }
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       if (lead) s_ids[lane] = top[e] != kEmptyKey ? uint32_t(top[e]) >> 1 : 0u;
@@ -780,7 +789,8 @@ void cagra_search_device(cvs_context* ctx, const cvs_cagra_index* idx, const flo
   const bool use_bitmap = bitmap_words <= (int64_t(1) << hash_bits);
   const size_t visit_words = use_bitmap ? size_t(bitmap_words) : (size_t(1) << hash_bits);
   const size_t lds = visit_words * 4 + (64 + 64 + CVS_CAGRA_MAX_WIDTH + 8) * 4 +
-                     (big ? size_t(idx->dpad) * 4 * (idx->traversal_bits == 16 ? 2 : 1) : 0);
+                     (big ? size_t(idx->dpad) * 4 * (idx->traversal_bits == 16 ? 2 : 1)
+                          : (idx->traversal_bits == 16 ? size_t(kBigDim) * 4 : 0));
 
   SearchArgs a{};
   a.rows = reinterpret_cast<const float4*>(idx->rows);
