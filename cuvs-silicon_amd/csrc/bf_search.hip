@@ -1096,13 +1096,19 @@ __global__ __launch_bounds__(256) void bf_merge_kernel(const uint64_t* __restric
   constexpr int R = 64 * E;  // candidates re-ranked (>= kp)
 
   // 1. Bound from the list minima (G <= 256), and the smallest list threshold.
+  // Loads unconditional (index clamped; values past G masked to the sentinel
+  // and +inf by bitwise operations the compiler keeps out of branches): all
+  // eight in flight together.
   uint64_t mins[4];
   float cut = INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int x = lane + 64 * i;
-    mins[i] = x < G ? lmin[q * G + x] : kSentinel;
-    if (x < G) cut = fminf(cut, lcut[q * G + x]);
+    const int64_t xi = q * G + (x < G ? x : G - 1);
+    const uint64_t mv = lmin[xi];
+    const uint32_t cb = __float_as_uint(lcut[xi]);
+    mins[i] = mv | (x < G ? 0ull : kSentinel);
+    cut = fminf(cut, __uint_as_float((cb & (x < G ? 0xffffffffu : 0u)) | (x < G ? 0u : 0x7f800000u)));
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) cut = fminf(cut, xor_lanes_f(cut, o));
