@@ -132,8 +132,16 @@ __global__ __launch_bounds__(256) void to_tiles_kernel(const float* __restrict__
       for (int i = 0; i < 8; ++i) v[i] = (row_ok && c0 + i < d) ? src[c0 + i] : 0.f;
     }
     if (mu) {
+      // Means loaded unconditionally (column clamped) and the result masked
+      // by an AND of its bits, which the compiler keeps out of branches: a
+      // load used only under its lane condition is waited for before the
+      // next one is issued.
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (c0 + i < d) ? (v[i] - mu[c0 + i]) * scale : 0.f;
+      for (int i = 0; i < 8; ++i) {
+        const float mi = mu[c0 + i < d ? c0 + i : d - 1];
+        const float r = (v[i] - mi) * scale;
+        v[i] = __uint_as_float(__float_as_uint(r) & (c0 + i < d ? 0xffffffffu : 0u));
+      }
     }
     _Float16 h[8];
 #pragma unroll
