@@ -176,9 +176,13 @@ int cvs_dataset_rows(const cvs_dataset* ds, const float** out_rows);
  * query that fails is re-ranked exactly over every row that could be (in
  * the worst case every row), so results are exact on any finite input.
  * Requires 1 <= k <= CVS_BF_MAX_K and d <= CVS_BF_MAX_DIM; d > 1024 or
- * k > 112 run a second path (fp16 MFMA keys of a query chunk against every
- * row, a radix select, the same certificate and exact re-rank).  Host
- * pointers, blocking. */
+ * k > 112 run a second path (a per-query threshold from sampled rows, fp16
+ * MFMA keys of every row listing those at or below it, a select over the
+ * list, the same certificate and exact re-rank; a query the list does not
+ * serve is answered from the full key matrix of its 128-query block).  Its
+ * workspace, held by the context, is sized for chunks of up to 512 queries:
+ * the key matrix of a chunk (at most ~2 GiB, written only for such blocks),
+ * 64 KiB of list per query and the sampled keys.  Host pointers, blocking. */
 int cvs_bf_search(cvs_context* ctx, const cvs_dataset* ds,
                   const float* queries, int64_t q, int64_t k,
                   uint32_t* out_neighbors, float* out_distances);
