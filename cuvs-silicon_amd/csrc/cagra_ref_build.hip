@@ -321,14 +321,20 @@ __global__ __launch_bounds__(256) void group_topk_kernel(const float* __restrict
     __syncthreads();
     float acc[4][4];
     dot_tile(rows, s_aid, it.n_own, rows, s_bid, nb, dp, sA, sB, acc);
+    // Every (r, c) of the tile is written (ids past n_own or nb repeat a
+    // valid one, and those entries are never read), so the norms' loads sit
+    // under no branch and go out together: under the bounds test each pair
+    // of loads was waited for before the next.
+    float na[4], nbv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      na[i] = rnorm[s_aid[4 * tr + i]];
+      nbv[i] = rnorm[s_bid[4 * tc + i]];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * tr + i, c = 4 * tc + j;
-        if (r < it.n_own && c < nb)
-          s_dist[r][c] = pair_dist(rnorm[s_aid[r]], acc[i][j], rnorm[s_bid[c]]);
-      }
+      for (int j = 0; j < 4; ++j) s_dist[4 * tr + i][4 * tc + j] = pair_dist(na[i], acc[i][j], nbv[j]);
     __syncthreads();
     for (int r = wave; r < it.n_own; r += 4) {
       const uint64_t list = s_list[r][lane];
