@@ -505,7 +505,8 @@ def leg_wide(cvs, ctx, args) -> dict:
     out = {"workload": f"exact brute-force k-NN, N={n} D={d} Q={q} K={k} (keys-matrix path: d > 1024)",
            "steps": steps, "ms_per_search": ms, "qps": q * steps / elapsed, "kernel_avg_ms": kavg,
            "keys_kernel_roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                    "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": alg_bytes},
+                                    "frac": achieved / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": alg_bytes,
+                                    "traffic": read_traffic("bf_wide_n1M_d1536_q100_k10_traffic.txt")},
            "step_frac": alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
            "uncertified_queries": {"escalated": escalated, "rescanned_all_rows": rescanned, "of": 2 * steps * q},
            "recall_at_10": recall_at_k(nbr, gt_i, k) if gt_i is not None else None,
