@@ -147,3 +147,21 @@ def test_wide_maximum_sizes(ctx, oracle):
     n, d, q, k = 2500, 16384, 3, 1024
     centres = rng.standard_normal((16, d)).astype(np.float32)
     run(ctx, oracle, clustered(rng, n, d, centres), clustered(rng, q, d, centres), k)
+
+
+def test_wide_second_pass_in_later_chunk(ctx, oracle):
+    """Every query falls back (the construction of
+    test_wide_sample_threshold_short) over two query chunks (512 + 88): the
+    second pass's per-block flags are indexed within each chunk."""
+    rng = np.random.default_rng(34)
+    n, d, q, k = 32768, 128, 600, 200
+    c = rng.standard_normal(d).astype(np.float32)
+    near = (np.arange(n) // 32) % 2 == 0
+    base = np.where(near[:, None], c, -30.0 * c).astype(np.float32) + \
+        0.5 * rng.standard_normal((n, d)).astype(np.float32)
+    qs = c + 0.5 * rng.standard_normal((q, d)).astype(np.float32)
+    nbr, dist = ctx.dataset(base).bf_search(qs, k)
+    sample = np.r_[0:5, 250:255, 510:520, 590:600]
+    ref_nbr, ref_dist = oracle.bf_exact(base, qs[sample], k + 1, threads=8)
+    assert_parity(nbr[sample], dist[sample], ref_nbr, ref_dist, k)
+    assert near[nbr.astype(np.int64)].all()
