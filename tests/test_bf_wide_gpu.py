@@ -36,6 +36,8 @@ def run(ctx, oracle, base, qs, k):
     (6000, 4096, 20, 100),
     (3000, 3000, 17, 77),      # d padded to 3008
     (4000, 1100, 9, 10),       # d padded to 1152
+    (5000, 1531, 7, 10),       # odd d: rows not 16-byte aligned, scalar exact re-rank
+    (3000, 130, 5, 150),       # d % 4 == 2 with k above the fused scan's limit
     (30000, 128, 60, 200),     # k above the fused scan's limit, small d
     (20000, 256, 40, 1000),
     (5000, 1536, 30, 200),
