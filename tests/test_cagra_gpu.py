@@ -98,6 +98,8 @@ def test_hashed_seeds_reach_a_component_without_seed_nodes(ctx):
     (2500, 1000, 32, 128, 4, 32),
     (4000, 128, 32, 256, 2, 16),
     (5000, 256, 32, 512, 1, 16),    # the reference harness's itopk
+    (3000, 77, 32, 64, 1, 16),      # odd d: query masks past d, unaligned fp32 rows
+    (3000, 77, 32, 64, 1, 32),
 ])
 def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width, bits):
     rng = np.random.default_rng(n + d)
@@ -116,7 +118,8 @@ def test_recall_at_least_reference(ctx, oracle, n, d, g, itopk, width, bits):
     assert recall(nbr, gt, k) > 0.8
 
 
-@pytest.mark.parametrize("d,bits,width", [(1536, 32, 1), (1536, 16, 1), (3072, 32, 4), (3072, 16, 1), (8192, 16, 1)])
+@pytest.mark.parametrize("d,bits,width", [(1536, 32, 1), (1536, 16, 1), (3072, 32, 4), (3072, 16, 1), (8192, 16, 1),
+                                          (1101, 16, 1), (1101, 32, 1)])
 def test_wide_rows(ctx, oracle, d, bits, width):
     """Rows wider than 1,024 columns: the query slice lives in LDS and rows
     are gathered in chunks of 1,024 columns (the reference's search takes any
