@@ -212,7 +212,7 @@ def neighbour_recall(graph, exact, k):
     return float(np.mean([len(set(graph[i].tolist()) & set(exact[i, :k].tolist())) / k for i in range(len(graph))]))
 
 
-@pytest.mark.parametrize("n,d,g", [(3000, 64, 32), (60_000, 128, 64)])
+@pytest.mark.parametrize("n,d,g", [(3000, 64, 32), (3000, 77, 32), (60_000, 128, 64)])
 def test_reference_build_matches_oracle(ctx, cvs, oracle, n, d, g):
     """cvs_cagra_build_reference (the reference's build, src/metal_context.mm:
     289-914, on the GPU) against the oracle's restatement of it on the same
