@@ -42,6 +42,8 @@ def run(ctx, oracle, base, qs, k):
     (20000, 256, 40, 1000),
     (5000, 1536, 30, 200),
     (700, 64, 5, 1000),        # k > n: padded slots
+    (10, 2000, 3, 200),        # fewer rows than one tile, k > n
+    (3000, 1536, 1, 10),       # a single query
 ])
 def test_wide_shapes(ctx, oracle, n, d, q, k):
     rng = np.random.default_rng(n + d + k)
