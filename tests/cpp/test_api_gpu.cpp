@@ -7,7 +7,8 @@
 //  - the dispatch test of tests/test_metal_search.cpp:16-58 (default
 //    parameters, dispatch count > 0) plus the exact answers of its inputs;
 //  - graph_degree = 0 (exact route, src/cagra.cpp:197-202) and the
-//    brute_force namespace (uint32 and int64 ids);
+//    brute_force namespace (uint32 and int64 ids; D = 1536 with K = 150 beyond
+//    the fused scan's limits, bit for bit);
 //  - build -> save_index -> load_index -> search on random data against exact
 //    search;
 //  - the default graph search traverses in fp32 (fp16 traversal is opt-in);
@@ -28,6 +29,7 @@
 #include <set>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "check.hpp"
@@ -460,6 +462,41 @@ void reference_beam_mode() {
 
 }  // namespace
 
+// brute_force beyond the fused scan's limits (D > 1024 and K > 112, the
+// reference's CPU loop has neither limit, src/cagra.cpp:211-252): integer
+// rows, so every fp32 distance is exact and the answer, ties by id, is fixed.
+void wide_brute_force() {
+  constexpr std::int64_t N = 600, D = 1536, Q = 3, K = 150;
+  std::vector<float> base(N * D), queries(Q * D);
+  std::mt19937 gen(17);
+  std::uniform_int_distribution<int> val(-3, 3);
+  for (auto& v : base) v = float(val(gen));
+  for (auto& v : queries) v = float(val(gen));
+  raft::resources res;
+  auto bidx = bf::build(res, raft::make_device_matrix_view<const float, std::int64_t>(base.data(), N, D));
+  std::vector<std::uint32_t> nbr(Q * K);
+  std::vector<float> dist(Q * K);
+  bf::search(res, bidx, raft::make_device_matrix_view<const float, std::int64_t>(queries.data(), Q, D),
+             raft::make_device_matrix_view<std::uint32_t, std::int64_t>(nbr.data(), Q, K),
+             raft::make_device_matrix_view<float, std::int64_t>(dist.data(), Q, K));
+  for (std::int64_t q = 0; q < Q; ++q) {
+    std::vector<std::pair<std::int64_t, std::uint32_t>> all(N);
+    for (std::int64_t i = 0; i < N; ++i) {
+      std::int64_t acc = 0;
+      for (std::int64_t j = 0; j < D; ++j) {
+        const std::int64_t t = std::int64_t(queries[q * D + j]) - std::int64_t(base[i * D + j]);
+        acc += t * t;
+      }
+      all[i] = {acc, std::uint32_t(i)};
+    }
+    std::sort(all.begin(), all.end());
+    for (std::int64_t r = 0; r < K; ++r) {
+      CHECK(nbr[q * K + r] == all[r].second);
+      CHECK(dist[q * K + r] == float(all[r].first));
+    }
+  }
+}
+
 int main(int argc, char** argv) {
   const std::string scratch = argc > 1 ? argv[1] : "/tmp";
   faiss_smoke();
@@ -469,5 +506,6 @@ int main(int argc, char** argv) {
   default_search_is_fp32();
   metal_context_matches_c_abi();
   reference_beam_mode();
+  wide_brute_force();
   return apitest::finish("test_api_gpu");
 }
